@@ -1,0 +1,309 @@
+"""CPU oracle for the Mamba-2 SSD hot path (test infrastructure, never shipped).
+
+This module is the repository's own restatement of the reference oracle
+``mamba_torch/ssd_reference.py`` of So-cean/mamba-ascendc.  It is plain
+PyTorch on the CPU and exists only so that ``tests/``, ``__graft_entry__.smoke``
+and the ``cpu_baseline`` leg of ``bench.py`` can check (and time) the HIP path.
+Product code must never import it.
+
+Functions and the reference lines whose behaviour they follow:
+
+* ``segsum``                -- mamba_torch/ssd_reference.py:80-110 (stable
+                               segment sum, -inf above the diagonal)
+* ``ssd_chunked_core``      -- mamba_torch/ssd_reference.py:113-189 (chunked SSD
+                               on per-head inputs: intra-chunk quadratic form,
+                               chunk states, inter-chunk recurrence, C.state)
+* ``ssd_chunk_scan_ref``    -- mamba_torch/ssd_reference.py:192-326 (public
+                               signature: dt bias, softplus, clamp applied even
+                               without softplus, L padding, per-group loop, D,
+                               z gate, cast back to input dtype, fp32 final)
+* ``ssd_sequential_ref``    -- mamba_torch/ssd_reference.py:10-77 (token-by-token
+                               recurrence; never forces fp32)
+* ``discretize``            -- mamba_torch/ssd_reference.py:237-248 and
+                               mamba_ascendc/csrc/ops/mamba2_ssd_dt_bwd/design.md
+                               (u = dt + bias, q = clamp(softplus(u)))
+
+How each function is pinned (tests/test_oracle.py):
+
+* ``segsum``: hand-computed known answers; exp(segsum) equals the product of
+  decays computed by a direct double loop.
+* ``ssd_chunked_core`` / ``ssd_chunk_scan_ref``: equality with the
+  token-by-token recurrence (``ssd_sequential_ref``) and with an independent
+  float64 C implementation (``oracle/ssd_seq.c``); partition invariance over
+  chunk sizes; closed forms (B == 0 gives y = D*x gated; A == 0 gives a prefix
+  sum of outer products; L == 1 gives y = q*(B.C)*x).
+* backward: torch autograd of the restatement is checked against the float64
+  C adjoint recurrence (``ssd_seq_bwd``) and central finite differences.
+"""
+
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+import torch.nn.functional as F
+
+__all__ = [
+    "segsum",
+    "discretize",
+    "ssd_chunked_core",
+    "ssd_chunk_scan_ref",
+    "ssd_sequential_ref",
+    "make_inputs",
+]
+
+
+def segsum(v: torch.Tensor) -> torch.Tensor:
+    """Segment sums of the last axis: out[..., i, j] = sum_{k=j+1..i} v[..., k].
+
+    The diagonal is 0 and entries above it are -inf, so ``exp(segsum(v))`` is the
+    lower-triangular decay matrix.  Sums are formed by a cumulative sum over a
+    masked copy rather than by differencing two prefix sums, which keeps the
+    small-difference entries free of cancellation
+    (mamba_torch/ssd_reference.py:80-110).
+    """
+    n = v.shape[-1]
+    strictly_lower = torch.ones(n, n, dtype=torch.bool, device=v.device).tril(-1)
+    # rows index i (end of the segment), columns index j (start, exclusive)
+    grid = v.unsqueeze(-1).expand(*v.shape, n).clone()
+    grid = grid.masked_fill(~strictly_lower, 0.0)
+    out = grid.cumsum(dim=-2)
+    lower = torch.ones(n, n, dtype=torch.bool, device=v.device).tril(0)
+    return out.masked_fill(~lower, float("-inf"))
+
+
+def discretize(dt, dt_bias, dt_softplus, dt_limit):
+    """q = clamp(softplus(dt + bias)) (clamp applies with or without softplus).
+
+    Follows mamba_torch/ssd_reference.py:237-241.
+    """
+    q = dt
+    if dt_bias is not None:
+        q = q + dt_bias.reshape(1, 1, -1).to(q.dtype)
+    if dt_softplus:
+        q = F.softplus(q)
+    return q.clamp(min=dt_limit[0], max=dt_limit[1])
+
+
+def ssd_chunked_core(xdt, dA, Bh, Ch, chunk_size, initial_states=None):
+    """Chunked SSD on per-head, already discretised inputs.
+
+    Args:
+        xdt: [b, l, h, p]   x * q
+        dA:  [b, l, h]      A * q
+        Bh, Ch: [b, l, h, n] (already broadcast from groups to heads)
+        initial_states: [b, h, p, n] or None
+    Returns:
+        y [b, l, h, p] and final state [b, h, p, n].
+
+    Restates mamba_torch/ssd_reference.py:113-189.  ``l`` must be a multiple of
+    ``chunk_size``.
+    """
+    b, l, h, p = xdt.shape
+    n = Bh.shape[-1]
+    T = chunk_size
+    assert l % T == 0, "sequence length must be a multiple of chunk_size"
+    k = l // T
+    xc = xdt.reshape(b, k, T, h, p)
+    Bc = Bh.reshape(b, k, T, h, n)
+    Cc = Ch.reshape(b, k, T, h, n)
+    a = dA.reshape(b, k, T, h).permute(0, 3, 1, 2)  # [b, h, k, T]
+    cs = a.cumsum(dim=-1)
+
+    # (1) intra-chunk: y_diag[t] = sum_{s<=t} (C_t . B_s) exp(cs_t - cs_s) xdt_s
+    decay = torch.exp(segsum(a))  # [b, h, k, T, T]
+    cb = torch.einsum("bkthn,bkshn->bkhts", Cc, Bc)  # [b, k, h, T, T]
+    w = cb * decay.permute(0, 2, 1, 3, 4)
+    y_diag = torch.einsum("bkhts,bkshp->bkthp", w, xc)
+
+    # (2) per-chunk states: U_k = sum_t exp(cs_last - cs_t) xdt_t (x) B_t
+    to_end = torch.exp(cs[..., -1:] - cs)  # [b, h, k, T]
+    U = torch.einsum("bkthn,bhkt,bkthp->bkhpn", Bc, to_end, xc)
+
+    # (3) inter-chunk recurrence over chunk boundaries:
+    #     S_start[k] = sum_{j<k} exp(sum_{j<m<k} cs_last_m) U_j (+ initial decayed)
+    if initial_states is None:
+        initial_states = torch.zeros(b, h, p, n, dtype=U.dtype, device=U.device)
+    seq = torch.cat([initial_states.unsqueeze(1), U], dim=1)  # [b, k+1, h, p, n]
+    last = F.pad(cs[..., -1], (1, 0))  # [b, h, k+1]
+    hop = torch.exp(segsum(last))  # [b, h, k+1, k+1]
+    states = torch.einsum("bhij,bjhpn->bihpn", hop, seq)
+    S_start = states[:, :-1]
+    final = states[:, -1]
+
+    # (4) contribution of the state entering each chunk: exp(cs_t) C_t . S_start
+    y_off = torch.einsum("bkthn,bkhpn,bhkt->bkthp", Cc, S_start, torch.exp(cs))
+    y = (y_diag + y_off).reshape(b, l, h, p)
+    return y, final
+
+
+def ssd_chunk_scan_ref(
+    x,
+    dt,
+    A,
+    B,
+    C,
+    chunk_size,
+    D=None,
+    z=None,
+    dt_bias=None,
+    dt_softplus=False,
+    dt_limit=(0.0, float("inf")),
+    initial_states=None,
+    return_final_state=False,
+    compute_dtype=torch.float32,
+):
+    """Mamba-2 SSD forward, public reference semantics.
+
+    Shapes: x [b,l,h,p], dt [b,l,h], A [h], B/C [b,l,g,n], D [h] or [h,p],
+    z [b,l,h,p], dt_bias [h], initial_states [b,h,p,n].
+
+    Behaviour follows mamba_torch/ssd_reference.py:192-326: inputs are upcast
+    to ``compute_dtype`` (fp32 by default; fp64 for finite differences), L is
+    zero-padded to a chunk multiple (dA = 0, x = 0 in the pad so the final state
+    is the state after token L), heads are processed one group at a time with
+    B/C shared inside the group, D and the z gate are applied after trimming,
+    the output is cast back to x's dtype and the final state stays in
+    ``compute_dtype``.
+    """
+    b, l, h, p = x.shape
+    g, n = B.shape[2], B.shape[3]
+    if h % g != 0:
+        raise ValueError(f"nheads={h} not divisible by ngroups={g}")
+    r = h // g
+    out_dtype = x.dtype
+    cd = compute_dtype
+    xf, dtf, Bf, Cf = x.to(cd), dt.to(cd), B.to(cd), C.to(cd)
+    q = discretize(dtf, None if dt_bias is None else dt_bias.to(cd), dt_softplus, dt_limit)
+    dA = q * A.to(cd).reshape(1, 1, h)
+    xdt = xf * q.unsqueeze(-1)
+
+    pad = (-l) % chunk_size
+    if pad:
+        xdt = F.pad(xdt, (0, 0, 0, 0, 0, pad))
+        dA = F.pad(dA, (0, 0, 0, pad))
+        Bf = F.pad(Bf, (0, 0, 0, 0, 0, pad))
+        Cf = F.pad(Cf, (0, 0, 0, 0, 0, pad))
+    init = None if initial_states is None else initial_states.to(cd)
+    if init is not None and tuple(init.shape) != (b, h, p, n):
+        raise ValueError(f"initial_states shape {tuple(init.shape)} != {(b, h, p, n)}")
+
+    ys, finals = [], []
+    for gi in range(g):
+        hs = slice(gi * r, (gi + 1) * r)
+        Bg = Bf[:, :, gi : gi + 1, :].expand(-1, -1, r, -1)
+        Cg = Cf[:, :, gi : gi + 1, :].expand(-1, -1, r, -1)
+        y_g, f_g = ssd_chunked_core(
+            xdt[:, :, hs], dA[:, :, hs], Bg, Cg, chunk_size,
+            None if init is None else init[:, hs],
+        )
+        ys.append(y_g)
+        finals.append(f_g)
+    y = torch.cat(ys, dim=2)[:, :l]
+    final = torch.cat(finals, dim=1)
+
+    if D is not None:
+        Df = D.to(cd)
+        y = y + xf * (Df.reshape(1, 1, h, 1) if Df.dim() == 1 else Df.reshape(1, 1, h, p))
+    if z is not None:
+        y = y * F.silu(z.to(cd))
+    y = y.to(out_dtype)
+    if return_final_state:
+        return y, final
+    return y
+
+
+def ssd_sequential_ref(
+    x,
+    dt,
+    A,
+    B,
+    C,
+    D=None,
+    z=None,
+    dt_bias=None,
+    dt_softplus=False,
+    dt_limit=(0.0, float("inf")),
+    initial_states=None,
+    return_final_state=False,
+):
+    """Token-by-token recurrence in the inputs' own dtype.
+
+    S_t = exp(A q_t) S_{t-1} + (x_t q_t) (x) B_t ;  y_t = S_t . C_t + D x_t ;
+    out_t = y_t * silu(z_t).  Follows mamba_torch/ssd_reference.py:10-77.
+    """
+    b, l, h, p = x.shape
+    g, n = B.shape[2], B.shape[3]
+    if h % g:
+        raise ValueError("nheads must be divisible by ngroups")
+    r = h // g
+    q = discretize(dt, dt_bias, dt_softplus, dt_limit)
+    Bh = B.repeat_interleave(r, dim=2)
+    Ch = C.repeat_interleave(r, dim=2)
+    S = (
+        torch.zeros(b, h, p, n, dtype=x.dtype, device=x.device)
+        if initial_states is None
+        else initial_states
+    )
+    outs = []
+    for t in range(l):
+        qt = q[:, t]  # [b, h]
+        a = torch.exp(qt * A.reshape(1, h))
+        S = a[..., None, None] * S + (x[:, t] * qt[..., None])[..., None] * Bh[:, t, :, None, :]
+        yt = (S * Ch[:, t, :, None, :]).sum(-1)
+        if D is not None:
+            yt = yt + x[:, t] * (D.reshape(1, h, 1) if D.dim() == 1 else D.reshape(1, h, p))
+        if z is not None:
+            yt = yt * F.silu(z[:, t])
+        outs.append(yt)
+    out = torch.stack(outs, dim=1)
+    if return_final_state:
+        return out, S
+    return out
+
+
+def make_inputs(shape, seed, device="cpu", dtype=torch.float32, features=()):
+    """Seeded inputs in the benchmark's generation order.
+
+    ``shape`` is [B, L, H, P, N, chunk, G].  Order and distributions: x = randn,
+    dt = rand (U[0,1)), A = -rand, B = randn, C = randn, all from one CPU
+    generator so CPU and GPU see bit-identical tensors.  Optional features
+    (``"D"``, ``"D2"``, ``"z"``, ``"bias"``, ``"init"``) are drawn afterwards in
+    that order so the core tensors do not change when features are added.
+    """
+    bsz, seqlen, nheads, headdim, dstate, _chunk, ngroups = shape
+    gen = torch.Generator("cpu").manual_seed(seed)
+    out = {
+        "x": torch.randn(bsz, seqlen, nheads, headdim, generator=gen),
+        "dt": torch.rand(bsz, seqlen, nheads, generator=gen),
+        "A": -torch.rand(nheads, generator=gen),
+        "B": torch.randn(bsz, seqlen, ngroups, dstate, generator=gen),
+        "C": torch.randn(bsz, seqlen, ngroups, dstate, generator=gen),
+    }
+    if "D" in features:
+        out["D"] = torch.randn(nheads, generator=gen)
+    if "D2" in features:
+        out["D"] = torch.randn(nheads, headdim, generator=gen)
+    if "z" in features:
+        out["z"] = torch.randn(bsz, seqlen, nheads, headdim, generator=gen)
+    if "bias" in features:
+        out["dt_bias"] = 0.5 * torch.randn(nheads, generator=gen)
+    if "init" in features:
+        out["initial_states"] = torch.randn(bsz, nheads, headdim, dstate, generator=gen)
+    return {k: v.to(device=device, dtype=dtype) for k, v in out.items()}
+
+
+def bench_seed(config_index: int) -> int:
+    """Seed scheme of the benchmark inputs: 20260806 + config index."""
+    return 20260806 + int(config_index)
+
+
+def parity_metrics(actual: torch.Tensor, expected: torch.Tensor) -> Tuple[float, float]:
+    """(max-abs error, relative L2 error) computed in float64."""
+    a = actual.detach().double().cpu()
+    e = expected.detach().double().cpu()
+    diff = a - e
+    maxabs = diff.abs().max().item() if diff.numel() else 0.0
+    denom = e.norm().item()
+    rel = diff.norm().item() / denom if denom > 0 else diff.norm().item()
+    return maxabs, rel

@@ -1,0 +1,287 @@
+"""Pins for the CPU oracle (oracle/ssd_reference.py and oracle/ssd_seq.c).
+
+The first group mirrors the reference's CPU oracle tests
+(tests/mamba2/test_reference.py:13-319); the rest pin the restatement against
+an independent float64 C recurrence, closed forms, partition invariance and
+finite differences, so that a dropped term, a wrong sign or a shifted index in
+either oracle fails at least one test.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle.ssd_reference import (
+    discretize,
+    make_inputs,
+    segsum,
+    ssd_chunk_scan_ref,
+    ssd_chunked_core,
+    ssd_sequential_ref,
+)
+from oracle.ssd_seq import seq_bwd, seq_fwd
+
+F64 = torch.float64
+
+
+def _inputs(b, l, h, p, n, g, seed=0, dtype=F64, features=()):
+    inp = make_inputs([b, l, h, p, n, 8, g], seed, dtype=dtype, features=features)
+    inp["dt"] = 0.1 + 0.9 * inp["dt"]
+    return inp
+
+
+# --------------------------------------------------------------------------- segsum
+
+def test_segsum_known_answer():
+    s = segsum(torch.tensor([1.0, 2.0, 3.0], dtype=F64))
+    inf = float("-inf")
+    expected = torch.tensor([[0.0, inf, inf], [2.0, 0.0, inf], [5.0, 3.0, 0.0]], dtype=F64)
+    assert torch.equal(s, expected)
+    L = torch.exp(s)
+    assert L[0, 1] == 0 and L[0, 2] == 0 and L[1, 2] == 0
+    assert math.isclose(L[2, 0].item(), math.exp(5.0))
+
+
+def test_segsum_matches_double_loop():
+    v = torch.randn(2, 3, 9, dtype=F64)
+    s = segsum(v)
+    for i in range(9):
+        for j in range(9):
+            if i < j:
+                assert torch.isinf(s[..., i, j]).all() and (s[..., i, j] < 0).all()
+            else:
+                ref = v[..., j + 1 : i + 1].sum(-1)
+                assert torch.allclose(s[..., i, j], ref, atol=1e-12)
+
+
+# --------------------------------------------------------------------------- forward pins
+
+def test_core_vs_sequential_fp32():
+    """_ssd_core-style chunked math equals the token recurrence (fp32, 1e-3)."""
+    b, l, h, p, n, T = 1, 32, 2, 4, 8, 8
+    A = torch.full((h,), math.log(0.5))
+    q = 0.1 + 0.1 * torch.rand(b, l, h)
+    x = torch.randn(b, l, h, p)
+    Bh = torch.randn(b, l, h, n)
+    Ch = torch.randn(b, l, h, n)
+    y, final = ssd_chunked_core(x * q[..., None], q * A, Bh, Ch, T)
+    S = torch.zeros(b, h, p, n)
+    for t in range(l):
+        S = torch.exp(q[:, t] * A)[..., None, None] * S + (x[:, t] * q[:, t, :, None])[..., None] * Bh[:, t, :, None, :]
+        yt = (S * Ch[:, t, :, None, :]).sum(-1)
+        assert (y[:, t] - yt).abs().max() < 1e-3
+    assert (final - S).abs().max() < 1e-3
+
+
+@pytest.mark.parametrize(
+    "features,g,softplus,limit",
+    [
+        ((), 1, True, (0.0, float("inf"))),
+        ((), 2, False, (0.0, float("inf"))),
+        (("D", "z", "bias"), 2, True, (0.0, float("inf"))),
+        (("D2", "init"), 1, True, (0.0, float("inf"))),
+        (("D2", "z", "bias", "init"), 2, True, (0.4, 0.9)),
+        (("bias",), 4, False, (-0.2, 0.3)),
+    ],
+)
+def test_chunked_vs_c_fp64(features, g, softplus, limit):
+    """Torch restatement (fp64) == independent C float64 recurrence."""
+    inp = _inputs(2, 37, 4, 8, 6, g, seed=3, features=features)
+    kw = dict(
+        D=inp.get("D"), z=inp.get("z"), dt_bias=inp.get("dt_bias"),
+        dt_softplus=softplus, dt_limit=limit, initial_states=inp.get("initial_states"),
+    )
+    y, fin = ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], 8,
+                                return_final_state=True, compute_dtype=F64, **kw)
+    yc, fc = seq_fwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], **kw)
+    assert torch.allclose(y, yc, atol=1e-10, rtol=1e-10)
+    assert torch.allclose(fin, fc, atol=1e-10, rtol=1e-10)
+    ys, fs = ssd_sequential_ref(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
+                                return_final_state=True, **kw)
+    assert torch.allclose(ys, yc, atol=1e-10, rtol=1e-10)
+    assert torch.allclose(fs, fc, atol=1e-10, rtol=1e-10)
+
+
+def test_partition_invariance():
+    inp = _inputs(1, 48, 2, 4, 8, 1, seed=5, features=("init",))
+    outs = [
+        ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], T,
+                           dt_softplus=True, initial_states=inp["initial_states"],
+                           return_final_state=True, compute_dtype=F64)
+        for T in (1, 3, 8, 16, 48, 64)
+    ]
+    for y, f in outs[1:]:
+        assert torch.allclose(y, outs[0][0], atol=1e-10)
+        assert torch.allclose(f, outs[0][1], atol=1e-10)
+
+
+def test_closed_form_B_zero():
+    """B == 0 and no initial state: the SSD term vanishes, y = D x silu(z)."""
+    inp = _inputs(2, 20, 4, 8, 6, 2, seed=7, features=("D2", "z"))
+    y = ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"], torch.zeros_like(inp["B"]), inp["C"], 8,
+                           D=inp["D"], z=inp["z"], dt_softplus=True, compute_dtype=F64)
+    ref = inp["x"] * inp["D"][None, None] * F.silu(inp["z"])
+    assert torch.allclose(y, ref, atol=1e-12)
+
+
+def test_closed_form_A_zero():
+    """A == 0: y_t = sum_{s<=t} (C_t . B_s) q_s x_s (pure causal prefix sum)."""
+    inp = _inputs(1, 24, 2, 4, 5, 1, seed=9)
+    A = torch.zeros(2, dtype=F64)
+    y, fin = ssd_chunk_scan_ref(inp["x"], inp["dt"], A, inp["B"], inp["C"], 8,
+                                dt_softplus=True, return_final_state=True, compute_dtype=F64)
+    q = F.softplus(inp["dt"])
+    xdt = inp["x"] * q[..., None]
+    CB = torch.einsum("bln,bsn->bls", inp["C"][:, :, 0], inp["B"][:, :, 0])
+    mask = torch.ones(24, 24, dtype=torch.bool).tril()
+    ref = torch.einsum("bls,bshp->blhp", CB * mask, xdt)
+    assert torch.allclose(y, ref, atol=1e-10)
+    ref_fin = torch.einsum("bshp,bsn->bhpn", xdt, inp["B"][:, :, 0])
+    assert torch.allclose(fin, ref_fin, atol=1e-10)
+
+
+def test_closed_form_single_token():
+    """L == 1 with initial state: y = exp(Aq) init.C + q x (B.C)."""
+    inp = _inputs(2, 1, 2, 4, 5, 1, seed=11, features=("init",))
+    y, fin = ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], 4,
+                                dt_softplus=True, initial_states=inp["initial_states"],
+                                return_final_state=True, compute_dtype=F64)
+    q = F.softplus(inp["dt"])[:, 0]  # [b, h]
+    decay = torch.exp(q * inp["A"])
+    bc = (inp["B"][:, 0, 0] * inp["C"][:, 0, 0]).sum(-1)  # [b]
+    init_c = torch.einsum("bhpn,bn->bhp", inp["initial_states"], inp["C"][:, 0, 0])
+    ref = decay[..., None] * init_c + q[..., None] * inp["x"][:, 0] * bc[:, None, None]
+    assert torch.allclose(y[:, 0], ref, atol=1e-12)
+    ref_fin = decay[..., None, None] * inp["initial_states"] + (q[..., None] * inp["x"][:, 0])[..., None] * inp["B"][:, 0, 0][:, None, None, :]
+    assert torch.allclose(fin, ref_fin, atol=1e-12)
+
+
+def test_clamp_applies_without_softplus():
+    dt = torch.tensor([[[-1.0, 0.5, 3.0]]], dtype=F64)
+    q = discretize(dt, None, False, (0.0, 1.0))
+    assert q.tolist() == [[[0.0, 0.5, 1.0]]]
+    q2 = discretize(dt, torch.tensor([0.0, 0.0, -2.5], dtype=F64), True, (0.0, float("inf")))
+    assert torch.allclose(q2, F.softplus(torch.tensor([[[-1.0, 0.5, 0.5]]], dtype=F64)))
+
+
+def test_padding_tail_and_final_state():
+    """L not a multiple of the chunk: output trimmed, final state = state after L."""
+    inp = _inputs(2, 30, 2, 4, 8, 1, seed=13)
+    y, fin = ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], 7,
+                                dt_softplus=True, return_final_state=True, compute_dtype=F64)
+    yc, fc = seq_fwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], dt_softplus=True)
+    assert y.shape == (2, 30, 2, 4)
+    assert torch.allclose(y, yc, atol=1e-10) and torch.allclose(fin, fc, atol=1e-10)
+
+
+def test_dtype_preservation_and_fp32_final():
+    inp = _inputs(1, 16, 2, 4, 8, 1, seed=1, dtype=torch.bfloat16)
+    out, fin = ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"].float(), inp["B"], inp["C"], 8,
+                                  dt_softplus=True, return_final_state=True)
+    assert out.dtype == torch.bfloat16 and fin.dtype == torch.float32
+    assert fin.shape == (1, 2, 4, 8)
+
+
+def test_shape_errors():
+    inp = _inputs(1, 8, 3, 4, 4, 2, seed=1)
+    with pytest.raises(ValueError):
+        ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], 4)
+
+
+# --------------------------------------------------------------------------- backward pins
+
+def _loss_grads_torch(inp, features, softplus, limit, T=8):
+    leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items()}
+    y, fin = ssd_chunk_scan_ref(
+        leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], T,
+        D=leaves.get("D"), z=leaves.get("z"), dt_bias=leaves.get("dt_bias"),
+        dt_softplus=softplus, dt_limit=limit, initial_states=leaves.get("initial_states"),
+        return_final_state=True, compute_dtype=F64,
+    )
+    gy = torch.linspace(-1, 1, y.numel(), dtype=F64).reshape(y.shape)
+    gf = torch.linspace(0.5, -0.5, fin.numel(), dtype=F64).reshape(fin.shape)
+    (y * gy).sum().backward(inputs=list(leaves.values()), retain_graph=True)
+    (fin * gf).sum().backward(inputs=list(leaves.values()))
+    return {k: v.grad for k, v in leaves.items()}, gy, gf
+
+
+@pytest.mark.parametrize(
+    "features,g,softplus,limit",
+    [
+        ((), 2, True, (0.0, float("inf"))),
+        (("D", "z", "bias", "init"), 2, True, (0.0, float("inf"))),
+        (("D2", "bias"), 1, True, (0.5, 0.9)),
+        (("z",), 4, False, (-0.2, 0.3)),
+    ],
+)
+def test_backward_autograd_vs_c_adjoint(features, g, softplus, limit):
+    inp = _inputs(2, 21, 4, 4, 5, g, seed=17, features=features)
+    tg, gy, gf = _loss_grads_torch(inp, features, softplus, limit)
+    cg = seq_bwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], gy, gf,
+                 D=inp.get("D"), z=inp.get("z"), dt_bias=inp.get("dt_bias"),
+                 dt_softplus=softplus, dt_limit=limit,
+                 initial_states=inp.get("initial_states"))
+    names = {"x": "dx", "dt": "ddt", "A": "dA", "B": "dB", "C": "dC", "D": "dD",
+             "z": "dz", "dt_bias": "ddt_bias", "initial_states": "dinitial"}
+    for k, g_t in tg.items():
+        assert torch.allclose(g_t, cg[names[k]], atol=1e-9, rtol=1e-9), k
+
+
+def test_c_adjoint_finite_differences():
+    """Directional derivative of the C forward equals <grad, direction> (fp64)."""
+    feats = ("D2", "z", "bias", "init")
+    inp = _inputs(1, 9, 2, 3, 4, 1, seed=19, features=feats)
+    kw = dict(dt_softplus=True, dt_limit=(0.0, float("inf")))
+    gy = torch.randn(1, 9, 2, 3, dtype=F64)
+    gf = torch.randn(1, 2, 3, 4, dtype=F64)
+    cg = seq_bwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], gy, gf, D=inp["D"], z=inp["z"],
+                 dt_bias=inp["dt_bias"], initial_states=inp["initial_states"], **kw)
+    names = {"x": "dx", "dt": "ddt", "A": "dA", "B": "dB", "C": "dC", "D": "dD",
+             "z": "dz", "dt_bias": "ddt_bias", "initial_states": "dinitial"}
+    gen = torch.Generator().manual_seed(23)
+    dirs = {k: torch.randn(v.shape, generator=gen, dtype=F64) for k, v in inp.items()}
+
+    def f(eps):
+        pert = {k: v + eps * dirs[k] for k, v in inp.items()}
+        y, fin = seq_fwd(pert["x"], pert["dt"], pert["A"], pert["B"], pert["C"], D=pert["D"],
+                         z=pert["z"], dt_bias=pert["dt_bias"],
+                         initial_states=pert["initial_states"], **kw)
+        return (y * gy).sum() + (fin * gf).sum()
+
+    eps = 1e-6
+    fd = (f(eps) - f(-eps)) / (2 * eps)
+    an = sum((cg[names[k]] * dirs[k]).sum() for k in inp)
+    assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (fd.item(), an.item())
+
+
+def test_planted_index_shift_is_caught():
+    """A plausible oracle mistake (decaying the entering state by exp(cs_{t-1})
+    instead of exp(cs_t)) must fail the sequential comparison."""
+    inp = _inputs(1, 16, 2, 4, 4, 1, seed=29, features=("init",))
+    q = F.softplus(inp["dt"])
+    xdt = inp["x"] * q[..., None]
+    dA = q * inp["A"]
+    Bh = inp["B"].expand(-1, -1, 2, -1)
+    Ch = inp["C"].expand(-1, -1, 2, -1)
+    y_good, _ = ssd_chunked_core(xdt, dA, Bh, Ch, 8, inp["initial_states"])
+    # planted: shift dA by one position inside each chunk
+    dA_bad = dA.clone()
+    dA_bad[:, 1:] = dA[:, :-1]
+    y_bad, _ = ssd_chunked_core(xdt, dA_bad, Bh, Ch, 8, inp["initial_states"])
+    yc, _ = seq_fwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], dt_softplus=True,
+                    initial_states=inp["initial_states"])
+    assert torch.allclose(y_good, yc, atol=1e-10)
+    assert not torch.allclose(y_bad, yc, atol=1e-3)
+
+
+def test_autograd_finite_reference_style():
+    """Reference-style smoke (tests/mamba2/test_reference.py:299-319)."""
+    inp = _inputs(1, 16, 2, 4, 8, 1, seed=31, dtype=torch.float32)
+    leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items()}
+    out = ssd_chunk_scan_ref(leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], 8,
+                             dt_softplus=True)
+    out.sum().backward()
+    for k, v in leaves.items():
+        assert v.grad is not None and torch.isfinite(v.grad).all(), k
