@@ -1,0 +1,129 @@
+/*
+ * mamba2_ssd.h -- C ABI of the MI355X (gfx950) Mamba-2 SSD hot path.
+ *
+ * Every entry point takes raw device pointers to contiguous fp32 tensors in the
+ * public layouts of the reference API, never allocates, and enqueues its work
+ * on the given HIP stream (passed as void*, i.e. a hipStream_t; NULL = the null
+ * stream).  Calls are reentrant; the only process-wide state is a thread-local
+ * error message.  Status codes are 0 on success and negative on failure;
+ * mamba2_ssd_last_error() returns the calling thread's last message.
+ *
+ * Layouts ([B,L,H,P,N,G] = batch, seqlen, nheads, headdim, dstate, ngroups):
+ *   x, z, out, dout, dx, dz   [B, L, H, P]
+ *   dt, ddt                   [B, L, H]
+ *   A, dt_bias, dA, ddt_bias  [H]
+ *   B, C, dB, dC              [B, L, G, N]
+ *   D, dD                     [H] or [H, P] (MAMBA2_SSD_D_PER_CHANNEL)
+ *   initial_states, final_state, dfinal_state, dinitial_states  [B, H, P, N]
+ *
+ * Reference interfaces replaced (So-cean/mamba-ascendc):
+ *   mamba2_ssd_fwd      -- torch.ops.mamba_ascend.mamba2_ssd_fwd schema
+ *                          (mamba_ascendc/csrc/register.cpp:175-179) and the
+ *                          Python forward paths behind ascend_kernel.mamba2_ssd_fwd
+ *                          (mamba_ascendc/python/ascend_kernel/ascend_kernel/mamba2.py:606-702)
+ *   mamba2_ssd_bwd_m1   -- the M1 backward composition _chunk_mix_ssd_bwd_m1
+ *                          (mamba2.py:1091-1658) reached from
+ *                          _Mamba2SsdAutogradM1.backward (mamba2.py:1782-1838)
+ *   mamba2_ssd_state_passing -- torch.ops.mamba_ascend.mamba2_ssd_state_passing
+ *                          (register.cpp:89-90; op_host mamba2_ssd_state_passing.cpp:12-78)
+ *   *_workspace_size    -- the ACLNN GetWorkspaceSize phase
+ *                          (mamba_ascendc/csrc/utils/torch_aclnn_helper.h:536-546)
+ */
+#ifndef MAMBA2_SSD_H_
+#define MAMBA2_SSD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MAMBA2_SSD_ABI_VERSION 1
+
+/* status codes */
+#define MAMBA2_SSD_OK 0
+#define MAMBA2_SSD_ERR_INVALID_ARGUMENT (-1) /* bad pointer, shape or flag */
+#define MAMBA2_SSD_ERR_UNSUPPORTED (-2)      /* valid but not implemented here */
+#define MAMBA2_SSD_ERR_WORKSPACE (-3)        /* workspace missing or too small */
+#define MAMBA2_SSD_ERR_LAUNCH (-4)           /* a HIP launch failed */
+
+/* feature flags */
+#define MAMBA2_SSD_DT_SOFTPLUS (1u << 0)
+#define MAMBA2_SSD_HAS_D (1u << 1)
+#define MAMBA2_SSD_D_PER_CHANNEL (1u << 2) /* D is [H, P] instead of [H] */
+#define MAMBA2_SSD_HAS_Z (1u << 3)
+#define MAMBA2_SSD_HAS_DT_BIAS (1u << 4)
+#define MAMBA2_SSD_HAS_INITIAL (1u << 5)
+
+typedef struct Mamba2SsdShape {
+    int64_t batch;
+    int64_t seqlen;
+    int64_t nheads;
+    int64_t headdim;
+    int64_t ngroups;
+    int64_t dstate;
+    int64_t chunk_size; /* logical chunk (results do not depend on it) */
+} Mamba2SsdShape;
+
+typedef struct Mamba2SsdFwdArgs {
+    Mamba2SsdShape shape;
+    uint32_t flags;
+    float dt_limit_min; /* clamp of dt after bias/softplus; use 0 and INFINITY */
+    float dt_limit_max; /* for the reference default (0, inf) */
+    const float *x, *dt, *A, *B, *C;
+    const float *D, *z, *dt_bias, *initial_states; /* NULL unless flagged */
+    float *out;         /* [B, L, H, P] */
+    float *final_state; /* [B, H, P, N] or NULL */
+} Mamba2SsdFwdArgs;
+
+typedef struct Mamba2SsdBwdArgs {
+    Mamba2SsdShape shape;
+    uint32_t flags;
+    float dt_limit_min;
+    float dt_limit_max;
+    const float *x, *dt, *A, *B, *C;
+    const float *D, *z, *dt_bias, *initial_states;
+    const float *dout;         /* [B, L, H, P]; NULL means zero */
+    const float *dfinal_state; /* [B, H, P, N]; NULL means zero */
+    float *dx, *ddt, *dA, *dB, *dC;
+    float *dD, *dz, *ddt_bias, *dinitial_states; /* required iff the feature is flagged */
+} Mamba2SsdBwdArgs;
+
+/* Bytes of device workspace mamba2_ssd_fwd needs for this shape/flags. */
+int mamba2_ssd_fwd_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes);
+
+/* Forward: out (and final_state when non-NULL). */
+int mamba2_ssd_fwd(const Mamba2SsdFwdArgs *args, void *workspace, size_t workspace_bytes,
+                   void *stream);
+
+/* Bytes of device workspace mamba2_ssd_bwd_m1 needs for this shape/flags. */
+int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes);
+
+/* M1 backward: gradients of the forward for the given upstream gradients.
+ * Supported: headdim == dstate == 64, fp32 contiguous, any seqlen. */
+int mamba2_ssd_bwd_m1(const Mamba2SsdBwdArgs *args, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* Inter-chunk state passing, in the reference's stage-op form:
+ *   chunk_states [B, H, K, P, N] (read), chunk_log_decay [B, H, K] (sum of dt*A over
+ *   each chunk), initial_states [B, H, P, N] or NULL;
+ *   writes states_start [B, H, K, P, N] (may alias chunk_states) and final_state
+ *   [B, H, P, N] (may be NULL):
+ *     states_start[k] = S ; S = exp(chunk_log_decay[k]) * S + chunk_states[k]. */
+int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_decay,
+                             const float *initial_states, float *states_start,
+                             float *final_state, int64_t batch, int64_t nheads,
+                             int64_t nchunks, int64_t headdim, int64_t dstate, void *stream);
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char *mamba2_ssd_last_error(void);
+
+/* MAMBA2_SSD_ABI_VERSION of the loaded library. */
+int mamba2_ssd_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA2_SSD_H_ */

@@ -1,0 +1,16 @@
+"""MI355X (gfx950) Mamba-2 SSD hot path behind the ``ascend_kernel`` API.
+
+Drop-in for the reference package's public entry points
+(mamba_ascendc/python/ascend_kernel/ascend_kernel/__init__.py):
+``mamba2_ssd_fwd`` and its alias ``mamba_chunk_scan_combined``.  Importing the
+package loads the HIP library (no GPU work) and registers the
+``torch.ops.mamba_ascend`` operators.
+"""
+
+from ._runtime import LIBRARY_PATH, load_library
+from .mamba2 import mamba2_ssd_fwd, mamba_chunk_scan_combined, register_ops
+
+load_library()
+register_ops()
+
+__all__ = ["mamba2_ssd_fwd", "mamba_chunk_scan_combined", "load_library", "LIBRARY_PATH"]

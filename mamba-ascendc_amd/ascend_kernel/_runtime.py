@@ -1,0 +1,148 @@
+"""Loader and ctypes binding of the HIP library ``libmamba2_ssd.so``.
+
+Mirrors the role of the reference's runtime loader
+(mamba_ascendc/python/ascend_kernel/ascend_kernel/_runtime.py:35-65), which
+dlopens the operator library once at import.  Here the library is the C ABI of
+include/mamba2_ssd.h; the structures below are its ctypes mirror.  There is no
+fallback: if the library is missing or fails to load, every GPU call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIBRARY_NAME = "libmamba2_ssd.so"
+LIBRARY_PATH = os.environ.get("MAMBA2_SSD_LIBRARY", os.path.join(_PKG_ROOT, LIBRARY_NAME))
+
+ABI_VERSION = 1
+
+DT_SOFTPLUS = 1 << 0
+HAS_D = 1 << 1
+D_PER_CHANNEL = 1 << 2
+HAS_Z = 1 << 3
+HAS_DT_BIAS = 1 << 4
+HAS_INITIAL = 1 << 5
+
+STATUS_NAMES = {
+    0: "OK",
+    -1: "INVALID_ARGUMENT",
+    -2: "UNSUPPORTED",
+    -3: "WORKSPACE",
+    -4: "LAUNCH",
+}
+
+_c_fp = ctypes.c_void_p
+
+
+class Mamba2SsdShape(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("seqlen", ctypes.c_int64),
+        ("nheads", ctypes.c_int64),
+        ("headdim", ctypes.c_int64),
+        ("ngroups", ctypes.c_int64),
+        ("dstate", ctypes.c_int64),
+        ("chunk_size", ctypes.c_int64),
+    ]
+
+
+class Mamba2SsdFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("shape", Mamba2SsdShape),
+        ("flags", ctypes.c_uint32),
+        ("dt_limit_min", ctypes.c_float),
+        ("dt_limit_max", ctypes.c_float),
+        ("x", _c_fp), ("dt", _c_fp), ("A", _c_fp), ("B", _c_fp), ("C", _c_fp),
+        ("D", _c_fp), ("z", _c_fp), ("dt_bias", _c_fp), ("initial_states", _c_fp),
+        ("out", _c_fp),
+        ("final_state", _c_fp),
+    ]
+
+
+class Mamba2SsdBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("shape", Mamba2SsdShape),
+        ("flags", ctypes.c_uint32),
+        ("dt_limit_min", ctypes.c_float),
+        ("dt_limit_max", ctypes.c_float),
+        ("x", _c_fp), ("dt", _c_fp), ("A", _c_fp), ("B", _c_fp), ("C", _c_fp),
+        ("D", _c_fp), ("z", _c_fp), ("dt_bias", _c_fp), ("initial_states", _c_fp),
+        ("dout", _c_fp), ("dfinal_state", _c_fp),
+        ("dx", _c_fp), ("ddt", _c_fp), ("dA", _c_fp), ("dB", _c_fp), ("dC", _c_fp),
+        ("dD", _c_fp), ("dz", _c_fp), ("ddt_bias", _c_fp), ("dinitial_states", _c_fp),
+    ]
+
+
+# Every symbol include/mamba2_ssd.h declares, with its ctypes signature.
+EXPORTS = {
+    "mamba2_ssd_abi_version": ([], ctypes.c_int),
+    "mamba2_ssd_last_error": ([], ctypes.c_char_p),
+    "mamba2_ssd_fwd_workspace_size": (
+        [ctypes.POINTER(Mamba2SsdShape), ctypes.c_uint32, ctypes.POINTER(ctypes.c_size_t)],
+        ctypes.c_int,
+    ),
+    "mamba2_ssd_fwd": (
+        [ctypes.POINTER(Mamba2SsdFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "mamba2_ssd_bwd_m1_workspace_size": (
+        [ctypes.POINTER(Mamba2SsdShape), ctypes.c_uint32, ctypes.POINTER(ctypes.c_size_t)],
+        ctypes.c_int,
+    ),
+    "mamba2_ssd_bwd_m1": (
+        [ctypes.POINTER(Mamba2SsdBwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "mamba2_ssd_state_passing": (
+        [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 5 + [ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load_library(path: str | None = None):
+    """Load (once) and return the ctypes handle of the HIP library.
+
+    Loading does not touch the GPU, so it also works on a CPU-only host.
+    Raises RuntimeError when the library is missing or its ABI differs.
+    """
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = path or LIBRARY_PATH
+        if not os.path.exists(p):
+            raise RuntimeError(
+                f"HIP library {p} not found; build it with `python -c \"import __graft_entry__ as g; g.build()\"` "
+                "or `python mamba-ascendc_amd/build.py`"
+            )
+        lib = ctypes.CDLL(p, mode=ctypes.RTLD_LOCAL)
+        for name, (argtypes, restype) in EXPORTS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        version = lib.mamba2_ssd_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{p}: ABI version {version}, expected {ABI_VERSION}")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def last_error(lib=None) -> str:
+    lib = lib or load_library()
+    msg = lib.mamba2_ssd_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(status: int, what: str, lib=None) -> None:
+    """Turn a nonzero C status into RuntimeError (the TORCH_CHECK of the reference)."""
+    if status != 0:
+        name = STATUS_NAMES.get(status, str(status))
+        raise RuntimeError(f"{what}: {name}: {last_error(lib)}")

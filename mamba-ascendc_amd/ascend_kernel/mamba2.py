@@ -1,0 +1,415 @@
+"""PyTorch-facing Mamba-2 SSD API on MI355X.
+
+Public surface mirrors mamba_ascendc/python/ascend_kernel/ascend_kernel/mamba2.py:
+
+* ``mamba2_ssd_fwd`` / ``mamba_chunk_scan_combined`` (mamba2.py:1923-2020): same
+  signature, same return convention (``out`` or ``(out, final_state)``), same
+  autograd contract (gradients for x, dt, A, B, C, D, z, dt_bias and
+  initial_states in forward-argument order, mamba2.py:1824-1838), same error
+  types (RuntimeError for bad tensors, NotImplementedError for an unsupported
+  training spec, mamba2.py:1978-1982).
+* ``torch.ops.mamba_ascend.mamba2_ssd_fwd`` / ``mamba2_ssd_bwd_m1`` /
+  ``mamba2_ssd_state_passing``: op schemas of mamba_ascendc/csrc/register.cpp
+  (forward 175-179, state passing 89-90), registered here on the CUDA key
+  (ROCm tensors are ``device.type == "cuda"``) plus a Meta implementation.
+
+Every op calls the HIP library through its C ABI (include/mamba2_ssd.h):
+outputs and workspace come from torch's caching allocator, work is enqueued on
+the current stream, and a nonzero status becomes RuntimeError.  There is no CPU
+path: CPU tensors are rejected.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _runtime as rt
+
+_NS = "mamba_ascend"
+_OPS_DEFINED = False
+_lib_frag = None
+
+
+# ----------------------------------------------------------------------------- validation
+
+def _check_tensor(op: str, name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{op}: {name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{op}: {name} must be a ROCm GPU tensor (got device {t.device})")
+    if t.dtype != torch.float32:
+        raise RuntimeError(f"{op}: {name} must be float32 (got {t.dtype})")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{op}: {name} must be contiguous")
+
+
+def _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
+                  dt_limit_min, dt_limit_max):
+    """Checks of the reference host wrapper
+    (mamba_ascendc/csrc/ops/mamba2_ssd_fwd/op_host/mamba2_ssd_fwd.cpp:15-113)."""
+    for name, t in (("x", x), ("dt", dt), ("A", A), ("B", B), ("C", C)):
+        _check_tensor(op, name, t)
+    for name, t in (("D", D), ("z", z), ("dt_bias", dt_bias), ("initial_states", initial_states)):
+        if t is not None:
+            _check_tensor(op, name, t)
+    if x.dim() != 4:
+        raise RuntimeError(f"{op}: x must have shape [B,L,H,P]")
+    if dt.dim() != 3:
+        raise RuntimeError(f"{op}: dt must have shape [B,L,H]")
+    if A.dim() != 1:
+        raise RuntimeError(f"{op}: A must have shape [H]")
+    if B.dim() != 4 or C.dim() != 4:
+        raise RuntimeError(f"{op}: B and C must have shape [B,L,G,N]")
+    batch, seqlen, nheads, headdim = x.shape
+    ngroups, dstate = B.shape[2], B.shape[3]
+    if min(batch, seqlen, nheads, headdim) <= 0:
+        raise RuntimeError(f"{op}: zero-sized dimensions are not supported")
+    if dstate <= 0 or ngroups <= 0:
+        raise RuntimeError(f"{op}: dstate and ngroups must be positive")
+    if tuple(dt.shape) != (batch, seqlen, nheads):
+        raise RuntimeError(f"{op}: dt shape must equal [B,L,H]")
+    if A.shape[0] != nheads:
+        raise RuntimeError(f"{op}: A shape must equal [H]")
+    if B.shape != C.shape:
+        raise RuntimeError(f"{op}: B and C shapes must match")
+    if B.shape[0] != batch or B.shape[1] != seqlen:
+        raise RuntimeError(f"{op}: B/C batch and sequence dimensions must match x")
+    if nheads % ngroups:
+        raise RuntimeError(f"{op}: nheads must be divisible by ngroups")
+    if int(chunk_size) <= 0:
+        raise RuntimeError(f"{op}: chunk_size must be positive")
+    if not float(dt_limit_min) <= float(dt_limit_max):
+        raise RuntimeError(f"{op}: dt_limit_min must not exceed dt_limit_max")
+    if D is not None:
+        if not ((D.dim() == 1 and D.shape[0] == nheads)
+                or (D.dim() == 2 and tuple(D.shape) == (nheads, headdim))):
+            raise RuntimeError(f"{op}: D must have shape [H] or [H,P]")
+    if z is not None and z.shape != x.shape:
+        raise RuntimeError(f"{op}: z shape must match x")
+    if dt_bias is not None and tuple(dt_bias.shape) != (nheads,):
+        raise RuntimeError(f"{op}: dt_bias shape must equal [H]")
+    if initial_states is not None and tuple(initial_states.shape) != (batch, nheads, headdim, dstate):
+        raise RuntimeError(f"{op}: initial_states must have shape [B,H,P,N]")
+    devices = {t.device for t in (x, dt, A, B, C, D, z, dt_bias, initial_states) if t is not None}
+    if len(devices) != 1:
+        raise RuntimeError(f"{op}: all tensors must be on the same device")
+
+
+def _flags(D, z, dt_bias, initial_states, dt_softplus) -> int:
+    f = 0
+    if dt_softplus:
+        f |= rt.DT_SOFTPLUS
+    if D is not None:
+        f |= rt.HAS_D
+        if D.dim() == 2:
+            f |= rt.D_PER_CHANNEL
+    if z is not None:
+        f |= rt.HAS_Z
+    if dt_bias is not None:
+        f |= rt.HAS_DT_BIAS
+    if initial_states is not None:
+        f |= rt.HAS_INITIAL
+    return f
+
+
+def _shape(x, B, chunk_size) -> rt.Mamba2SsdShape:
+    b, l, h, p = x.shape
+    return rt.Mamba2SsdShape(b, l, h, p, B.shape[2], B.shape[3], int(chunk_size))
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _limit(v: float) -> float:
+    # the schema default 3.4e38 and +inf both mean "no upper clamp"
+    v = float(v)
+    return math.inf if v >= 3.4e38 else v
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+# ----------------------------------------------------------------------------- raw calls
+
+def _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softplus,
+             dt_limit_min, dt_limit_max, want_final=True):
+    lib = rt.load_library()
+    shape = _shape(x, B, chunk_size)
+    flags = _flags(D, z, dt_bias, initial_states, dt_softplus)
+    nbytes = ctypes.c_size_t(0)
+    rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shape), flags, ctypes.byref(nbytes)),
+             "mamba2_ssd_fwd_workspace_size", lib)
+    out = torch.empty_like(x)
+    b, _, h, p = x.shape
+    final = torch.empty(b, h, p, B.shape[3], device=x.device, dtype=torch.float32) if want_final else None
+    ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=x.device)
+    args = rt.Mamba2SsdFwdArgs(
+        shape, flags, float(dt_limit_min), _limit(dt_limit_max),
+        _ptr(x), _ptr(dt), _ptr(A), _ptr(B), _ptr(C),
+        _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(initial_states),
+        _ptr(out), _ptr(final),
+    )
+    with torch.cuda.device(x.device):
+        rt.check(lib.mamba2_ssd_fwd(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(x.device)),
+                 "mamba2_ssd_fwd", lib)
+    return out, final
+
+
+def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, chunk_size,
+             dt_softplus, dt_limit_min, dt_limit_max):
+    lib = rt.load_library()
+    shape = _shape(x, B, chunk_size)
+    flags = _flags(D, z, dt_bias, initial_states, dt_softplus)
+    nbytes = ctypes.c_size_t(0)
+    rt.check(lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(shape), flags, ctypes.byref(nbytes)),
+             "mamba2_ssd_bwd_m1_workspace_size", lib)
+    dx = torch.empty_like(x)
+    ddt = torch.empty_like(dt)
+    dA = torch.empty_like(A)
+    dB = torch.empty_like(B)
+    dC = torch.empty_like(C)
+    dD = torch.empty_like(D) if D is not None else None
+    dz = torch.empty_like(z) if z is not None else None
+    ddt_bias = torch.empty_like(dt_bias) if dt_bias is not None else None
+    dinit = torch.empty_like(initial_states) if initial_states is not None else None
+    ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=x.device)
+    args = rt.Mamba2SsdBwdArgs(
+        shape, flags, float(dt_limit_min), _limit(dt_limit_max),
+        _ptr(x), _ptr(dt), _ptr(A), _ptr(B), _ptr(C),
+        _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(initial_states),
+        _ptr(dout), _ptr(dfinal_state),
+        _ptr(dx), _ptr(ddt), _ptr(dA), _ptr(dB), _ptr(dC),
+        _ptr(dD), _ptr(dz), _ptr(ddt_bias), _ptr(dinit),
+    )
+    with torch.cuda.device(x.device):
+        rt.check(lib.mamba2_ssd_bwd_m1(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(x.device)),
+                 "mamba2_ssd_bwd_m1", lib)
+    return dx, ddt, dA, dB, dC, dD, dz, ddt_bias, dinit
+
+
+# ----------------------------------------------------------------------------- torch ops
+
+_FWD_SCHEMA = (
+    "mamba2_ssd_fwd(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? z, "
+    "Tensor? dt_bias, Tensor? initial_states, int chunk_size=256, bool dt_softplus=False, "
+    "float dt_limit_min=0.0, float dt_limit_max=3.4e38) -> (Tensor, Tensor)"
+)
+_BWD_SCHEMA = (
+    "mamba2_ssd_bwd_m1(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor dout, "
+    "Tensor? dfinal_state, Tensor? D, Tensor? z, Tensor? dt_bias, Tensor? initial_states, "
+    "int chunk_size=64, bool dt_softplus=False, float dt_limit_min=0.0, "
+    "float dt_limit_max=3.4e38) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
+    "Tensor, Tensor)"
+)
+_SP_SCHEMA = (
+    "mamba2_ssd_state_passing(Tensor chunk_states, Tensor dA_cumsum, Tensor? initial_states) "
+    "-> (Tensor, Tensor)"
+)
+
+
+def _op_fwd_cuda(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size=256,
+                 dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
+    _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
+                  dt_limit_min, dt_limit_max)
+    return _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softplus,
+                    dt_limit_min, dt_limit_max)
+
+
+def _op_fwd_meta(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size=256,
+                 dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
+    b, _, h, p = x.shape
+    return torch.empty_like(x), x.new_empty(b, h, p, B.shape[3], dtype=torch.float32)
+
+
+def _empty_like_or_none(t, ref):
+    return ref.new_empty(0) if t is None else t
+
+
+def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
+                 chunk_size=64, dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
+    op = "mamba2_ssd_bwd_m1"
+    _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
+                  dt_limit_min, dt_limit_max)
+    _check_tensor(op, "dout", dout)
+    if dout.shape != x.shape:
+        raise RuntimeError(f"{op}: dout shape must match x")
+    if dfinal_state is not None:
+        _check_tensor(op, "dfinal_state", dfinal_state)
+        if tuple(dfinal_state.shape) != (x.shape[0], x.shape[2], x.shape[3], B.shape[3]):
+            raise RuntimeError(f"{op}: dfinal_state must have shape [B,H,P,N]")
+    grads = _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
+                     chunk_size, dt_softplus, dt_limit_min, dt_limit_max)
+    return tuple(_empty_like_or_none(g, x) for g in grads)
+
+
+def _op_bwd_meta(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
+                 chunk_size=64, dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
+    like = lambda t: x.new_empty(0) if t is None else torch.empty_like(t)  # noqa: E731
+    return (torch.empty_like(x), torch.empty_like(dt), torch.empty_like(A), torch.empty_like(B),
+            torch.empty_like(C), like(D), like(z), like(dt_bias), like(initial_states))
+
+
+def _op_sp_cuda(chunk_states, dA_cumsum, initial_states):
+    op = "mamba2_ssd_state_passing"
+    _check_tensor(op, "chunk_states", chunk_states)
+    _check_tensor(op, "dA_cumsum", dA_cumsum)
+    if chunk_states.dim() != 5:
+        raise RuntimeError(f"{op}: chunk_states must have shape [B,H,K,P,N]")
+    b, h, k, p, n = chunk_states.shape
+    if dA_cumsum.dim() != 4 or tuple(dA_cumsum.shape[:3]) != (b, h, k):
+        raise RuntimeError(f"{op}: dA_cumsum must have shape [B,H,K,T]")
+    if initial_states is not None:
+        _check_tensor(op, "initial_states", initial_states)
+        if tuple(initial_states.shape) != (b, h, p, n):
+            raise RuntimeError(f"{op}: initial_states must have shape [B,H,P,N]")
+    log_decay = dA_cumsum[..., -1].contiguous()
+    states = torch.empty_like(chunk_states)
+    final = chunk_states.new_empty(b, h, p, n)
+    lib = rt.load_library()
+    with torch.cuda.device(chunk_states.device):
+        rt.check(lib.mamba2_ssd_state_passing(
+            _ptr(chunk_states), _ptr(log_decay), _ptr(initial_states), _ptr(states), _ptr(final),
+            b, h, k, p, n, _stream(chunk_states.device)), op, lib)
+    return states, final
+
+
+def _op_sp_meta(chunk_states, dA_cumsum, initial_states):
+    b, h, k, p, n = chunk_states.shape
+    return torch.empty_like(chunk_states), chunk_states.new_empty(b, h, p, n)
+
+
+def register_ops() -> None:
+    """Define ``torch.ops.mamba_ascend.*`` once (CUDA + Meta implementations)."""
+    global _OPS_DEFINED, _lib_frag
+    if _OPS_DEFINED:
+        return
+    frag = torch.library.Library(_NS, "FRAGMENT")
+    for schema, cuda_fn, meta_fn in (
+        (_FWD_SCHEMA, _op_fwd_cuda, _op_fwd_meta),
+        (_BWD_SCHEMA, _op_bwd_cuda, _op_bwd_meta),
+        (_SP_SCHEMA, _op_sp_cuda, _op_sp_meta),
+    ):
+        name = schema.split("(", 1)[0]
+        frag.define(schema)
+        frag.impl(name, cuda_fn, "CUDA")
+        frag.impl(name, meta_fn, "Meta")
+    _lib_frag = frag
+    _OPS_DEFINED = True
+
+
+# ----------------------------------------------------------------------------- autograd
+
+def _requires_grad(*values) -> bool:
+    return torch.is_grad_enabled() and any(
+        isinstance(v, torch.Tensor) and v.requires_grad for v in values
+    )
+
+
+def _can_use_native_bwd_m1(x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states) -> bool:
+    """Training spec served by the M1 backward (mamba2.py:742-803): fp32
+    contiguous GPU tensors with headdim == dstate == 64.  Unlike the reference,
+    any chunk_size and any seqlen are accepted: the kernels run fixed 64-token
+    execution chunks and the result does not depend on the logical chunk."""
+    tensors = [t for t in (x, dt, A, B, C, D, z, dt_bias, initial_states) if t is not None]
+    if any(t.device.type != "cuda" or t.dtype != torch.float32 or not t.is_contiguous()
+           for t in tensors):
+        return False
+    if x.dim() != 4 or B.dim() != 4:
+        return False
+    return x.shape[-1] == 64 and B.shape[-1] == 64 and int(chunk_size) > 0
+
+
+class _Mamba2SsdAutogradM1(torch.autograd.Function):
+    """Autograd contract of mamba2.py:1661-1838: saves the inputs, recomputes
+    the forward intermediates in backward, returns 13 gradients."""
+
+    @staticmethod
+    def forward(ctx, x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus,
+                dt_limit_min, dt_limit_max, initial_states):
+        out, final_state = torch.ops.mamba_ascend.mamba2_ssd_fwd(
+            x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
+            float(dt_limit_min), float(dt_limit_max))
+        empty = x.new_empty(0)
+        ctx.save_for_backward(
+            x, dt, A, B, C,
+            D if D is not None else empty,
+            z if z is not None else empty,
+            dt_bias if dt_bias is not None else empty,
+            initial_states if initial_states is not None else empty,
+        )
+        ctx.has = (D is not None, z is not None, dt_bias is not None, initial_states is not None)
+        ctx.chunk_size = int(chunk_size)
+        ctx.dt_softplus = bool(dt_softplus)
+        ctx.dt_limit = (float(dt_limit_min), float(dt_limit_max))
+        return out, final_state
+
+    @staticmethod
+    def backward(ctx, dout, dfinal_state):
+        x, dt, A, B, C, D, z, dt_bias, initial_states = ctx.saved_tensors
+        has_D, has_z, has_bias, has_init = ctx.has
+        if dout is None:
+            dout = torch.zeros_like(x)
+        grads = torch.ops.mamba_ascend.mamba2_ssd_bwd_m1(
+            x, dt, A, B, C, dout.contiguous(),
+            None if dfinal_state is None else dfinal_state.contiguous(),
+            D if has_D else None, z if has_z else None, dt_bias if has_bias else None,
+            initial_states if has_init else None, ctx.chunk_size, ctx.dt_softplus,
+            ctx.dt_limit[0], ctx.dt_limit[1])
+        dx, ddt, dA, dB, dC, dD, dz, ddt_bias, dinit = grads
+        return (dx, ddt, dA, dB, dC, None,
+                dD if has_D else None, dz if has_z else None, ddt_bias if has_bias else None,
+                None, None, None, dinit if has_init else None)
+
+
+# ----------------------------------------------------------------------------- public API
+
+def mamba2_ssd_fwd(
+    x: torch.Tensor,
+    dt: torch.Tensor,
+    A: torch.Tensor,
+    B: torch.Tensor,
+    C: torch.Tensor,
+    chunk_size: int,
+    D: Optional[torch.Tensor] = None,
+    z: Optional[torch.Tensor] = None,
+    dt_bias: Optional[torch.Tensor] = None,
+    dt_softplus: bool = False,
+    dt_limit: Tuple[float, float] = (0.0, float("inf")),
+    initial_states: Optional[torch.Tensor] = None,
+    return_final_state: bool = False,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """Mamba-2 SSD forward (chunked selective scan) on MI355X.
+
+    Shapes: x [B,L,H,P], dt [B,L,H], A [H], B/C [B,L,G,N], D [H] or [H,P],
+    z [B,L,H,P], dt_bias [H], initial_states [B,H,P,N]; all fp32 contiguous
+    ROCm tensors.  Returns ``out`` [B,L,H,P], plus ``final_state`` [B,H,P,N]
+    when ``return_final_state``.  When any input requires grad the call goes
+    through the M1 autograd function.
+    """
+    register_ops()
+    lo, hi = float(dt_limit[0]), float(dt_limit[1])
+    if _requires_grad(x, dt, A, B, C, D, z, dt_bias, initial_states):
+        if not _can_use_native_bwd_m1(x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states):
+            raise NotImplementedError(
+                "mamba2_ssd_fwd backward requires contiguous FP32 GPU tensors with "
+                "headdim == dstate == 64"
+            )
+        out, final_state = _Mamba2SsdAutogradM1.apply(
+            x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus, lo, hi, initial_states)
+    else:
+        _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
+                      initial_states, lo, hi)
+        out, final_state = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
+                                    dt_softplus, lo, hi, want_final=return_final_state)
+    if return_final_state:
+        return out, final_state
+    return out
+
+
+mamba_chunk_scan_combined = mamba2_ssd_fwd

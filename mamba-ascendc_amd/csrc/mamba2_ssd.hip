@@ -1,0 +1,233 @@
+// C ABI of the Mamba-2 SSD hot path (declarations in include/mamba2_ssd.h).
+//
+// Host side of the library: argument validation (the checks of the reference
+// host wrappers, mamba_ascendc/csrc/ops/mamba2_ssd_fwd/op_host/mamba2_ssd_fwd.cpp:15-136),
+// workspace sizing, and kernel launches on the caller's stream.  Nothing here
+// allocates device memory.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/mamba2_ssd.h"
+#include "ssd_bwd_kernels.h"
+#include "ssd_fwd_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_err[0] = '\0';
+    return MAMBA2_SSD_OK;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+constexpr uint32_t kKnownFlags = MAMBA2_SSD_DT_SOFTPLUS | MAMBA2_SSD_HAS_D |
+                                 MAMBA2_SSD_D_PER_CHANNEL | MAMBA2_SSD_HAS_Z |
+                                 MAMBA2_SSD_HAS_DT_BIAS | MAMBA2_SSD_HAS_INITIAL;
+
+int check_shape(const Mamba2SsdShape *s, uint32_t flags) {
+    if (!s) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "shape is NULL");
+    if (flags & ~kKnownFlags) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "unknown flag bits 0x%x", flags);
+    if ((flags & MAMBA2_SSD_D_PER_CHANNEL) && !(flags & MAMBA2_SSD_HAS_D))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "D_PER_CHANNEL set without HAS_D");
+    if (s->batch <= 0 || s->seqlen < 0 || s->nheads <= 0 || s->headdim <= 0 || s->ngroups <= 0 ||
+        s->dstate <= 0)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "non-positive dimension (B=%lld L=%lld H=%lld P=%lld G=%lld N=%lld)",
+                    (long long)s->batch, (long long)s->seqlen, (long long)s->nheads,
+                    (long long)s->headdim, (long long)s->ngroups, (long long)s->dstate);
+    if (s->chunk_size <= 0)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "chunk_size must be positive, got %lld",
+                    (long long)s->chunk_size);
+    if (s->nheads % s->ngroups)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "nheads=%lld not divisible by ngroups=%lld",
+                    (long long)s->nheads, (long long)s->ngroups);
+    if (s->batch > 65535 || s->nheads > 65535)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "batch and nheads must be <= 65535");
+    return MAMBA2_SSD_OK;
+}
+
+// Shapes served by the MFMA chunk kernels; everything else runs the generic
+// token recurrence.
+bool fast_path(const Mamba2SsdShape *s) {
+    return s->headdim == 64 && (s->dstate == 64 || s->dstate == 128);
+}
+
+int64_t nchunks(const Mamba2SsdShape *s) { return (s->seqlen + ssd::kChunk - 1) / ssd::kChunk; }
+
+size_t fwd_ws_bytes(const Mamba2SsdShape *s) {
+    if (!fast_path(s) || s->seqlen == 0) return 0;
+    const size_t bhk = (size_t)s->batch * s->nheads * nchunks(s);
+    return align256(bhk * s->headdim * s->dstate * sizeof(float)) + align256(bhk * sizeof(float));
+}
+
+int launch_status(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(MAMBA2_SSD_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+    return MAMBA2_SSD_OK;
+}
+
+template <int P, int N>
+int launch_fwd_fast(const ssd::FwdParams &prm, int B, hipStream_t st) {
+    const dim3 grid(prm.K, prm.H, B);
+    hipLaunchKernelGGL((ssd::k_chunk_state<P, N>), grid, dim3(ssd::kThreads), 0, st, prm);
+    if (int rc = launch_status("k_chunk_state")) return rc;
+    const int PN = P * N;
+    const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
+    hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, prm.states,
+                       prm.chunk_log_decay, prm.init, prm.states, prm.final_state, prm.K, PN);
+    if (int rc = launch_status("k_state_pass")) return rc;
+    hipLaunchKernelGGL((ssd::k_chunk_scan<P, N>), grid, dim3(ssd::kThreads), 0, st, prm);
+    return launch_status("k_chunk_scan");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mamba2_ssd_abi_version(void) { return MAMBA2_SSD_ABI_VERSION; }
+
+const char *mamba2_ssd_last_error(void) { return g_err; }
+
+int mamba2_ssd_fwd_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes) {
+    if (int rc = check_shape(shape, flags)) return rc;
+    if (!bytes) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "bytes is NULL");
+    *bytes = fwd_ws_bytes(shape);
+    return ok();
+}
+
+int mamba2_ssd_fwd(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
+                   void *stream) {
+    if (!a) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "args is NULL");
+    const Mamba2SsdShape *s = &a->shape;
+    if (int rc = check_shape(s, a->flags)) return rc;
+    if (!a->x || !a->dt || !a->A || !a->B || !a->C || !a->out)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "x, dt, A, B, C and out must be non-NULL");
+    const uint32_t f = a->flags;
+    if (bool(f & MAMBA2_SSD_HAS_D) != (a->D != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "D pointer and HAS_D flag disagree");
+    if (bool(f & MAMBA2_SSD_HAS_Z) != (a->z != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "z pointer and HAS_Z flag disagree");
+    if (bool(f & MAMBA2_SSD_HAS_DT_BIAS) != (a->dt_bias != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "dt_bias pointer and HAS_DT_BIAS flag disagree");
+    if (bool(f & MAMBA2_SSD_HAS_INITIAL) != (a->initial_states != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "initial_states pointer and HAS_INITIAL flag disagree");
+    if (!(a->dt_limit_min <= a->dt_limit_max))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "dt_limit_min > dt_limit_max");
+    const size_t need = fwd_ws_bytes(s);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need,
+                    workspace ? workspace_bytes : (size_t)0);
+    hipStream_t st = (hipStream_t)stream;
+
+    ssd::FwdParams prm{};
+    prm.x = a->x;
+    prm.dt = a->dt;
+    prm.A = a->A;
+    prm.B = a->B;
+    prm.C = a->C;
+    prm.D = a->D;
+    prm.z = a->z;
+    prm.dt_bias = a->dt_bias;
+    prm.init = a->initial_states;
+    prm.out = a->out;
+    prm.final_state = a->final_state;
+    prm.L = s->seqlen;
+    prm.H = (int)s->nheads;
+    prm.G = (int)s->ngroups;
+    prm.R = (int)(s->nheads / s->ngroups);
+    prm.K = (int)nchunks(s);
+    prm.softplus = (f & MAMBA2_SSD_DT_SOFTPLUS) != 0;
+    prm.has_D = (f & MAMBA2_SSD_HAS_D) != 0;
+    prm.d_per_channel = (f & MAMBA2_SSD_D_PER_CHANNEL) != 0;
+    prm.has_z = (f & MAMBA2_SSD_HAS_Z) != 0;
+    prm.lo = a->dt_limit_min;
+    prm.hi = a->dt_limit_max;
+
+    const int B = (int)s->batch;
+    if (s->seqlen == 0) {
+        // no tokens: the final state is the initial state (or zero)
+        if (a->final_state) {
+            const size_t n = (size_t)s->batch * s->nheads * s->headdim * s->dstate * sizeof(float);
+            hipError_t e = a->initial_states
+                               ? hipMemcpyAsync(a->final_state, a->initial_states, n,
+                                                hipMemcpyDeviceToDevice, st)
+                               : hipMemsetAsync(a->final_state, 0, n, st);
+            if (e != hipSuccess)
+                return fail(MAMBA2_SSD_ERR_LAUNCH, "final-state copy failed: %s", hipGetErrorString(e));
+        }
+        return ok();
+    }
+    if (fast_path(s)) {
+        const size_t bhk = (size_t)s->batch * s->nheads * prm.K;
+        prm.states = (float *)workspace;
+        prm.chunk_log_decay =
+            (float *)((char *)workspace + align256(bhk * s->headdim * s->dstate * sizeof(float)));
+        int rc = s->dstate == 64 ? launch_fwd_fast<64, 64>(prm, B, st)
+                                 : launch_fwd_fast<64, 128>(prm, B, st);
+        return rc ? rc : ok();
+    }
+    if (s->dstate > 256)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "dstate=%lld > 256 is not supported",
+                    (long long)s->dstate);
+    const dim3 grid((unsigned)s->headdim, prm.H, B);
+    hipLaunchKernelGGL(ssd::k_generic_fwd, grid, dim3(64), 0, st, prm, (int)s->headdim,
+                       (int)s->dstate);
+    if (int rc = launch_status("k_generic_fwd")) return rc;
+    return ok();
+}
+
+int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_decay,
+                             const float *initial_states, float *states_start,
+                             float *final_state, int64_t batch, int64_t nheads, int64_t nchunks_,
+                             int64_t headdim, int64_t dstate, void *stream) {
+    if (!chunk_states || !chunk_log_decay || !states_start)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "chunk_states, chunk_log_decay and states_start must be non-NULL");
+    if (batch <= 0 || nheads <= 0 || nchunks_ <= 0 || headdim <= 0 || dstate <= 0)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "non-positive dimension");
+    const int64_t PN = headdim * dstate;
+    if (PN % 4)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "headdim*dstate must be a multiple of 4");
+    if (batch * nheads > 65535 || PN > (int64_t)1 << 30 || nchunks_ > (int64_t)1 << 30)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "problem too large for one launch");
+    const dim3 grid((unsigned)((PN / 4 + ssd::kThreads - 1) / ssd::kThreads), (unsigned)(batch * nheads));
+    hipLaunchKernelGGL(ssd::k_state_pass, grid, dim3(ssd::kThreads), 0, (hipStream_t)stream,
+                       chunk_states, chunk_log_decay, initial_states, states_start, final_state,
+                       (int)nchunks_, (int)PN);
+    if (int rc = launch_status("k_state_pass")) return rc;
+    return ok();
+}
+
+int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes) {
+    if (int rc = check_shape(shape, flags)) return rc;
+    if (!bytes) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "bytes is NULL");
+    *bytes = 0;
+    return ok();
+}
+
+int mamba2_ssd_bwd_m1(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
+                      void *stream) {
+    (void)a;
+    (void)workspace;
+    (void)workspace_bytes;
+    (void)stream;
+    return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "mamba2_ssd_bwd_m1 is not built yet");
+}
+
+}  // extern "C"

@@ -1,0 +1,181 @@
+"""CPU-side checks of the C ABI and the host logic (no GPU work).
+
+* the library loads and exports every function include/mamba2_ssd.h declares;
+* argument validation returns the documented status codes before any HIP call
+  (the host checks of mamba_ascendc/csrc/ops/mamba2_ssd_fwd/op_host/mamba2_ssd_fwd.cpp:15-113);
+* the Python API raises the reference's error types (RuntimeError for bad
+  tensors, NotImplementedError for an unsupported training spec,
+  mamba2.py:1978-1982) and the Meta implementation infers shapes.
+"""
+
+import ctypes
+import math
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from ascend_kernel import _runtime as rt
+from ascend_kernel import mamba2 as api
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mamba2_ssd.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mamba2_ssd_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared_functions()
+    assert "mamba2_ssd_fwd" in names and "mamba2_ssd_bwd_m1" in names
+    assert set(names) == set(rt.EXPORTS), (names, sorted(rt.EXPORTS))
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", rt.LIBRARY_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (mamba2_ssd_\w+)", out))
+    for name in _declared_functions():
+        assert name in exported, name
+    lib = rt.load_library()
+    assert lib.mamba2_ssd_abi_version() == rt.ABI_VERSION
+
+
+def _shape(**kw):
+    d = dict(batch=2, seqlen=128, nheads=4, headdim=64, ngroups=2, dstate=64, chunk_size=64)
+    d.update(kw)
+    return rt.Mamba2SsdShape(**d)
+
+
+@pytest.mark.parametrize(
+    "kw,flags,code",
+    [
+        (dict(), 0, 0),
+        (dict(nheads=3), 0, -1),
+        (dict(batch=0), 0, -1),
+        (dict(chunk_size=0), 0, -1),
+        (dict(dstate=-1), 0, -1),
+        (dict(), rt.D_PER_CHANNEL, -1),
+        (dict(), 1 << 12, -1),
+        (dict(batch=70000), 0, -2),
+    ],
+)
+def test_workspace_size_validation(kw, flags, code):
+    lib = rt.load_library()
+    nbytes = ctypes.c_size_t(123)
+    rc = lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(_shape(**kw)), flags, ctypes.byref(nbytes))
+    assert rc == code, rt.last_error(lib)
+    if code:
+        assert rt.last_error(lib)
+    rc = lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(_shape(**kw)), flags, ctypes.byref(nbytes))
+    assert rc == code
+
+
+def test_workspace_size_formula():
+    lib = rt.load_library()
+    nbytes = ctypes.c_size_t(0)
+    s = _shape(batch=8, seqlen=4096, nheads=256, ngroups=64)
+    assert lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(s), 0, ctypes.byref(nbytes)) == 0
+    k = 4096 // 64
+    # chunk states [B,H,K,P,N] fp32 + per-chunk log decay [B,H,K]
+    assert nbytes.value >= 8 * 256 * k * 64 * 64 * 4 + 8 * 256 * k * 4
+
+
+def test_fwd_rejects_null_and_flag_mismatch_without_gpu():
+    lib = rt.load_library()
+    args = rt.Mamba2SsdFwdArgs()
+    args.shape = _shape()
+    args.dt_limit_max = math.inf
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
+    assert "non-NULL" in rt.last_error(lib)
+    fake = ctypes.c_void_p(0x1000)
+    for name in ("x", "dt", "A", "B", "C", "out"):
+        setattr(args, name, fake)
+    args.flags = rt.HAS_D  # flag without pointer
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
+    assert "HAS_D" in rt.last_error(lib)
+    args.flags = 0
+    args.dt_limit_min, args.dt_limit_max = 1.0, 0.5
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
+    args.dt_limit_min, args.dt_limit_max = 0.0, math.inf
+    # fast-path shape without workspace
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -3
+    assert lib.mamba2_ssd_fwd(None, None, 0, None) == -1
+
+
+def test_state_passing_rejects_bad_arguments():
+    lib = rt.load_library()
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.mamba2_ssd_state_passing(None, fake, None, fake, None, 1, 1, 1, 64, 64, None) == -1
+    assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 1, 1, 0, 64, 64, None) == -1
+    assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 1, 1, 1, 3, 3, None) == -2
+
+
+def _cpu_inputs():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 64, 2, 64, generator=g)
+    dt = torch.rand(1, 64, 2, generator=g)
+    A = -torch.rand(2, generator=g)
+    B = torch.randn(1, 64, 1, 64, generator=g)
+    C = torch.randn(1, 64, 1, 64, generator=g)
+    return x, dt, A, B, C
+
+
+def test_public_api_rejects_cpu_tensors():
+    x, dt, A, B, C = _cpu_inputs()
+    with pytest.raises(RuntimeError, match="ROCm GPU tensor"):
+        api.mamba2_ssd_fwd(x, dt, A, B, C, 64)
+
+
+def test_public_api_training_spec_error():
+    x, dt, A, B, C = _cpu_inputs()
+    x.requires_grad_(True)
+    with pytest.raises(NotImplementedError):
+        api.mamba2_ssd_fwd(x, dt, A, B, C, 64, dt_softplus=True)
+
+
+def test_meta_shape_inference():
+    api.register_ops()
+    x = torch.empty(2, 100, 8, 64, device="meta")
+    dt = torch.empty(2, 100, 8, device="meta")
+    A = torch.empty(8, device="meta")
+    B = torch.empty(2, 100, 2, 128, device="meta")
+    out, final = torch.ops.mamba_ascend.mamba2_ssd_fwd(x, dt, A, B, B, None, None, None, None, 64)
+    assert out.shape == x.shape and final.shape == (2, 8, 64, 128)
+    grads = torch.ops.mamba_ascend.mamba2_ssd_bwd_m1(x, dt, A, B, B, x, None, None, None, None, None)
+    assert [tuple(g.shape) for g in grads[:5]] == [tuple(x.shape), tuple(dt.shape), (8,), tuple(B.shape), tuple(B.shape)]
+    states, fin = torch.ops.mamba_ascend.mamba2_ssd_state_passing(
+        torch.empty(2, 8, 4, 64, 64, device="meta"), torch.empty(2, 8, 4, 64, device="meta"), None)
+    assert states.shape == (2, 8, 4, 64, 64) and fin.shape == (2, 8, 64, 64)
+
+
+@pytest.mark.parametrize(
+    "mutate,match",
+    [
+        (lambda t: {**t, "dt": t["dt"][..., :1].contiguous()}, "dt shape"),
+        (lambda t: {**t, "A": t["A"][:1].contiguous()}, "A shape"),
+        (lambda t: {**t, "C": t["C"][:, :, :, :32].contiguous()}, "B and C shapes"),
+        (lambda t: {**t, "x": t["x"].transpose(1, 2)}, "contiguous"),
+        (lambda t: {**t, "x": t["x"].double()}, "float32"),
+    ],
+)
+def test_validation_messages(mutate, match, monkeypatch):
+    """Shape/dtype/layout checks, with the device check bypassed (no GPU here)."""
+    x, dt, A, B, C = _cpu_inputs()
+    t = mutate(dict(x=x, dt=dt, A=A, B=B, C=C))
+
+    def check(op, name, ten):
+        if ten.dtype != torch.float32:
+            raise RuntimeError(f"{op}: {name} must be float32 (got {ten.dtype})")
+        if not ten.is_contiguous():
+            raise RuntimeError(f"{op}: {name} must be contiguous")
+
+    monkeypatch.setattr(api, "_check_tensor", check)
+    with pytest.raises(RuntimeError, match=match):
+        api._validate_fwd("mamba2_ssd_fwd", t["x"], t["dt"], t["A"], t["B"], t["C"], 64,
+                          None, None, None, None, 0.0, math.inf)
