@@ -97,6 +97,17 @@ int mamba2_ssd_fwd_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, s
 int mamba2_ssd_fwd(const Mamba2SsdFwdArgs *args, void *workspace, size_t workspace_bytes,
                    void *stream);
 
+/* Forward with a per-kernel event trace, for benchmarks and profilers.
+ * events[] are caller-created hipEvent_t handles (passed as void*): events[0]
+ * is recorded on the stream before the first kernel and events[i + 1] right
+ * after kernel i.  On return *nkernels holds the number of kernels launched
+ * and, when names is non-NULL, names[i] the (static) name of kernel i.
+ * Replaces the stage decomposition the reference obtains from the NPU
+ * profiler (benchmarks/mamba2_forward_npu_profile.py:36-112, 156-171). */
+int mamba2_ssd_fwd_traced(const Mamba2SsdFwdArgs *args, void *workspace, size_t workspace_bytes,
+                          void *stream, void *const *events, int nevents, const char **names,
+                          int *nkernels);
+
 /* Bytes of device workspace mamba2_ssd_bwd_m1 needs for this shape/flags. */
 int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes);
 

@@ -88,6 +88,12 @@ EXPORTS = {
         [ctypes.POINTER(Mamba2SsdFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
         ctypes.c_int,
     ),
+    "mamba2_ssd_fwd_traced": (
+        [ctypes.POINTER(Mamba2SsdFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+         ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+         ctypes.POINTER(ctypes.c_int)],
+        ctypes.c_int,
+    ),
     "mamba2_ssd_bwd_m1_workspace_size": (
         [ctypes.POINTER(Mamba2SsdShape), ctypes.c_uint32, ctypes.POINTER(ctypes.c_size_t)],
         ctypes.c_int,

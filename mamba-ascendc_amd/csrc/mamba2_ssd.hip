@@ -74,25 +74,48 @@ size_t fwd_ws_bytes(const Mamba2SsdShape *s) {
     return align256(bhk * s->headdim * s->dstate * sizeof(float)) + align256(bhk * sizeof(float));
 }
 
-int launch_status(const char *what) {
-    hipError_t e = hipGetLastError();
+// Optional per-kernel event trace: events[0] is recorded before the first
+// kernel and events[i + 1] right after kernel i, all on the launch stream.
+struct Trace {
+    void *const *events = nullptr;
+    int capacity = 0;
+    int used = 0;
+    const char **names = nullptr; // kernel name of stage i (static strings)
+};
+
+int record(Trace *tr, hipStream_t st, const char *name) {
+    if (!tr || !tr->events) return MAMBA2_SSD_OK;
+    if (tr->used >= tr->capacity)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "trace needs more than %d events",
+                    tr->capacity);
+    hipError_t e = hipEventRecord((hipEvent_t)tr->events[tr->used], st);
     if (e != hipSuccess)
-        return fail(MAMBA2_SSD_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+        return fail(MAMBA2_SSD_ERR_LAUNCH, "hipEventRecord failed: %s", hipGetErrorString(e));
+    if (name && tr->names && tr->used > 0) tr->names[tr->used - 1] = name;
+    ++tr->used;
     return MAMBA2_SSD_OK;
 }
 
+int launch_status(const char *what, Trace *tr = nullptr, hipStream_t st = nullptr) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(MAMBA2_SSD_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+    return record(tr, st, what);
+}
+
 template <int P, int N>
-int launch_fwd_fast(const ssd::FwdParams &prm, int B, hipStream_t st) {
+int launch_fwd_fast(const ssd::FwdParams &prm, int B, hipStream_t st, Trace *tr) {
     const dim3 grid(prm.K, prm.H, B);
+    if (int rc = record(tr, st, nullptr)) return rc;
     hipLaunchKernelGGL((ssd::k_chunk_state<P, N>), grid, dim3(ssd::kThreads), 0, st, prm);
-    if (int rc = launch_status("k_chunk_state")) return rc;
+    if (int rc = launch_status("k_chunk_state", tr, st)) return rc;
     const int PN = P * N;
     const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
     hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, prm.states,
                        prm.chunk_log_decay, prm.init, prm.states, prm.final_state, prm.K, PN);
-    if (int rc = launch_status("k_state_pass")) return rc;
+    if (int rc = launch_status("k_state_pass", tr, st)) return rc;
     hipLaunchKernelGGL((ssd::k_chunk_scan<P, N>), grid, dim3(ssd::kThreads), 0, st, prm);
-    return launch_status("k_chunk_scan");
+    return launch_status("k_chunk_scan", tr, st);
 }
 
 }  // namespace
@@ -110,8 +133,12 @@ int mamba2_ssd_fwd_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, s
     return ok();
 }
 
-int mamba2_ssd_fwd(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
-                   void *stream) {
+}  // extern "C"
+
+namespace {
+
+int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes, void *stream,
+             Trace *tr) {
     if (!a) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "args is NULL");
     const Mamba2SsdShape *s = &a->shape;
     if (int rc = check_shape(s, a->flags)) return rc;
@@ -178,18 +205,42 @@ int mamba2_ssd_fwd(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_
         prm.states = (float *)workspace;
         prm.chunk_log_decay =
             (float *)((char *)workspace + align256(bhk * s->headdim * s->dstate * sizeof(float)));
-        int rc = s->dstate == 64 ? launch_fwd_fast<64, 64>(prm, B, st)
-                                 : launch_fwd_fast<64, 128>(prm, B, st);
+        int rc = s->dstate == 64 ? launch_fwd_fast<64, 64>(prm, B, st, tr)
+                                 : launch_fwd_fast<64, 128>(prm, B, st, tr);
         return rc ? rc : ok();
     }
     if (s->dstate > 256)
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "dstate=%lld > 256 is not supported",
                     (long long)s->dstate);
     const dim3 grid((unsigned)s->headdim, prm.H, B);
+    if (int rc = record(tr, st, nullptr)) return rc;
     hipLaunchKernelGGL(ssd::k_generic_fwd, grid, dim3(64), 0, st, prm, (int)s->headdim,
                        (int)s->dstate);
-    if (int rc = launch_status("k_generic_fwd")) return rc;
+    if (int rc = launch_status("k_generic_fwd", tr, st)) return rc;
     return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int mamba2_ssd_fwd(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
+                   void *stream) {
+    return fwd_impl(a, workspace, workspace_bytes, stream, nullptr);
+}
+
+int mamba2_ssd_fwd_traced(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
+                          void *stream, void *const *events, int nevents, const char **names,
+                          int *nkernels) {
+    if (!events || nevents < 2 || !nkernels)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "traced call needs events[>=2] and nkernels");
+    Trace tr;
+    tr.events = events;
+    tr.capacity = nevents;
+    tr.names = names;
+    const int rc = fwd_impl(a, workspace, workspace_bytes, stream, &tr);
+    *nkernels = tr.used > 0 ? tr.used - 1 : 0;
+    return rc;
 }
 
 int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_decay,
