@@ -75,6 +75,8 @@ typedef struct Mamba2SsdFwdArgs {
     const float *D, *z, *dt_bias, *initial_states; /* NULL unless flagged */
     float *out;         /* [B, L, H, P] */
     float *final_state; /* [B, H, P, N] or NULL */
+    float *pre_gate;    /* [B, L, H, P] y + D x before the z gate (written only
+                           with HAS_Z; what the backward needs for dz), or NULL */
 } Mamba2SsdFwdArgs;
 
 typedef struct Mamba2SsdBwdArgs {
@@ -86,6 +88,7 @@ typedef struct Mamba2SsdBwdArgs {
     const float *D, *z, *dt_bias, *initial_states;
     const float *dout;         /* [B, L, H, P]; NULL means zero */
     const float *dfinal_state; /* [B, H, P, N]; NULL means zero */
+    const float *pre_gate;     /* [B, L, H, P] from the forward; required iff HAS_Z */
     float *dx, *ddt, *dA, *dB, *dC;
     float *dD, *dz, *ddt_bias, *dinitial_states; /* required iff the feature is flagged */
 } Mamba2SsdBwdArgs;
@@ -112,9 +115,17 @@ int mamba2_ssd_fwd_traced(const Mamba2SsdFwdArgs *args, void *workspace, size_t 
 int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes);
 
 /* M1 backward: gradients of the forward for the given upstream gradients.
- * Supported: headdim == dstate == 64, fp32 contiguous, any seqlen. */
+ * Supported: headdim == dstate == 64, fp32 contiguous, any seqlen and
+ * chunk_size (the result does not depend on the logical chunk).  dx, ddt, dA,
+ * dB, dC are always written; dD, dz, ddt_bias, dinitial_states when their
+ * feature flag is set.  Deterministic: every reduction runs in a fixed order. */
 int mamba2_ssd_bwd_m1(const Mamba2SsdBwdArgs *args, void *workspace, size_t workspace_bytes,
                       void *stream);
+
+/* Backward with a per-kernel event trace (same contract as mamba2_ssd_fwd_traced). */
+int mamba2_ssd_bwd_m1_traced(const Mamba2SsdBwdArgs *args, void *workspace,
+                             size_t workspace_bytes, void *stream, void *const *events,
+                             int nevents, const char **names, int *nkernels);
 
 /* Inter-chunk state passing, in the reference's stage-op form:
  *   chunk_states [B, H, K, P, N] (read), chunk_log_decay [B, H, K] (sum of dt*A over

@@ -59,6 +59,7 @@ class Mamba2SsdFwdArgs(ctypes.Structure):
         ("D", _c_fp), ("z", _c_fp), ("dt_bias", _c_fp), ("initial_states", _c_fp),
         ("out", _c_fp),
         ("final_state", _c_fp),
+        ("pre_gate", _c_fp),
     ]
 
 
@@ -70,7 +71,7 @@ class Mamba2SsdBwdArgs(ctypes.Structure):
         ("dt_limit_max", ctypes.c_float),
         ("x", _c_fp), ("dt", _c_fp), ("A", _c_fp), ("B", _c_fp), ("C", _c_fp),
         ("D", _c_fp), ("z", _c_fp), ("dt_bias", _c_fp), ("initial_states", _c_fp),
-        ("dout", _c_fp), ("dfinal_state", _c_fp),
+        ("dout", _c_fp), ("dfinal_state", _c_fp), ("pre_gate", _c_fp),
         ("dx", _c_fp), ("ddt", _c_fp), ("dA", _c_fp), ("dB", _c_fp), ("dC", _c_fp),
         ("dD", _c_fp), ("dz", _c_fp), ("ddt_bias", _c_fp), ("dinitial_states", _c_fp),
     ]
@@ -100,6 +101,12 @@ EXPORTS = {
     ),
     "mamba2_ssd_bwd_m1": (
         [ctypes.POINTER(Mamba2SsdBwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "mamba2_ssd_bwd_m1_traced": (
+        [ctypes.POINTER(Mamba2SsdBwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+         ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+         ctypes.POINTER(ctypes.c_int)],
         ctypes.c_int,
     ),
     "mamba2_ssd_state_passing": (

@@ -138,7 +138,9 @@ def _stream(device: torch.device):
 # ----------------------------------------------------------------------------- raw calls
 
 def _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softplus,
-             dt_limit_min, dt_limit_max, want_final=True):
+             dt_limit_min, dt_limit_max, want_final=True, want_pre_gate=False):
+    """Returns (out, final_state or None, pre_gate or None); pre_gate (y + D x
+    before the z gate) is produced only when z is given and it is asked for."""
     lib = rt.load_library()
     shape = _shape(x, B, chunk_size)
     flags = _flags(D, z, dt_bias, initial_states, dt_softplus)
@@ -148,21 +150,22 @@ def _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softp
     out = torch.empty_like(x)
     b, _, h, p = x.shape
     final = torch.empty(b, h, p, B.shape[3], device=x.device, dtype=torch.float32) if want_final else None
+    pre_gate = torch.empty_like(x) if (want_pre_gate and z is not None) else None
     ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=x.device)
     args = rt.Mamba2SsdFwdArgs(
         shape, flags, float(dt_limit_min), _limit(dt_limit_max),
         _ptr(x), _ptr(dt), _ptr(A), _ptr(B), _ptr(C),
         _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(initial_states),
-        _ptr(out), _ptr(final),
+        _ptr(out), _ptr(final), _ptr(pre_gate),
     )
     with torch.cuda.device(x.device):
         rt.check(lib.mamba2_ssd_fwd(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(x.device)),
                  "mamba2_ssd_fwd", lib)
-    return out, final
+    return out, final, pre_gate
 
 
 def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, chunk_size,
-             dt_softplus, dt_limit_min, dt_limit_max):
+             dt_softplus, dt_limit_min, dt_limit_max, pre_gate=None):
     lib = rt.load_library()
     shape = _shape(x, B, chunk_size)
     flags = _flags(D, z, dt_bias, initial_states, dt_softplus)
@@ -183,7 +186,7 @@ def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, 
         shape, flags, float(dt_limit_min), _limit(dt_limit_max),
         _ptr(x), _ptr(dt), _ptr(A), _ptr(B), _ptr(C),
         _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(initial_states),
-        _ptr(dout), _ptr(dfinal_state),
+        _ptr(dout), _ptr(dfinal_state), _ptr(pre_gate),
         _ptr(dx), _ptr(ddt), _ptr(dA), _ptr(dB), _ptr(dC),
         _ptr(dD), _ptr(dz), _ptr(ddt_bias), _ptr(dinit),
     )
@@ -203,7 +206,7 @@ _FWD_SCHEMA = (
 _BWD_SCHEMA = (
     "mamba2_ssd_bwd_m1(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor dout, "
     "Tensor? dfinal_state, Tensor? D, Tensor? z, Tensor? dt_bias, Tensor? initial_states, "
-    "int chunk_size=64, bool dt_softplus=False, float dt_limit_min=0.0, "
+    "Tensor? pre_gate=None, int chunk_size=64, bool dt_softplus=False, float dt_limit_min=0.0, "
     "float dt_limit_max=3.4e38) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
     "Tensor, Tensor)"
 )
@@ -217,8 +220,9 @@ def _op_fwd_cuda(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size=256,
                  dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
     _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
                   dt_limit_min, dt_limit_max)
-    return _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softplus,
-                    dt_limit_min, dt_limit_max)
+    out, final, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
+                             dt_softplus, dt_limit_min, dt_limit_max)
+    return out, final
 
 
 def _op_fwd_meta(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size=256,
@@ -232,7 +236,8 @@ def _empty_like_or_none(t, ref):
 
 
 def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
-                 chunk_size=64, dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
+                 pre_gate=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
+                 dt_limit_max=3.4e38):
     op = "mamba2_ssd_bwd_m1"
     _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
                   dt_limit_min, dt_limit_max)
@@ -243,13 +248,21 @@ def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_stat
         _check_tensor(op, "dfinal_state", dfinal_state)
         if tuple(dfinal_state.shape) != (x.shape[0], x.shape[2], x.shape[3], B.shape[3]):
             raise RuntimeError(f"{op}: dfinal_state must have shape [B,H,P,N]")
+    if z is not None:
+        if pre_gate is None:
+            raise RuntimeError(f"{op}: z needs the forward's pre_gate (y + D x before the gate)")
+        _check_tensor(op, "pre_gate", pre_gate)
+        if pre_gate.shape != x.shape:
+            raise RuntimeError(f"{op}: pre_gate shape must match x")
     grads = _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
-                     chunk_size, dt_softplus, dt_limit_min, dt_limit_max)
+                     chunk_size, dt_softplus, dt_limit_min, dt_limit_max,
+                     pre_gate if z is not None else None)
     return tuple(_empty_like_or_none(g, x) for g in grads)
 
 
 def _op_bwd_meta(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
-                 chunk_size=64, dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
+                 pre_gate=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
+                 dt_limit_max=3.4e38):
     like = lambda t: x.new_empty(0) if t is None else torch.empty_like(t)  # noqa: E731
     return (torch.empty_like(x), torch.empty_like(dt), torch.empty_like(A), torch.empty_like(B),
             torch.empty_like(C), like(D), like(z), like(dt_bias), like(initial_states))
@@ -332,9 +345,14 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus,
                 dt_limit_min, dt_limit_max, initial_states):
-        out, final_state = torch.ops.mamba_ascend.mamba2_ssd_fwd(
+        _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
+                      initial_states, dt_limit_min, dt_limit_max)
+        # the pre-gate output y + D x is saved when z is present (dz needs it),
+        # as the reference's Train forward does (mamba2.py:1682-1770)
+        out, final_state, pre_gate = _fwd_raw(
             x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
-            float(dt_limit_min), float(dt_limit_max))
+            float(dt_limit_min), float(dt_limit_max), want_final=True,
+            want_pre_gate=z is not None)
         empty = x.new_empty(0)
         ctx.save_for_backward(
             x, dt, A, B, C,
@@ -342,6 +360,7 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
             z if z is not None else empty,
             dt_bias if dt_bias is not None else empty,
             initial_states if initial_states is not None else empty,
+            pre_gate if pre_gate is not None else empty,
         )
         ctx.has = (D is not None, z is not None, dt_bias is not None, initial_states is not None)
         ctx.chunk_size = int(chunk_size)
@@ -351,7 +370,7 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, dfinal_state):
-        x, dt, A, B, C, D, z, dt_bias, initial_states = ctx.saved_tensors
+        x, dt, A, B, C, D, z, dt_bias, initial_states, pre_gate = ctx.saved_tensors
         has_D, has_z, has_bias, has_init = ctx.has
         if dout is None:
             dout = torch.zeros_like(x)
@@ -359,8 +378,8 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
             x, dt, A, B, C, dout.contiguous(),
             None if dfinal_state is None else dfinal_state.contiguous(),
             D if has_D else None, z if has_z else None, dt_bias if has_bias else None,
-            initial_states if has_init else None, ctx.chunk_size, ctx.dt_softplus,
-            ctx.dt_limit[0], ctx.dt_limit[1])
+            initial_states if has_init else None, pre_gate if has_z else None,
+            ctx.chunk_size, ctx.dt_softplus, ctx.dt_limit[0], ctx.dt_limit[1])
         dx, ddt, dA, dB, dC, dD, dz, ddt_bias, dinit = grads
         return (dx, ddt, dA, dB, dC, None,
                 dD if has_D else None, dz if has_z else None, ddt_bias if has_bias else None,
@@ -405,7 +424,7 @@ def mamba2_ssd_fwd(
     else:
         _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
                       initial_states, lo, hi)
-        out, final_state = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
+        out, final_state, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
                                     dt_softplus, lo, hi, want_final=return_final_state)
     if return_final_state:
         return out, final_state

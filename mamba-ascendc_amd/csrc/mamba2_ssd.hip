@@ -174,6 +174,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     prm.init = a->initial_states;
     prm.out = a->out;
     prm.final_state = a->final_state;
+    prm.pre_gate = (f & MAMBA2_SSD_HAS_Z) ? a->pre_gate : nullptr;
     prm.L = s->seqlen;
     prm.H = (int)s->nheads;
     prm.G = (int)s->ngroups;
@@ -217,6 +218,160 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     hipLaunchKernelGGL(ssd::k_generic_fwd, grid, dim3(64), 0, st, prm, (int)s->headdim,
                        (int)s->dstate);
     if (int rc = launch_status("k_generic_fwd", tr, st)) return rc;
+    return ok();
+}
+
+// Backward workspace: states [B,H,K,P,N] | log decay [B,H,K] | dstates [B,H,K,P,N]
+// | dA partials [B,H,K] | ddt_bias partials [B,H,K] | dD partials [B,H,K,P].
+struct BwdLayout {
+    size_t states, log_decay, dstates, part_dA, part_db, part_dD, total;
+};
+
+BwdLayout bwd_layout(const Mamba2SsdShape *s) {
+    const size_t bhk = (size_t)s->batch * s->nheads * nchunks(s);
+    const size_t pn = (size_t)s->headdim * s->dstate;
+    BwdLayout l{};
+    size_t off = 0;
+    l.states = off;
+    off += align256(bhk * pn * sizeof(float));
+    l.log_decay = off;
+    off += align256(bhk * sizeof(float));
+    l.dstates = off;
+    off += align256(bhk * pn * sizeof(float));
+    l.part_dA = off;
+    off += align256(bhk * sizeof(float));
+    l.part_db = off;
+    off += align256(bhk * sizeof(float));
+    l.part_dD = off;
+    off += align256(bhk * (size_t)s->headdim * sizeof(float));
+    l.total = off;
+    return l;
+}
+
+bool bwd_supported(const Mamba2SsdShape *s) { return s->headdim == 64 && s->dstate == 64; }
+
+size_t bwd_ws_bytes(const Mamba2SsdShape *s) {
+    if (!bwd_supported(s) || s->seqlen == 0) return 0;
+    return bwd_layout(s).total;
+}
+
+int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes, void *stream,
+             Trace *tr) {
+    if (!a) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "args is NULL");
+    const Mamba2SsdShape *s = &a->shape;
+    if (int rc = check_shape(s, a->flags)) return rc;
+    const uint32_t f = a->flags;
+    if (!a->x || !a->dt || !a->A || !a->B || !a->C)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "x, dt, A, B and C must be non-NULL");
+    if (!a->dx || !a->ddt || !a->dA || !a->dB || !a->dC)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "dx, ddt, dA, dB and dC must be non-NULL");
+    if (bool(f & MAMBA2_SSD_HAS_D) != (a->D != nullptr) ||
+        bool(f & MAMBA2_SSD_HAS_D) != (a->dD != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "D / dD pointers and HAS_D flag disagree");
+    if (bool(f & MAMBA2_SSD_HAS_Z) != (a->z != nullptr) ||
+        bool(f & MAMBA2_SSD_HAS_Z) != (a->dz != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "z / dz pointers and HAS_Z flag disagree");
+    if ((f & MAMBA2_SSD_HAS_Z) && !a->pre_gate)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "HAS_Z needs the forward's pre_gate");
+    if (bool(f & MAMBA2_SSD_HAS_DT_BIAS) != (a->dt_bias != nullptr) ||
+        bool(f & MAMBA2_SSD_HAS_DT_BIAS) != (a->ddt_bias != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "dt_bias / ddt_bias pointers and HAS_DT_BIAS flag disagree");
+    if (bool(f & MAMBA2_SSD_HAS_INITIAL) != (a->initial_states != nullptr) ||
+        bool(f & MAMBA2_SSD_HAS_INITIAL) != (a->dinitial_states != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "initial_states / dinitial_states pointers and HAS_INITIAL flag disagree");
+    if (!(a->dt_limit_min <= a->dt_limit_max))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "dt_limit_min > dt_limit_max");
+    if (!bwd_supported(s))
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
+                    "mamba2_ssd_bwd_m1 needs headdim == dstate == 64 (got %lld, %lld)",
+                    (long long)s->headdim, (long long)s->dstate);
+    if (s->seqlen == 0)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "mamba2_ssd_bwd_m1 needs seqlen > 0");
+    const BwdLayout lay = bwd_layout(s);
+    if (!workspace || workspace_bytes < lay.total)
+        return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", lay.total,
+                    workspace ? workspace_bytes : (size_t)0);
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    const int B = (int)s->batch, H = (int)s->nheads, K = (int)nchunks(s);
+    const int PN = 64 * 64;
+
+    // forward recompute of the chunk-start states
+    ssd::FwdParams fp{};
+    fp.x = a->x;
+    fp.dt = a->dt;
+    fp.A = a->A;
+    fp.B = a->B;
+    fp.C = a->C;
+    fp.dt_bias = a->dt_bias;
+    fp.init = a->initial_states;
+    fp.states = (float *)(ws + lay.states);
+    fp.chunk_log_decay = (float *)(ws + lay.log_decay);
+    fp.L = s->seqlen;
+    fp.H = H;
+    fp.G = (int)s->ngroups;
+    fp.R = (int)(s->nheads / s->ngroups);
+    fp.K = K;
+    fp.softplus = (f & MAMBA2_SSD_DT_SOFTPLUS) != 0;
+    fp.lo = a->dt_limit_min;
+    fp.hi = a->dt_limit_max;
+
+    ssd::BwdParams bp{};
+    bp.x = a->x;
+    bp.dt = a->dt;
+    bp.A = a->A;
+    bp.B = a->B;
+    bp.C = a->C;
+    bp.D = a->D;
+    bp.z = a->z;
+    bp.dt_bias = a->dt_bias;
+    bp.dout = a->dout;
+    bp.pre_gate = a->pre_gate;
+    bp.dx = a->dx;
+    bp.ddt = a->ddt;
+    bp.dB = a->dB;
+    bp.dC = a->dC;
+    bp.dz = a->dz;
+    bp.states = fp.states;
+    bp.log_decay = fp.chunk_log_decay;
+    bp.dstates = (float *)(ws + lay.dstates);
+    bp.part_dA = (float *)(ws + lay.part_dA);
+    bp.part_dbias = (float *)(ws + lay.part_db);
+    bp.part_dD = (float *)(ws + lay.part_dD);
+    bp.L = s->seqlen;
+    bp.H = H;
+    bp.G = fp.G;
+    bp.R = fp.R;
+    bp.K = K;
+    bp.softplus = fp.softplus;
+    bp.has_D = (f & MAMBA2_SSD_HAS_D) != 0;
+    bp.d_per_channel = (f & MAMBA2_SSD_D_PER_CHANNEL) != 0;
+    bp.has_z = (f & MAMBA2_SSD_HAS_Z) != 0;
+    bp.lo = fp.lo;
+    bp.hi = fp.hi;
+
+    const dim3 chunk_grid(K, H, B);
+    const dim3 state_grid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * H);
+    if (int rc = record(tr, st, nullptr)) return rc;
+    hipLaunchKernelGGL((ssd::k_chunk_state<64, 64>), chunk_grid, dim3(ssd::kThreads), 0, st, fp);
+    if (int rc = launch_status("k_chunk_state", tr, st)) return rc;
+    hipLaunchKernelGGL(ssd::k_state_pass, state_grid, dim3(ssd::kThreads), 0, st, fp.states,
+                       fp.chunk_log_decay, fp.init, fp.states, (float *)nullptr, K, PN);
+    if (int rc = launch_status("k_state_pass", tr, st)) return rc;
+    hipLaunchKernelGGL(ssd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);
+    if (int rc = launch_status("k_bwd_dstate", tr, st)) return rc;
+    hipLaunchKernelGGL(ssd::k_state_pass_bwd, state_grid, dim3(ssd::kThreads), 0, st, bp.dstates,
+                       fp.chunk_log_decay, a->dfinal_state, a->dinitial_states, K, PN);
+    if (int rc = launch_status("k_state_pass_bwd", tr, st)) return rc;
+    hipLaunchKernelGGL(ssd::k_bwd_chunk, dim3(K, (unsigned)s->ngroups, B), dim3(ssd::kThreads), 0,
+                       st, bp);
+    if (int rc = launch_status("k_bwd_chunk", tr, st)) return rc;
+    hipLaunchKernelGGL(ssd::k_bwd_finalize, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
+                       bp.part_dbias, bp.part_dD, a->dA, a->ddt_bias, a->dD, B, H, K, 64,
+                       bp.has_D, bp.d_per_channel);
+    if (int rc = launch_status("k_bwd_finalize", tr, st)) return rc;
     return ok();
 }
 
@@ -268,17 +423,27 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
 int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes) {
     if (int rc = check_shape(shape, flags)) return rc;
     if (!bytes) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "bytes is NULL");
-    *bytes = 0;
+    *bytes = bwd_ws_bytes(shape);
     return ok();
 }
 
 int mamba2_ssd_bwd_m1(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
                       void *stream) {
-    (void)a;
-    (void)workspace;
-    (void)workspace_bytes;
-    (void)stream;
-    return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "mamba2_ssd_bwd_m1 is not built yet");
+    return bwd_impl(a, workspace, workspace_bytes, stream, nullptr);
+}
+
+int mamba2_ssd_bwd_m1_traced(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
+                             void *stream, void *const *events, int nevents, const char **names,
+                             int *nkernels) {
+    if (!events || nevents < 2 || !nkernels)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "traced call needs events[>=2] and nkernels");
+    Trace tr;
+    tr.events = events;
+    tr.capacity = nevents;
+    tr.names = names;
+    const int rc = bwd_impl(a, workspace, workspace_bytes, stream, &tr);
+    *nkernels = tr.used > 0 ? tr.used - 1 : 0;
+    return rc;
 }
 
 }  // extern "C"

@@ -115,4 +115,109 @@ __device__ __forceinline__ int perm32(int s) {
     return 8 * ((s & 15) >> 2) + 4 * (s >> 4) + (s & 3);
 }
 
+// Inverse of perm32 over a whole 64-slot row: the token stored at slot `pos`.
+__device__ __forceinline__ int perm_token(int pos) {
+    const int m = pos >> 5, j = (pos >> 3) & 3, i = pos & 7;
+    return 32 * m + (i < 4 ? 4 * j + i : 16 + 4 * j + (i - 4));
+}
+
+// ---------------------------------------------------------------------------
+// 64 x 64 split tiles in LDS.  A tile is two arrays (hi, lo) of 64 rows with a
+// padded row stride of kTS halves; operand reads are 16-byte half8 loads of
+// row r16 at column 32 * ks + 8 * kq, the MFMA operand layout above.
+// ---------------------------------------------------------------------------
+constexpr int kTS = 72;           // row stride (halves): 64 + 8 of padding
+constexpr int kTile = 64 * kTS;   // halves per array
+
+struct SplitTile {
+    _Float16 *hi, *lo;
+};
+
+__device__ __forceinline__ SplitTile tile_at(_Float16 *base, int i) {
+    return SplitTile{base + (2 * i) * kTile, base + (2 * i + 1) * kTile};
+}
+
+// Token-major staging: tile[t][c] = f(t, c4) (a float4 of columns c4..c4+3),
+// for the 64 x 64 tile, using all threads of a 256-thread workgroup.
+template <class F>
+__device__ __forceinline__ void stage_rows(SplitTile d, F f) {
+    for (int i = threadIdx.x; i < 64 * 16; i += 256) {
+        const int t = i >> 4, c4 = (i & 15) * 4;
+        half4 vh, vl;
+        split4(f(t, c4), vh, vl);
+        *(half4 *)&d.hi[t * kTS + c4] = vh;
+        *(half4 *)&d.lo[t * kTS + c4] = vl;
+    }
+}
+
+// Column-major staging: tile[c][slot] = f(t, c) with t = the token of `slot`
+// (perm_token order when PERM, else slot itself).  Thread c = tid % 64 reads
+// one column, so for each token the 64 lanes of a wave read 64 consecutive
+// floats of a row.
+template <bool PERM, class F>
+__device__ __forceinline__ void stage_cols(SplitTile d, F f) {
+    const int c = threadIdx.x & 63, tb = threadIdx.x >> 6;
+#pragma unroll
+    for (int run = tb; run < 8; run += 4) {
+        half8 vh, vl;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int slot = run * 8 + i;
+            const int t = PERM ? perm_token(slot) : slot;
+            _Float16 a, b;
+            split_f16(f(t, c), a, b);
+            vh[i] = a;
+            vl[i] = b;
+        }
+        *(half8 *)&d.hi[c * kTS + run * 8] = vh;
+        *(half8 *)&d.lo[c * kTS + run * 8] = vl;
+    }
+}
+
+// Operand fragment of row `row`, k-step ks (32 columns) from a split tile.
+struct Frag {
+    half8 h, l;
+};
+
+__device__ __forceinline__ Frag frag(SplitTile s, int row, int ks) {
+    const int kq = (threadIdx.x & 63) >> 4;
+    Frag f;
+    f.h = *(const half8 *)&s.hi[row * kTS + ks * 32 + kq * 8];
+    f.l = *(const half8 *)&s.lo[row * kTS + ks * 32 + kq * 8];
+    return f;
+}
+
+__device__ __forceinline__ f32x4 mma3f(Frag a, Frag b, f32x4 c) { return mma3(a.h, a.l, b.h, b.l, c); }
+
+// Pack eight fp32 values into a split operand fragment.
+__device__ __forceinline__ Frag pack_frag(const float (&v)[8]) {
+    Frag f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        _Float16 a, b;
+        split_f16(v[i], a, b);
+        f.h[i] = a;
+        f.l[i] = b;
+    }
+    return f;
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Sum over the 16 lanes that share a lane group (same l / 16).
+__device__ __forceinline__ float sum16(float v) {
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 8, 64);
+    return v;
+}
+
+// Sum over the 4 lanes that share l % 16.
+__device__ __forceinline__ float sum_kq(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 }  // namespace ssd

@@ -24,6 +24,7 @@ constexpr int kThreads = 256; // 4 waves per workgroup
 struct FwdParams {
     const float *x, *dt, *A, *B, *C, *D, *z, *dt_bias, *init;
     float *out, *final_state;
+    float *pre_gate;        // [B, L, H, P] y + D x before the z gate, or NULL
     float *states;          // [B, H, K, P, N]: chunk states, then states at chunk starts
     float *chunk_log_decay; // [B, H, K]
     int64_t L;
@@ -358,6 +359,7 @@ __global__ __launch_bounds__(kThreads) void k_chunk_scan(FwdParams prm) {
                 const float d = prm.d_per_channel ? prm.D[h * P + pc] : prm.D[h];
                 v += d * prm.x[row + pc];
             }
+            if (prm.pre_gate) prm.pre_gate[row + pc] = v;
             if (prm.has_z) v *= silu_f(prm.z[row + pc]);
             prm.out[row + pc] = v;
         }
@@ -400,6 +402,7 @@ __global__ __launch_bounds__(64) void k_generic_fwd(FwdParams prm, int P, int N)
         float y = wave_sum(part);
         if (lane == 0) {
             if (prm.has_D) y += (prm.d_per_channel ? prm.D[h * P + pc] : prm.D[h]) * xv;
+            if (prm.pre_gate) prm.pre_gate[row + pc] = y;
             if (prm.has_z) y *= silu_f(prm.z[row + pc]);
             prm.out[row + pc] = y;
         }

@@ -1,0 +1,142 @@
+"""GPU parity of the HIP M1 backward against autograd of the CPU oracle.
+
+The oracle (oracle/ssd_reference.py, pinned in tests/test_oracle.py against an
+independent float64 adjoint recurrence and finite differences) is run with
+torch autograd on the same seeded inputs.  Small cases use float64 on the CPU
+and a tight relative-L2 bound (the split-fp16 MFMA scheme keeps about 22 bits
+per operand); the BASELINE M1 configuration [4,2048,16,64,64,64,4] uses the
+fp32 oracle, the loss mean(y^2) + mean(final^2), and the contract bound
+rel-L2 <= 5e-3 on every gradient (the reference's own gate is NRMSE <= 8e-3,
+mamba_ascendc/tests/test_mamba2_ssd_bwd_m1.py:161-165).
+"""
+
+import math
+import sys
+
+import pytest
+import torch
+
+from oracle.ssd_reference import bench_seed, make_inputs, parity_metrics, ssd_chunk_scan_ref
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("x", "dt", "A", "B", "C", "D", "z", "dt_bias", "initial_states")
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _grads_gpu(inp, chunk, softplus, limit, gy, gf, mode="both"):
+    import ascend_kernel
+
+    leaves = {k: v.cuda().requires_grad_(True) for k, v in inp.items()}
+    out, fin = ascend_kernel.mamba2_ssd_fwd(
+        leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], chunk,
+        D=leaves.get("D"), z=leaves.get("z"), dt_bias=leaves.get("dt_bias"),
+        dt_softplus=softplus, dt_limit=limit, initial_states=leaves.get("initial_states"),
+        return_final_state=True)
+    loss = 0
+    if mode in ("both", "out"):
+        loss = loss + (out * gy.cuda()).sum()
+    if mode in ("both", "final"):
+        loss = loss + (fin * gf.cuda()).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    return {k: (v.grad.cpu() if v.grad is not None else torch.zeros_like(v).cpu())
+            for k, v in leaves.items()}
+
+
+def _grads_ref(inp, chunk, softplus, limit, gy, gf, dtype, mode="both"):
+    leaves = {k: v.to(dtype).clone().requires_grad_(True) for k, v in inp.items()}
+    out, fin = ssd_chunk_scan_ref(
+        leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], chunk,
+        D=leaves.get("D"), z=leaves.get("z"), dt_bias=leaves.get("dt_bias"),
+        dt_softplus=softplus, dt_limit=limit, initial_states=leaves.get("initial_states"),
+        return_final_state=True, compute_dtype=dtype)
+    loss = 0
+    if mode in ("both", "out"):
+        loss = loss + (out * gy.to(dtype)).sum()
+    if mode in ("both", "final"):
+        loss = loss + (fin * gf.to(dtype)).sum()
+    loss.backward()
+    # an input the selected outputs do not depend on (C for final-only) has no grad
+    return {k: (v.grad if v.grad is not None else torch.zeros_like(v)) for k, v in leaves.items()}
+
+
+CASES = [
+    # shape [B, L, H, P, N, chunk, G], features, softplus, dt_limit, upstream mode
+    ([2, 128, 4, 64, 64, 64, 2], (), True, (0.0, math.inf), "both"),
+    ([1, 200, 4, 64, 64, 64, 1], (), True, (0.0, math.inf), "both"),          # ragged tail
+    ([2, 64, 8, 64, 64, 64, 2], ("D", "z", "bias", "init"), True, (0.0, math.inf), "both"),
+    ([1, 130, 4, 64, 64, 32, 4], ("D2", "z"), False, (0.1, 0.8), "both"),     # clamp, no softplus
+    ([1, 1, 2, 64, 64, 64, 1], ("init",), True, (0.0, math.inf), "both"),     # single token
+    ([2, 192, 4, 64, 64, 64, 2], ("bias",), True, (0.0, math.inf), "out"),    # output-only
+    ([2, 192, 4, 64, 64, 128, 2], ("init",), True, (0.0, math.inf), "final"), # final-only
+    ([1, 320, 16, 64, 64, 64, 2], ("D",), True, (0.0, math.inf), "both"),    # 8 heads per group
+]
+
+
+@pytest.mark.parametrize("shape,features,softplus,limit,mode", CASES,
+                         ids=[f"{c[0]}-{'+'.join(c[1])}-{c[4]}" for c in CASES])
+def test_backward_parity_small(shape, features, softplus, limit, mode):
+    _need_gpu()
+    _say(f"backward parity {shape} {features} {mode}")
+    inp = make_inputs(shape, seed=21, features=features)
+    gen = torch.Generator().manual_seed(5)
+    b, l, h, p, n, chunk, g = shape
+    gy = torch.randn(b, l, h, p, generator=gen)
+    gf = torch.randn(b, h, p, n, generator=gen)
+    got = _grads_gpu(inp, chunk, softplus, limit, gy, gf, mode)
+    want = _grads_ref(inp, chunk, softplus, limit, gy, gf, torch.float64, mode)
+    for k in inp:
+        ma, rl = parity_metrics(got[k], want[k])
+        _say(f"  d{k:<15} maxabs {ma:.3e} relL2 {rl:.3e}")
+        assert torch.isfinite(got[k]).all(), k
+        assert rl <= 2e-4, (k, rl)
+
+
+def test_backward_deterministic():
+    _need_gpu()
+    shape = [2, 256, 8, 64, 64, 64, 2]
+    inp = make_inputs(shape, seed=3, features=("D", "bias"))
+    gen = torch.Generator().manual_seed(6)
+    gy = torch.randn(2, 256, 8, 64, generator=gen)
+    gf = torch.randn(2, 8, 64, 64, generator=gen)
+    a = _grads_gpu(inp, 64, True, (0.0, math.inf), gy, gf)
+    c = _grads_gpu(inp, 64, True, (0.0, math.inf), gy, gf)
+    for k in a:
+        assert torch.equal(a[k], c[k]), k
+
+
+def test_backward_baseline_config4():
+    """BASELINE M1 config [4,2048,16,64,64,64,4], loss mean(y^2) + mean(final^2)."""
+    _need_gpu()
+    import ascend_kernel
+
+    shape = [4, 2048, 16, 64, 64, 64, 4]
+    _say(f"config 4 {shape}")
+    inp = make_inputs(shape, seed=bench_seed(3))
+    leaves = {k: v.cuda().requires_grad_(True) for k, v in inp.items()}
+    out, fin = ascend_kernel.mamba2_ssd_fwd(leaves["x"], leaves["dt"], leaves["A"], leaves["B"],
+                                            leaves["C"], 64, dt_softplus=True,
+                                            return_final_state=True)
+    (out.pow(2).mean() + fin.pow(2).mean()).backward()
+    torch.cuda.synchronize()
+    ref_leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items()}
+    ro, rf = ssd_chunk_scan_ref(ref_leaves["x"], ref_leaves["dt"], ref_leaves["A"], ref_leaves["B"],
+                                ref_leaves["C"], 64, dt_softplus=True, return_final_state=True)
+    (ro.pow(2).mean() + rf.pow(2).mean()).backward()
+    for k in inp:
+        got, want = leaves[k].grad.cpu(), ref_leaves[k].grad
+        ma, rl = parity_metrics(got, want)
+        cos = torch.nn.functional.cosine_similarity(got.double().flatten(), want.double().flatten(), dim=0).item()
+        _say(f"  d{k:<3} maxabs {ma:.3e} relL2 {rl:.3e} cos {cos:.9f}")
+        assert rl <= 5e-3 and ma <= 2e-2, (k, ma, rl)
+        assert cos >= 0.999, (k, cos)
