@@ -130,6 +130,19 @@ def fwd_kernel_model(name: str, shape) -> dict:
     return {"bytes": units * per, "flops": units * fl, "units": units, "bytes_per_unit": per}
 
 
+def measured_traffic(kernel, shape):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary of this configuration (profiles/pmc_traffic_c<cfg>.json), or None."""
+    for cfg, shp in CONFIGS.items():
+        if shp == list(shape):
+            path = os.path.join(ROOT, "profiles", f"pmc_traffic_c{cfg}.json")
+            if os.path.exists(path):
+                with open(path) as fh:
+                    data = json.load(fh)
+                return data.get("traffic_bytes", {}).get(kernel)
+    return None
+
+
 def op_work(shape):
     """Op-level algorithmic work: F = 2*B*L*[G*T*N + H*(T*P + 2*N*P)] and the
     compulsory fp32 public I/O bytes (x, out, dt, A, B, C, final)."""
@@ -204,6 +217,63 @@ def bench_forward(torch, lib, rt, api, hip, inp, shape, steps, warmup):
     res, names, wall = run_traced(torch, lib, rt, hip, call, steps)
     ok = bool(torch.isfinite(out).all()) and bool(torch.isfinite(final).all())
     return res, names, wall, ok, ws.numel()
+
+
+def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup):
+    """fwd + M1 bwd through the C ABI with per-kernel events; upstream
+    gradients of the loss mean(y^2) + mean(final^2).  None if unsupported."""
+    x, dt, A, B, C = (inp[k] for k in ("x", "dt", "A", "B", "C"))
+    b, l, h, p, n, chunk, g = shape
+    shp = rt.Mamba2SsdShape(b, l, h, p, g, n, chunk)
+    flags = rt.DT_SOFTPLUS
+    fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shp), flags, ctypes.byref(fb)), "ws", lib)
+    rt.check(lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(shp), flags, ctypes.byref(bb)), "ws", lib)
+    if p != 64 or n != 64:
+        return None
+    P = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    out = torch.empty_like(x)
+    final = torch.empty(b, h, p, n, device=x.device, dtype=torch.float32)
+    ws = torch.empty(max(1, fb.value, bb.value), dtype=torch.uint8, device=x.device)
+    grads = {k: torch.empty_like(v) for k, v in inp.items()}
+    dout = torch.empty_like(x)
+    dfinal = torch.empty_like(final)
+    fargs = rt.Mamba2SsdFwdArgs(shp, flags, 0.0, math.inf, P(x), P(dt), P(A), P(B), P(C),
+                                None, None, None, None, P(out), P(final), None)
+    bargs = rt.Mamba2SsdBwdArgs(shp, flags, 0.0, math.inf, P(x), P(dt), P(A), P(B), P(C),
+                                None, None, None, None, P(dout), P(dfinal), None,
+                                P(grads["x"]), P(grads["dt"]), P(grads["A"]), P(grads["B"]),
+                                P(grads["C"]), None, None, None, None)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rt.check(lib.mamba2_ssd_fwd(ctypes.byref(fargs), P(ws), ws.numel(), stream), "fwd", lib)
+    torch.mul(out, 2.0 / out.numel(), out=dout)
+    torch.mul(final, 2.0 / final.numel(), out=dfinal)
+
+    def call_f(ev, nev, names, nk):
+        rt.check(lib.mamba2_ssd_fwd_traced(ctypes.byref(fargs), P(ws), ws.numel(), stream,
+                                           ev, nev, names, ctypes.byref(nk)), "fwd", lib)
+
+    def call_b(ev, nev, names, nk):
+        rt.check(lib.mamba2_ssd_bwd_m1_traced(ctypes.byref(bargs), P(ws), ws.numel(), stream,
+                                              ev, nev, names, ctypes.byref(nk)), "bwd", lib)
+
+    run_traced(torch, lib, rt, hip, call_b, warmup)
+    fres, _, _ = run_traced(torch, lib, rt, hip, call_f, steps)
+    bres, bnames, _ = run_traced(torch, lib, rt, hip, call_b, steps)
+    ok = all(bool(torch.isfinite(v).all()) for v in grads.values())
+    return fres, bres, bnames, ok, ws.numel()
+
+
+def copy_calibration(torch, nbytes):
+    """A plain device copy of known size, for scaling the FETCH_SIZE/WRITE_SIZE
+    counters of a rocprofv3 --pmc run (it shows up there as torch's copy kernel)."""
+    src = torch.empty(nbytes // 4, device="cuda", dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return nbytes
 
 
 def bench_api(torch, api, inp, chunk, steps, warmup):
@@ -309,6 +379,72 @@ def cpu_baseline(torch, shape, seed, budget_s):
     }
 
 
+# ----------------------------------------------------------------------------- profiles
+
+def _short(name: str) -> str:
+    """`ssd::k_chunk_scan<64, 64>(...)` -> `k_chunk_scan<64, 64>`."""
+    base = name.split("(")[0].replace("void ", "").strip()
+    return base.replace("ssd::", "")
+
+
+def summarize_profiles(trace_dir, fetch_dir, write_dir, shape, copy_bytes=1 << 30):
+    """Markdown summary of a rocprofv3 kernel-trace (--stats, csv) run and two
+    --pmc runs (FETCH_SIZE, WRITE_SIZE; csv) of `bench.py --copy-calib`.
+
+    Counter scale factors come from the last three dispatches of the runtime's
+    copy kernel, which are the calibration copies of `copy_bytes` each.
+    Returns (markdown, traffic dict keyed by kernel base name)."""
+    import csv
+    import glob
+
+    def one(pattern):
+        files = glob.glob(os.path.join(pattern, "**", "*"), recursive=True)
+        return files
+
+    stats_f = [f for f in one(trace_dir) if f.endswith("kernel_stats.csv")][0]
+    rows = [r for r in csv.DictReader(open(stats_f)) if "ssd::" in r["Name"]]
+    lines = ["| kernel | calls | avg ms | min ms | max ms | share of profiled time |",
+             "|---|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        lines.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e6:.4f} | "
+                     f"{float(r['MinNs']) / 1e6:.4f} | {float(r['MaxNs']) / 1e6:.4f} | "
+                     f"{float(r['Percentage']):.2f} % |")
+    md = ["### Kernel durations (rocprofv3 --kernel-trace --stats)", "", *lines, ""]
+
+    def counters(d):
+        f = [x for x in one(d) if x.endswith("counter_collection.csv")][0]
+        per, copies = {}, []
+        for r in csv.DictReader(open(f)):
+            v = float(r["Counter_Value"])
+            if "ssd::" in r["Kernel_Name"]:
+                per.setdefault(_short(r["Kernel_Name"]), []).append(v)
+            elif "copyBuffer" in r["Kernel_Name"]:
+                copies.append((int(r["Dispatch_Id"]), v))
+        copies.sort()
+        cal = [v for _, v in copies[-3:]]
+        return {k: statistics.fmean(v) for k, v in per.items()}, statistics.fmean(cal)
+
+    fetch, fcal = counters(fetch_dir)
+    write, wcal = counters(write_dir)
+    kib = copy_bytes / 1024
+    fscale, wscale = kib / fcal, kib / wcal
+    traffic = {}
+    md += ["### HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)", "",
+           f"Calibration: a plain {copy_bytes >> 20} MiB device copy reads FETCH_SIZE = {fcal:.0f} KiB "
+           f"and WRITE_SIZE = {wcal:.0f} KiB per dispatch, so the counters are scaled by "
+           f"{fscale:.3f} (fetch) and {wscale:.3f} (write).", "",
+           "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled traffic GB | algorithmic GB (fwd model) |",
+           "|---|---:|---:|---:|---:|"]
+    for k in fetch:
+        t = (fetch[k] * fscale + write.get(k, 0.0) * wscale) * 1024
+        traffic[k.split("<")[0]] = t
+        alg = fwd_kernel_model(k.split("<")[0], shape)["bytes"]
+        alg_s = "" if alg != alg else f"{alg / 1e9:.3f}"
+        md.append(f"| `{k}` | {fetch[k]:.0f} | {write.get(k, 0.0):.0f} | {t / 1e9:.3f} | {alg_s} |")
+    md.append("")
+    return "\n".join(md), traffic
+
+
 # ----------------------------------------------------------------------------- main
 
 def main(argv=None):
@@ -319,9 +455,22 @@ def main(argv=None):
     ap.add_argument("--config", type=int, default=HEADLINE, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--no-bwd", action="store_true", help="skip the fwd+bwd timing")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run 3 plain 1 GiB device copies (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--cpu-budget", type=float, default=20.0,
                     help="approximate seconds of CPU-oracle work for the baseline")
+    ap.add_argument("--summarize-profile", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
+                    help="print a markdown summary of rocprofv3 csv output and exit (no GPU)")
+    ap.add_argument("--traffic-json", help="with --summarize-profile: also write per-kernel traffic")
     args = ap.parse_args(argv)
+
+    if args.summarize_profile:
+        md, traffic = summarize_profiles(*args.summarize_profile, CONFIGS[args.config])
+        print(md)
+        if args.traffic_json:
+            with open(args.traffic_json, "w") as fh:
+                json.dump({"config": CONFIGS[args.config], "traffic_bytes": traffic}, fh, indent=1)
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for --gpus {args.gpus}): the SSD hot path "
@@ -374,11 +523,27 @@ def main(argv=None):
     api_ms = bench_api(torch, api, inp, chunk, max(5, args.steps // 3), 3)
     log(f"public API forward median {api_ms:.4f} ms")
 
-    fwd_bwd_ms, bwd_note = (None, "skipped (--no-bwd)")
+    fwd_bwd_ms, bwd_note, api_fwd_bwd_ms, bwd_kern, bwd_ms = None, "skipped (--no-bwd)", None, {}, None
     if not args.no_bwd:
-        fwd_bwd_ms, bwd_note = bench_fwd_bwd(torch, api, inp, chunk, max(5, args.steps // 3), 3)
-        if fwd_bwd_ms is not None:
-            log(f"fwd+bwd median {fwd_bwd_ms:.4f} ms")
+        tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, args.steps, args.warmup)
+        if tr is None:
+            bwd_note = "M1 backward needs headdim == dstate == 64"
+        else:
+            fres, bres, bnames, bfinite, _ = tr
+            bwd_ms = statistics.median(r[0] for r in bres)
+            fwd_bwd_ms = statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres))
+            bwd_note = f"C-ABI fwd + M1 bwd, loss mean(y^2)+mean(final^2), grads finite={bfinite}"
+            for i, name in enumerate(bnames):
+                durs = [r[1][i] for r in bres]
+                bwd_kern[name] = {"avg_ms": round(statistics.fmean(durs), 6),
+                                  "median_ms": round(statistics.median(durs), 6)}
+                log(f"  bwd {name:<18} avg {bwd_kern[name]['avg_ms']:8.4f} ms")
+            log(f"bwd median {bwd_ms:.4f} ms; fwd+bwd median {fwd_bwd_ms:.4f} ms")
+            api_fwd_bwd_ms, _ = bench_fwd_bwd(torch, api, inp, chunk, max(5, args.steps // 3), 3)
+            log(f"public API (autograd) fwd+bwd median {api_fwd_bwd_ms:.4f} ms")
+    if args.copy_calib:
+        copy_calibration(torch, 1 << 30)
+        log("copy calibration: 3 x 1 GiB device copies")
 
     flops, nbytes = op_work(shape)
     dom = max(kern, key=lambda k: kern[k]["avg_ms"])
@@ -390,7 +555,7 @@ def main(argv=None):
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": d["GB_s"] / HBM_PEAK_GBS,
-        "traffic": None,
+        "traffic": measured_traffic(dom, shape),
     }
     del inp
     torch.cuda.empty_cache()
@@ -421,7 +586,10 @@ def main(argv=None):
             "seed": seed,
         },
         "fwd_bwd_ms": None if fwd_bwd_ms is None else round(fwd_bwd_ms, 5),
+        "bwd_ms": None if bwd_ms is None else round(bwd_ms, 5),
         "fwd_bwd_note": bwd_note,
+        "api_fwd_bwd_ms": None if api_fwd_bwd_ms is None else round(api_fwd_bwd_ms, 5),
+        "bwd_kernels": bwd_kern,
         "api_fwd_ms": round(api_ms, 5),
         "op": {
             "flops": flops,

@@ -126,7 +126,7 @@ def _ptr(t: Optional[torch.Tensor]):
 
 
 def _limit(v: float) -> float:
-    # the schema default 3.4e38 and +inf both mean "no upper clamp"
+    # the schema default 3.402823466e+38 (FLT_MAX) and +inf both mean "no upper clamp"
     v = float(v)
     return math.inf if v >= 3.4e38 else v
 
@@ -199,25 +199,27 @@ def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, 
 # ----------------------------------------------------------------------------- torch ops
 
 _FWD_SCHEMA = (
-    "mamba2_ssd_fwd(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? z, "
-    "Tensor? dt_bias, Tensor? initial_states, int chunk_size=256, bool dt_softplus=False, "
-    "float dt_limit_min=0.0, float dt_limit_max=3.4e38) -> (Tensor, Tensor)"
+    "mamba2_ssd_fwd(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D=None, "
+    "Tensor? z=None, Tensor? dt_bias=None, Tensor? initial_states=None, int chunk_size=256, "
+    "bool dt_softplus=False, float dt_limit_min=0.0, float dt_limit_max=3.402823466e+38) "
+    "-> (Tensor, Tensor)"
 )
 _BWD_SCHEMA = (
     "mamba2_ssd_bwd_m1(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor dout, "
-    "Tensor? dfinal_state, Tensor? D, Tensor? z, Tensor? dt_bias, Tensor? initial_states, "
-    "Tensor? pre_gate=None, int chunk_size=64, bool dt_softplus=False, float dt_limit_min=0.0, "
-    "float dt_limit_max=3.4e38) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
+    "Tensor? dfinal_state=None, Tensor? D=None, Tensor? z=None, Tensor? dt_bias=None, "
+    "Tensor? initial_states=None, Tensor? pre_gate=None, int chunk_size=64, "
+    "bool dt_softplus=False, float dt_limit_min=0.0, float dt_limit_max=3.402823466e+38) "
+    "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
     "Tensor, Tensor)"
 )
 _SP_SCHEMA = (
-    "mamba2_ssd_state_passing(Tensor chunk_states, Tensor dA_cumsum, Tensor? initial_states) "
-    "-> (Tensor, Tensor)"
+    "mamba2_ssd_state_passing(Tensor chunk_states, Tensor dA_cumsum, "
+    "Tensor? initial_states=None) -> (Tensor, Tensor)"
 )
 
 
-def _op_fwd_cuda(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size=256,
-                 dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
+def _op_fwd_cuda(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, chunk_size=256,
+                 dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.402823466e+38):
     _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
                   dt_limit_min, dt_limit_max)
     out, final, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
@@ -225,8 +227,8 @@ def _op_fwd_cuda(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size=256,
     return out, final
 
 
-def _op_fwd_meta(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size=256,
-                 dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.4e38):
+def _op_fwd_meta(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, chunk_size=256,
+                 dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.402823466e+38):
     b, _, h, p = x.shape
     return torch.empty_like(x), x.new_empty(b, h, p, B.shape[3], dtype=torch.float32)
 
@@ -235,9 +237,10 @@ def _empty_like_or_none(t, ref):
     return ref.new_empty(0) if t is None else t
 
 
-def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
+def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bias=None,
+                 initial_states=None,
                  pre_gate=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
-                 dt_limit_max=3.4e38):
+                 dt_limit_max=3.402823466e+38):
     op = "mamba2_ssd_bwd_m1"
     _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
                   dt_limit_min, dt_limit_max)
@@ -260,15 +263,16 @@ def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_stat
     return tuple(_empty_like_or_none(g, x) for g in grads)
 
 
-def _op_bwd_meta(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
+def _op_bwd_meta(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bias=None,
+                 initial_states=None,
                  pre_gate=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
-                 dt_limit_max=3.4e38):
+                 dt_limit_max=3.402823466e+38):
     like = lambda t: x.new_empty(0) if t is None else torch.empty_like(t)  # noqa: E731
     return (torch.empty_like(x), torch.empty_like(dt), torch.empty_like(A), torch.empty_like(B),
             torch.empty_like(C), like(D), like(z), like(dt_bias), like(initial_states))
 
 
-def _op_sp_cuda(chunk_states, dA_cumsum, initial_states):
+def _op_sp_cuda(chunk_states, dA_cumsum, initial_states=None):
     op = "mamba2_ssd_state_passing"
     _check_tensor(op, "chunk_states", chunk_states)
     _check_tensor(op, "dA_cumsum", dA_cumsum)
@@ -292,7 +296,7 @@ def _op_sp_cuda(chunk_states, dA_cumsum, initial_states):
     return states, final
 
 
-def _op_sp_meta(chunk_states, dA_cumsum, initial_states):
+def _op_sp_meta(chunk_states, dA_cumsum, initial_states=None):
     b, h, k, p, n = chunk_states.shape
     return torch.empty_like(chunk_states), chunk_states.new_empty(b, h, p, n)
 
