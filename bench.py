@@ -125,6 +125,14 @@ def fwd_kernel_model(name: str, shape) -> dict:
     elif name == "k_chunk_scan":
         per = f4 * (2 * T * p + T + p * n + 2 * T * n / r)
         fl = 2 * (T * T * n / r + T * T * p + T * n * p)
+    elif name == "k_fwd_seg":
+        # fused: x, dt, B, C in, y out; the state stays on chip (segment
+        # entry/exit states are a few per stream and not counted)
+        per = f4 * (2 * T * p + T + 2 * T * n / r)
+        fl = 2 * (T * T * n / r + T * T * p + 2 * T * n * p)
+    elif name == "k_fwd_seg_state":
+        per = f4 * (T * p + T + T * n / r)
+        fl = 2 * T * p * n
     else:
         per, fl = float("nan"), float("nan")
     return {"bytes": units * per, "flops": units * fl, "units": units, "bytes_per_unit": per}

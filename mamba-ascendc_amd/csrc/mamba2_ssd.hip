@@ -13,6 +13,7 @@
 
 #include "../../include/mamba2_ssd.h"
 #include "ssd_bwd_kernels.h"
+#include "ssd_fwd_fused.h"
 #include "ssd_fwd_kernels.h"
 
 namespace {
@@ -68,11 +69,46 @@ bool fast_path(const Mamba2SsdShape *s) {
 
 int64_t nchunks(const Mamba2SsdShape *s) { return (s->seqlen + ssd::kChunk - 1) / ssd::kChunk; }
 
-size_t fwd_ws_bytes(const Mamba2SsdShape *s) {
-    if (!fast_path(s) || s->seqlen == 0) return 0;
-    const size_t bhk = (size_t)s->batch * s->nheads * nchunks(s);
-    return align256(bhk * s->headdim * s->dstate * sizeof(float)) + align256(bhk * sizeof(float));
+// Forward plan.  headdim = dstate = 64 runs the fused segment-serial kernel:
+// segments are added only when there are fewer than kMinStreams (b, h)
+// streams, so that the grid still has about that many workgroups.  Other
+// MFMA shapes run the three-kernel chunk path.
+constexpr int64_t kMinStreams = 1024;
+
+struct FwdPlan {
+    bool fused = false, chunked = false;
+    int nseg = 1, M = 1;
+    size_t seg_state = 0, seg_decay = 0; // workspace offsets (fused, nseg > 1)
+    size_t ws = 0;
+};
+
+FwdPlan fwd_plan(const Mamba2SsdShape *s) {
+    FwdPlan pl;
+    if (s->seqlen == 0) return pl;
+    const int64_t K = nchunks(s), streams = s->batch * s->nheads;
+    const size_t pn = (size_t)s->headdim * s->dstate;
+    if (s->headdim == 64 && s->dstate == 64) {
+        pl.fused = true;
+        int64_t nseg = streams >= kMinStreams ? 1 : (kMinStreams + streams - 1) / streams;
+        nseg = nseg < K ? nseg : K;
+        const int64_t M = (K + nseg - 1) / nseg;
+        pl.M = (int)M;
+        pl.nseg = (int)((K + M - 1) / M);
+        if (pl.nseg > 1) {
+            const size_t units = (size_t)streams * pl.nseg;
+            pl.seg_state = 0;
+            pl.seg_decay = align256(units * pn * sizeof(float));
+            pl.ws = pl.seg_decay + align256(units * sizeof(float));
+        }
+    } else if (fast_path(s)) {
+        pl.chunked = true;
+        const size_t bhk = (size_t)streams * K;
+        pl.ws = align256(bhk * pn * sizeof(float)) + align256(bhk * sizeof(float));
+    }
+    return pl;
 }
+
+size_t fwd_ws_bytes(const Mamba2SsdShape *s) { return fwd_plan(s).ws; }
 
 // Optional per-kernel event trace: events[0] is recorded before the first
 // kernel and events[i + 1] right after kernel i, all on the launch stream.
@@ -201,7 +237,33 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         }
         return ok();
     }
-    if (fast_path(s)) {
+    const FwdPlan pl = fwd_plan(s);
+    if (pl.fused) {
+        ssd::SegParams sp{};
+        sp.nseg = pl.nseg;
+        sp.M = pl.M;
+        const unsigned units = (unsigned)(s->batch * s->nheads * pl.nseg);
+        if (int rc = record(tr, st, nullptr)) return rc;
+        if (pl.nseg > 1) {
+            sp.seg_state = (float *)((char *)workspace + pl.seg_state);
+            sp.seg_log_decay = (float *)((char *)workspace + pl.seg_decay);
+            hipLaunchKernelGGL(ssd::k_fwd_seg<true>, dim3(units), dim3(ssd::kThreads), 0, st, prm, sp);
+            if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
+            const int PN = 64 * 64;
+            const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
+            hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, sp.seg_state,
+                               sp.seg_log_decay, prm.init, sp.seg_state, prm.final_state, pl.nseg, PN);
+            if (int rc = launch_status("k_state_pass", tr, st)) return rc;
+            sp.seg_in = sp.seg_state;
+            sp.write_final = 0;
+        } else {
+            sp.write_final = 1;
+        }
+        hipLaunchKernelGGL(ssd::k_fwd_seg<false>, dim3(units), dim3(ssd::kThreads), 0, st, prm, sp);
+        if (int rc = launch_status("k_fwd_seg", tr, st)) return rc;
+        return ok();
+    }
+    if (pl.chunked) {
         const size_t bhk = (size_t)s->batch * s->nheads * prm.K;
         prm.states = (float *)workspace;
         prm.chunk_log_decay =

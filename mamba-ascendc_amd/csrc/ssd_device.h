@@ -2,9 +2,9 @@
 //
 // Precision scheme: every contraction runs on the fp16 matrix cores with
 // fp32 accumulation, but each fp32 operand v is carried as an unevaluated sum
-// hi + lo of two fp16 values (hi = fp16(v), lo = fp16(v - hi)), and a product
-// is formed from three MFMAs: hi*hi + hi*lo + lo*hi.  This keeps about 22 bits
-// of operand precision, which is what the fp32 public contract needs (plain
+// hi + lo of two fp16 values (hi = fp16(v), lo = fp16(v - hi), see split2),
+// and a product is formed from three MFMAs: hi*hi + hi*lo + lo*hi.  This keeps
+// about 21 bits of operand precision, which is what the fp32 contract needs (plain
 // fp16 or bf16 operands miss a 2e-2 max-abs bound by one to two orders of
 // magnitude on long sequences with slow decay).
 #pragma once
@@ -38,19 +38,34 @@ __device__ __forceinline__ f32x4 mma3(half8 ah, half8 al, half8 bh, half8 bl, f3
     return c;
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Split two fp32 values into fp16 (hi, lo) pairs with hi + lo ~= v.
+// hi comes from ONE packed conversion (round toward zero) and lo is formed
+// against that very register.  Writing hi = (_Float16)v; lo = v - (float)hi
+// lets the compiler convert v twice (a packed v_cvt_pk_f16_f32 for the stored
+// hi, a scalar v_cvt_f16_f32 for the subtraction); on a rounding tie the two
+// disagree and hi + lo is off by one fp16 ulp.  With hi truncated, |lo| <
+// ulp16(v) and the pair keeps about 21 significant bits.
+__device__ __forceinline__ void split2(float a, float b, half2v &hi, half2v &lo) {
+    hi = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
+    const float ra = a - (float)hi[0], rb = b - (float)hi[1];
+    lo = half2v{(_Float16)ra, (_Float16)rb};
+}
+
 __device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo) {
-    hi = (_Float16)v;
-    lo = (_Float16)(v - (float)hi);
+    half2v h, l;
+    split2(v, 0.f, h, l);
+    hi = h[0];
+    lo = l[0];
 }
 
 __device__ __forceinline__ void split4(float4 v, half4 &hi, half4 &lo) {
-    const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const _Float16 h = (_Float16)vv[i];
-        hi[i] = h;
-        lo[i] = (_Float16)(vv[i] - (float)h);
-    }
+    half2v h0, l0, h1, l1;
+    split2(v.x, v.y, h0, l0);
+    split2(v.z, v.w, h1, l1);
+    hi = half4{h0[0], h0[1], h1[0], h1[1]};
+    lo = half4{l0[0], l0[1], l1[0], l1[1]};
 }
 
 __device__ __forceinline__ float softplus_f(float u) {
@@ -193,16 +208,26 @@ __device__ __forceinline__ f32x4 mma3f(Frag a, Frag b, f32x4 c) { return mma3(a.
 __device__ __forceinline__ Frag pack_frag(const float (&v)[8]) {
     Frag f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        _Float16 a, b;
-        split_f16(v[i], a, b);
-        f.h[i] = a;
-        f.l[i] = b;
+    for (int i = 0; i < 8; i += 2) {
+        half2v h, l;
+        split2(v[i], v[i + 1], h, l);
+        f.h[i] = h[0];
+        f.h[i + 1] = h[1];
+        f.l[i] = l[0];
+        f.l[i + 1] = l[1];
     }
     return f;
 }
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Value of v in lane `lane` (which must be the same for the whole wave).
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// The wave index as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Sum over the 16 lanes that share a lane group (same l / 16).
 __device__ __forceinline__ float sum16(float v) {

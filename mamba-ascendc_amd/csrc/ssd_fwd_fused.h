@@ -1,0 +1,315 @@
+// Fused forward of the Mamba-2 SSD hot path for headdim = dstate = 64.
+//
+// One workgroup owns one (batch b, head h, segment) and walks the segment's
+// 64-token chunks in order, carrying the 64 x 64 state S in registers, so the
+// per-chunk states never go through HBM.  Per chunk (q = discretised dt,
+// cs = chunk-local cumsum of A q, decay_t = exp(cs_last - cs_t)):
+//
+//   y_t = exp(cs_t) C_t . S + sum_{s <= t} (C_t . B_s) exp(cs_t - cs_s) q_s x_s
+//         (+ D x_t, * silu(z_t))
+//   S  <- exp(cs_last) S + sum_t decay_t q_t x_t (x) B_t
+//
+// Long sequences with few (b, h) streams are cut into segments so the grid
+// still fills the GPU: a state-only pass (kStateOnly) computes each
+// segment's state contribution from zero and its total log decay, the
+// inter-segment recurrence (k_state_pass over segments) gives the state
+// entering every segment, and the full pass starts each segment from it.
+// With one segment per stream the full pass alone does everything and needs
+// no workspace.
+//
+// Tiles (split fp16, LDS), for the chunk being processed:
+//   T1 = B [t][n]              (A operand of C.B^T, rows s)
+//   T2 = (q x)^T [p][slot]     (A operand of y^T, B operand of U^T; perm order)
+//   T3 = (decay B)^T [n][slot] (A operand of U^T; perm order)
+//   T4 = S [p][n]              (A operand of the C.S term)
+// and, in registers, C_t for the lane's own token row t = 16 w + l % 16.
+// Outputs are produced transposed (y^T[p][t], U^T[n][p]) so that the C.B^T
+// tiles feed the next product straight from registers (see perm32) and S
+// stays in the accumulator layout of U^T.
+//
+// The math is that of mamba_ascendc/csrc/ops/mamba2_ssd_fwd/design.md:10-20 and
+// the chunked decomposition of mamba_torch/ssd_reference.py:113-189; the
+// fusion, blocking and layouts are this file's own.
+#pragma once
+
+#include "ssd_fwd_kernels.h"
+
+namespace ssd {
+
+struct SegParams {
+    int nseg;              // segments per (b, h) stream
+    int M;                 // chunks per segment (the last one may be shorter)
+    float *seg_state;      // [B, H, nseg, P, N] segment contributions (state-only pass)
+    float *seg_log_decay;  // [B, H, nseg]
+    const float *seg_in;   // [B, H, nseg, P, N] state entering each segment, or NULL
+    int write_final;       // full pass writes final_state (single segment)
+};
+
+constexpr int kXcds = 8; // MI355X: workgroups go round-robin over 8 XCDs
+
+// Workgroup id -> work unit, keeping the R heads of one group on one XCD
+// (consecutive workgroups of an XCD walk the heads of one group, so B and C
+// of a chunk are read from HBM once into that XCD's L2).  Ids past the last
+// full block of kXcds * R map to themselves.
+__device__ __forceinline__ int xcd_unit(int id, int total, int R) {
+    const int span = kXcds * R;
+    const int main = (total / span) * span;
+    if (id >= main) return id;
+    const int x = id % kXcds, n = id / kXcds;
+    return R * ((n / R) * kXcds + x) + n % R;
+}
+
+template <bool kStateOnly>
+__global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams sp) {
+    constexpr int T = 64, P = 64, N = 64;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[8 * kTile];
+    __shared__ float s_cs[T];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int own = 16 * w + r16;
+    const int c = tid & 63; // column handled by this thread when staging
+
+    // unit = ((b * G + g) * nseg + sg) * R + r
+    const int total = (int)(gridDim.x);
+    const int u = xcd_unit(blockIdx.x, total, prm.R);
+    const int r = u % prm.R;
+    const int sg = (u / prm.R) % sp.nseg;
+    const int bg = u / (prm.R * sp.nseg);
+    const int g = bg % prm.G, b = bg / prm.G;
+    const int h = g * prm.R + r;
+    const int H = prm.H, G = prm.G;
+    const int64_t rowHP = (int64_t)H * P, rowGN = (int64_t)G * N;
+    const int kbeg = sg * sp.M, kend = min(kbeg + sp.M, prm.K);
+    const float Ah = prm.A[h];
+    const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
+
+    SplitTile T1 = tile_at(lds, 0), T2 = tile_at(lds, 1), T3 = tile_at(lds, 2), T4 = tile_at(lds, 3);
+
+    // state: Sr[pb][i] = S[p = 16 pb + l % 16][n = 16 w + 4 (l / 16) + i]
+    f32x4 Sr[4];
+    {
+        const float *s0 = nullptr;
+        if (!kStateOnly) {
+            if (sp.seg_in)
+                s0 = sp.seg_in + (((int64_t)b * H + h) * sp.nseg + sg) * (int64_t)(P * N);
+            else if (prm.init)
+                s0 = prm.init + ((int64_t)b * H + h) * (int64_t)(P * N);
+        }
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb) {
+            if (s0) {
+                const float4 v = *(const float4 *)(s0 + (16 * pb + r16) * N + 16 * w + 4 * kq);
+                Sr[pb] = f32x4{v.x, v.y, v.z, v.w};
+            } else {
+                Sr[pb] = zero4();
+            }
+        }
+    }
+    if (!kStateOnly) {
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb) {
+            half4 hh, ll;
+            split4(make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]), hh, ll);
+            *(half4 *)&T4.hi[(16 * pb + r16) * kTS + 16 * w + 4 * kq] = hh;
+            *(half4 *)&T4.lo[(16 * pb + r16) * kTS + 16 * w + 4 * kq] = ll;
+        }
+    }
+
+    // prefetch registers: 16 tokens of column c of x and B (perm order of the
+    // two 8-slot runs w and w + 4), the lane's own row of C, dt of token `lane`
+    float xr[16], br[16], dtr = 0.f;
+    float4 cr[4];
+    auto prefetch = [&](int k) {
+        const int64_t t0 = (int64_t)k * T;
+        const int tv = (int)min((int64_t)T, prm.L - t0);
+        const float *xb = prm.x + (((int64_t)b * prm.L + t0) * H + h) * P + c;
+        const float *bb = prm.B + (((int64_t)b * prm.L + t0) * G + g) * N + c;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int t = perm_token((w + 4 * rr) * 8 + i);
+                xr[rr * 8 + i] = t < tv ? xb[(int64_t)t * rowHP] : 0.f;
+                br[rr * 8 + i] = t < tv ? bb[(int64_t)t * rowGN] : 0.f;
+            }
+        if (!kStateOnly) {
+            const float *cb = prm.C + (((int64_t)b * prm.L + t0 + own) * G + g) * N;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                cr[j] = own < tv ? *(const float4 *)(cb + 32 * (j >> 1) + 8 * kq + 4 * (j & 1))
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        dtr = lane < tv ? prm.dt[((int64_t)b * prm.L + t0 + lane) * H + h] : 0.f;
+    };
+    if (kbeg < kend) prefetch(kbeg);
+
+    float log_decay_sum = 0.f;
+    for (int k = kbeg; k < kend; ++k) {
+        const int64_t t0 = (int64_t)k * T;
+        const int tv = (int)min((int64_t)T, prm.L - t0);
+
+        // ---- staging: discretise (every wave, lane = token), fill T1..T3
+        float q = 0.f, a = 0.f;
+        if (lane < tv) {
+            q = discretize_dt(dtr, bias, prm.softplus != 0, prm.lo, prm.hi);
+            a = Ah * q;
+        }
+        const float cs = wave_inclusive_scan(a);
+        const float cs_last = readlane_f(cs, T - 1);
+        log_decay_sum += cs_last;
+        if (!kStateOnly && w == 0) s_cs[lane] = cs;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int run = w + 4 * rr;
+            float xv[8], dv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int t = perm_token(run * 8 + i);
+                const float bv = br[rr * 8 + i];
+                xv[i] = xr[rr * 8 + i] * readlane_f(q, t);
+                dv[i] = bv * __expf(cs_last - readlane_f(cs, t));
+                if (!kStateOnly) {
+                    _Float16 hh, ll;
+                    split_f16(bv, hh, ll);
+                    T1.hi[t * kTS + c] = hh;
+                    T1.lo[t * kTS + c] = ll;
+                }
+            }
+            const Frag fx = pack_frag(xv), fd = pack_frag(dv);
+            *(half8 *)&T2.hi[c * kTS + run * 8] = fx.h;
+            *(half8 *)&T2.lo[c * kTS + run * 8] = fx.l;
+            *(half8 *)&T3.hi[c * kTS + run * 8] = fd.h;
+            *(half8 *)&T3.lo[c * kTS + run * 8] = fd.l;
+        }
+        Frag Cown[2];
+        if (!kStateOnly) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const float4 v0 = cr[2 * ks], v1 = cr[2 * ks + 1];
+                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                Cown[ks] = pack_frag(vv);
+            }
+        }
+        if (k + 1 < kend) prefetch(k + 1);
+        __syncthreads();
+
+        // ---- output: y^T[p][t] for t = own
+        if (!kStateOnly) {
+            const float cs_own = s_cs[own];
+            Frag WT[2];
+            {
+                float wv[2][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f32x4 cb = zero4();
+                    if (j <= w)
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks)
+                            cb = mma3f(frag(T1, 16 * j + r16, ks), Cown[ks], cb);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int s = 16 * j + 4 * kq + i;
+                        const float e = (j <= w && s <= own) ? __expf(cs_own - s_cs[s]) : 0.f;
+                        wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
+                    }
+                }
+                WT[0] = pack_frag(wv[0]);
+                WT[1] = pack_frag(wv[1]);
+            }
+            f32x4 acc[4];
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) {
+                acc[pb] = zero4();
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    acc[pb] = mma3f(frag(T4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
+            }
+            const float ecs = __expf(cs_own);
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[pb][i] *= ecs;
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+                if (2 * m <= w)
+#pragma unroll
+                    for (int pb = 0; pb < 4; ++pb)
+                        acc[pb] = mma3f(frag(T2, 16 * pb + r16, m), WT[m], acc[pb]);
+            if (own < tv) {
+                const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P;
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) {
+                    const int p = 16 * pb + 4 * kq;
+                    float4 v = make_float4(acc[pb][0], acc[pb][1], acc[pb][2], acc[pb][3]);
+                    if (prm.has_D) {
+                        const float4 xv = *(const float4 *)(prm.x + row + p);
+                        float4 d;
+                        if (prm.d_per_channel)
+                            d = *(const float4 *)(prm.D + h * P + p);
+                        else
+                            d = make_float4(prm.D[h], prm.D[h], prm.D[h], prm.D[h]);
+                        v.x += d.x * xv.x;
+                        v.y += d.y * xv.y;
+                        v.z += d.z * xv.z;
+                        v.w += d.w * xv.w;
+                    }
+                    if (prm.pre_gate) *(float4 *)(prm.pre_gate + row + p) = v;
+                    if (prm.has_z) {
+                        const float4 zv = *(const float4 *)(prm.z + row + p);
+                        v.x *= silu_f(zv.x);
+                        v.y *= silu_f(zv.y);
+                        v.z *= silu_f(zv.z);
+                        v.w *= silu_f(zv.w);
+                    }
+                    *(float4 *)(prm.out + row + p) = v;
+                }
+            }
+        }
+
+        // ---- state update: S <- exp(cs_last) S + U, U^T[n][p] = T3 x T2
+        {
+            f32x4 U[4];
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) U[pb] = zero4();
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const Frag a3 = frag(T3, 16 * w + r16, m);
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag(T2, 16 * pb + r16, m), U[pb]);
+            }
+            const float alpha = __expf(cs_last);
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Sr[pb][i] = alpha * Sr[pb][i] + U[pb][i];
+        }
+        __syncthreads(); // every read of T1..T4 for this chunk is done
+        if (!kStateOnly) {
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) {
+                half4 hh, ll;
+                split4(make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]), hh, ll);
+                *(half4 *)&T4.hi[(16 * pb + r16) * kTS + 16 * w + 4 * kq] = hh;
+                *(half4 *)&T4.lo[(16 * pb + r16) * kTS + 16 * w + 4 * kq] = ll;
+            }
+        }
+    }
+
+    float *dst = nullptr;
+    if (kStateOnly) {
+        const int64_t si = ((int64_t)b * H + h) * sp.nseg + sg;
+        dst = sp.seg_state + si * (int64_t)(P * N);
+        if (tid == 0) sp.seg_log_decay[si] = log_decay_sum;
+    } else if (sp.write_final && prm.final_state) {
+        dst = prm.final_state + ((int64_t)b * H + h) * (int64_t)(P * N);
+    }
+    if (dst) {
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+            *(float4 *)(dst + (16 * pb + r16) * N + 16 * w + 4 * kq) =
+                make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
+    }
+}
+
+}  // namespace ssd

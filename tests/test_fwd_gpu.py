@@ -164,3 +164,30 @@ def test_forward_parity_baseline_configs(cfg_index, shape, batches, groups):
     assert ma <= MAXABS and rl <= RELL2
     assert fma <= MAXABS and frl <= RELL2
     assert torch.isfinite(out).all()
+
+
+def test_split_rounding_ties():
+    """Operands that sit exactly on fp16 rounding ties (x = 1 + odd * 2^-11 with
+    q = 1, A = 0, B = C = 1, so y[t][p] = N * sum_{s<=t} x[s][p] is an exact
+    prefix sum).  The hi/lo split must keep hi + lo == x for every element;
+    a split whose hi and lo come from two differently rounding conversions
+    is off by one fp16 ulp on each tie."""
+    _need_gpu()
+    import ascend_kernel
+
+    for n, chunk in ((64, 64), (128, 128)):
+        b, l, h, p, g = 1, 256, 4, 64, 1
+        k = torch.arange(b * l * h * p, dtype=torch.float64).reshape(b, l, h, p)
+        x = (1.0 + (2 * (k % 512) + 1) * 2.0 ** -11).float()  # every element a tie
+        dt = torch.ones(b, l, h)
+        A = torch.zeros(h)
+        B = torch.ones(b, l, g, n)
+        C = torch.ones(b, l, g, n)
+        out, fin = ascend_kernel.mamba2_ssd_fwd(x.cuda(), dt.cuda(), A.cuda(), B.cuda(), C.cuda(),
+                                                chunk, dt_softplus=False, return_final_state=True)
+        ref = n * x.double().cumsum(1)
+        ref_fin = x.double().sum(1)[..., None].expand(b, h, p, n)
+        ma, rl = parity_metrics(out.cpu(), ref)
+        fma, frl = parity_metrics(fin.cpu(), ref_fin)
+        _say(f"  ties N={n}: out maxabs {ma:.3e} rel {rl:.3e} | final maxabs {fma:.3e} rel {frl:.3e}")
+        assert rl <= 1e-6 and frl <= 1e-6, (n, ma, rl, fma, frl)
