@@ -77,13 +77,29 @@ def test_workspace_size_validation(kw, flags, code):
 
 
 def test_workspace_size_formula():
+    """Forward plan: P = N = 64 runs the fused segment-serial kernel, which
+    needs no workspace when there are >= 1024 (b, h) streams (C3) and a
+    per-segment state buffer otherwise; N = 128 runs the chunk path with a
+    [B,H,K,P,N] state buffer.  The backward needs states, dstates and partials."""
     lib = rt.load_library()
     nbytes = ctypes.c_size_t(0)
-    s = _shape(batch=8, seqlen=4096, nheads=256, ngroups=64)
-    assert lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(s), 0, ctypes.byref(nbytes)) == 0
+
+    def ws(fn, **kw):
+        assert fn(ctypes.byref(_shape(**kw)), 0, ctypes.byref(nbytes)) == 0
+        return nbytes.value
+
+    fwd = lib.mamba2_ssd_fwd_workspace_size
+    assert ws(fwd, batch=8, seqlen=4096, nheads=256, ngroups=64) == 0
+    # 64 streams -> 16 segments of 2 chunks: [B,H,nseg,P,N] + [B,H,nseg]
+    got = ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4)
+    assert got >= 4 * 16 * 16 * 64 * 64 * 4 + 4 * 16 * 16 * 4
+    assert got < 4 * 16 * 32 * 64 * 64 * 4  # never the per-chunk buffer
+    k = 2048 // 64
+    assert ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4, dstate=128) >= 4 * 16 * k * 64 * 128 * 4
+    assert ws(fwd, seqlen=0) == 0
+    bwd = lib.mamba2_ssd_bwd_m1_workspace_size
     k = 4096 // 64
-    # chunk states [B,H,K,P,N] fp32 + per-chunk log decay [B,H,K]
-    assert nbytes.value >= 8 * 256 * k * 64 * 64 * 4 + 8 * 256 * k * 4
+    assert ws(bwd, batch=8, seqlen=4096, nheads=256, ngroups=64) >= 2 * 8 * 256 * k * 64 * 64 * 4
 
 
 def test_fwd_rejects_null_and_flag_mismatch_without_gpu():
