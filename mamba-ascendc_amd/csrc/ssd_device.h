@@ -226,6 +226,37 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every outstanding global load of the wave, which would stall on
+// a prefetch issued just before it; this one leaves such loads in flight.
+// Use it only where the workgroup shares data through LDS alone.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Raw buffer resource over `p` (gfx9 descriptor: no stride, no swizzle,
+// 32-bit data format).  Loads through it take a per-lane byte offset in a
+// VGPR and a wave-uniform byte offset in an SGPR, so a column of a tile
+// costs one VGPR offset instead of a 64-bit address per element.  Range
+// checking is not relied on: callers guard every access themselves.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, 0x7fffffff,
+                                             0x00020000);
+}
+
+// The builtin returns the raw 32 bits (unsigned); reinterpret, do not convert.
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int lane_bytes, int uniform_bytes) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane_bytes, uniform_bytes, 0));
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// 2^v on the transcendental unit (one v_exp_f32, about 1 ulp).
+__device__ __forceinline__ float exp2_f(float v) { return __builtin_amdgcn_exp2f(v); }
+
 // The wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 

@@ -17,6 +17,9 @@
 // With one segment per stream the full pass alone does everything and needs
 // no workspace.
 //
+// Exponentials are taken in the log2 domain: the chunk cumsum is formed over
+// A q log2(e), so every decay factor is a single exp2 of a difference.
+//
 // Tiles (split fp16, LDS), for the chunk being processed:
 //   T1 = B [t][n]              (A operand of C.B^T, rows s)
 //   T2 = (q x)^T [p][slot]     (A operand of y^T, B operand of U^T; perm order)
@@ -60,7 +63,7 @@ __device__ __forceinline__ int xcd_unit(int id, int total, int R) {
 }
 
 template <bool kStateOnly>
-__global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams sp) {
+__global__ __launch_bounds__(kThreads, 2) void k_fwd_seg(FwdParams prm, SegParams sp) {
     constexpr int T = 64, P = 64, N = 64;
     __shared__ __attribute__((aligned(16))) _Float16 lds[8 * kTile];
     __shared__ float s_cs[T];
@@ -81,7 +84,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
     const int H = prm.H, G = prm.G;
     const int64_t rowHP = (int64_t)H * P, rowGN = (int64_t)G * N;
     const int kbeg = sg * sp.M, kend = min(kbeg + sp.M, prm.K);
-    const float Ah = prm.A[h];
+    const float Ah2 = prm.A[h] * kLog2e; // A in log2 units
     const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
 
     SplitTile T1 = tile_at(lds, 0), T2 = tile_at(lds, 1), T3 = tile_at(lds, 2), T4 = tile_at(lds, 3);
@@ -120,18 +123,19 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
     // two 8-slot runs w and w + 4), the lane's own row of C, dt of token `lane`
     float xr[16], br[16], dtr = 0.f;
     float4 cr[4];
+    const int rowHP4 = (int)(rowHP * 4), rowGN4 = (int)(rowGN * 4); // token strides, bytes
     auto prefetch = [&](int k) {
         const int64_t t0 = (int64_t)k * T;
         const int tv = (int)min((int64_t)T, prm.L - t0);
-        const float *xb = prm.x + (((int64_t)b * prm.L + t0) * H + h) * P + c;
-        const float *bb = prm.B + (((int64_t)b * prm.L + t0) * G + g) * N + c;
+        const auto rx = buf_rsrc(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P);
+        const auto rb = buf_rsrc(prm.B + (((int64_t)b * prm.L + t0) * G + g) * N);
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const int t = perm_token((w + 4 * rr) * 8 + i);
-                xr[rr * 8 + i] = t < tv ? xb[(int64_t)t * rowHP] : 0.f;
-                br[rr * 8 + i] = t < tv ? bb[(int64_t)t * rowGN] : 0.f;
+                const int t = perm_token((w + 4 * rr) * 8 + i); // wave-uniform
+                xr[rr * 8 + i] = t < tv ? buf_load(rx, 4 * c, t * rowHP4) : 0.f;
+                br[rr * 8 + i] = t < tv ? buf_load(rb, 4 * c, t * rowGN4) : 0.f;
             }
         if (!kStateOnly) {
             const float *cb = prm.C + (((int64_t)b * prm.L + t0 + own) * G + g) * N;
@@ -153,9 +157,9 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
         float q = 0.f, a = 0.f;
         if (lane < tv) {
             q = discretize_dt(dtr, bias, prm.softplus != 0, prm.lo, prm.hi);
-            a = Ah * q;
+            a = Ah2 * q;
         }
-        const float cs = wave_inclusive_scan(a);
+        const float cs = wave_inclusive_scan(a); // log2 units
         const float cs_last = readlane_f(cs, T - 1);
         log_decay_sum += cs_last;
         if (!kStateOnly && w == 0) s_cs[lane] = cs;
@@ -168,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
                 const int t = perm_token(run * 8 + i);
                 const float bv = br[rr * 8 + i];
                 xv[i] = xr[rr * 8 + i] * readlane_f(q, t);
-                dv[i] = bv * __expf(cs_last - readlane_f(cs, t));
+                dv[i] = bv * exp2_f(cs_last - readlane_f(cs, t));
                 if (!kStateOnly) {
                     _Float16 hh, ll;
                     split_f16(bv, hh, ll);
@@ -192,7 +196,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
             }
         }
         if (k + 1 < kend) prefetch(k + 1);
-        __syncthreads();
+        lds_barrier(); // the prefetch of chunk k + 1 stays in flight
 
         // ---- output: y^T[p][t] for t = own
         if (!kStateOnly) {
@@ -210,7 +214,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int s = 16 * j + 4 * kq + i;
-                        const float e = (j <= w && s <= own) ? __expf(cs_own - s_cs[s]) : 0.f;
+                        const float e = (j <= w && s <= own) ? exp2_f(cs_own - s_cs[s]) : 0.f;
                         wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
                     }
                 }
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
                 for (int ks = 0; ks < 2; ++ks)
                     acc[pb] = mma3f(frag(T4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
             }
-            const float ecs = __expf(cs_own);
+            const float ecs = exp2_f(cs_own);
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
@@ -278,13 +282,13 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
 #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag(T2, 16 * pb + r16, m), U[pb]);
             }
-            const float alpha = __expf(cs_last);
+            const float alpha = exp2_f(cs_last);
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) Sr[pb][i] = alpha * Sr[pb][i] + U[pb][i];
         }
-        __syncthreads(); // every read of T1..T4 for this chunk is done
+        lds_barrier(); // every read of T1..T4 for this chunk is done
         if (!kStateOnly) {
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
@@ -300,7 +304,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_seg(FwdParams prm, SegParams s
     if (kStateOnly) {
         const int64_t si = ((int64_t)b * H + h) * sp.nseg + sg;
         dst = sp.seg_state + si * (int64_t)(P * N);
-        if (tid == 0) sp.seg_log_decay[si] = log_decay_sum;
+        if (tid == 0) sp.seg_log_decay[si] = log_decay_sum * kLn2; // natural units
     } else if (sp.write_final && prm.final_state) {
         dst = prm.final_state + ((int64_t)b * H + h) * (int64_t)(P * N);
     }
