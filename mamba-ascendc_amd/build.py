@@ -24,6 +24,9 @@ FLAGS = [
     "-shared",
     # packed fp32 VALU ops stay off (code generation choice for this target)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results go to ordinary VGPRs: no v_accvgpr_read/write shuffles
+    # between the matrix products and the fp32 epilogue math
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
 ]
 

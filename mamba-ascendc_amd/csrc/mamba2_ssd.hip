@@ -247,7 +247,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         if (pl.nseg > 1) {
             sp.seg_state = (float *)((char *)workspace + pl.seg_state);
             sp.seg_log_decay = (float *)((char *)workspace + pl.seg_decay);
-            hipLaunchKernelGGL(ssd::k_fwd_seg<true>, dim3(units), dim3(ssd::kThreads), 0, st, prm, sp);
+            hipLaunchKernelGGL(ssd::k_fwd_seg<true>, dim3(units), dim3(ssd::kWsThreads), 0, st, prm, sp);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
             const int PN = 64 * 64;
             const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
@@ -259,7 +259,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         } else {
             sp.write_final = 1;
         }
-        hipLaunchKernelGGL(ssd::k_fwd_seg<false>, dim3(units), dim3(ssd::kThreads), 0, st, prm, sp);
+        hipLaunchKernelGGL(ssd::k_fwd_seg<false>, dim3(units), dim3(ssd::kWsThreads), 0, st, prm, sp);
         if (int rc = launch_status("k_fwd_seg", tr, st)) return rc;
         return ok();
     }

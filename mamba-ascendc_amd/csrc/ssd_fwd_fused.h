@@ -35,6 +35,8 @@
 // fusion, blocking and layouts are this file's own.
 #pragma once
 
+#include <type_traits>
+
 #include "ssd_fwd_kernels.h"
 
 namespace ssd {
@@ -62,20 +64,31 @@ __device__ __forceinline__ int xcd_unit(int id, int total, int R) {
     return R * ((n / R) * kXcds + x) + n % R;
 }
 
-template <bool kStateOnly>
-__global__ __launch_bounds__(kThreads, 2) void k_fwd_seg(FwdParams prm, SegParams sp) {
-    constexpr int T = 64, P = 64, N = 64;
-    __shared__ __attribute__((aligned(16))) _Float16 lds[8 * kTile];
-    __shared__ float s_cs[T];
+constexpr int kWsThreads = 512; // 4 producer + 4 consumer waves
 
-    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+template <bool kStateOnly>
+__global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams sp) {
+    constexpr int T = 64, P = 64, N = 64;
+    // stage tiles, double buffered by chunk parity s: full pass T1(s), T2(s),
+    // T3(s) = tiles 3 s .. 3 s + 2 and T4(s) = tile 6 + s; state-only pass
+    // T2(s), T3(s) = tiles 2 s, 2 s + 1
+    constexpr int kTiles = kStateOnly ? 4 : 8;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * kTiles * kTile];
+    __shared__ float s_cs[2][T];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const bool producer = wave >= 4;
+    const int w = wave & 3; // index of the wave within its role
     const int r16 = lane & 15, kq = lane >> 4;
-    const int own = 16 * w + r16;
-    const int c = tid & 63; // column handled by this thread when staging
+    const int c = lane;           // producer: tile column staged by this lane
+
+    auto T1 = [&](int s) { return tile_at(lds, 3 * s); };
+    auto T2 = [&](int s) { return tile_at(lds, kStateOnly ? 2 * s : 3 * s + 1); };
+    auto T3 = [&](int s) { return tile_at(lds, kStateOnly ? 2 * s + 1 : 3 * s + 2); };
+    auto T4 = [&](int s) { return tile_at(lds, 6 + s); };
 
     // unit = ((b * G + g) * nseg + sg) * R + r
-    const int total = (int)(gridDim.x);
-    const int u = xcd_unit(blockIdx.x, total, prm.R);
+    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, prm.R);
     const int r = u % prm.R;
     const int sg = (u / prm.R) % sp.nseg;
     const int bg = u / (prm.R * sp.nseg);
@@ -84,47 +97,19 @@ __global__ __launch_bounds__(kThreads, 2) void k_fwd_seg(FwdParams prm, SegParam
     const int H = prm.H, G = prm.G;
     const int64_t rowHP = (int64_t)H * P, rowGN = (int64_t)G * N;
     const int kbeg = sg * sp.M, kend = min(kbeg + sp.M, prm.K);
-    const float Ah2 = prm.A[h] * kLog2e; // A in log2 units
-    const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
 
-    SplitTile T1 = tile_at(lds, 0), T2 = tile_at(lds, 1), T3 = tile_at(lds, 2), T4 = tile_at(lds, 3);
-
-    // state: Sr[pb][i] = S[p = 16 pb + l % 16][n = 16 w + 4 (l / 16) + i]
-    f32x4 Sr[4];
-    {
-        const float *s0 = nullptr;
-        if (!kStateOnly) {
-            if (sp.seg_in)
-                s0 = sp.seg_in + (((int64_t)b * H + h) * sp.nseg + sg) * (int64_t)(P * N);
-            else if (prm.init)
-                s0 = prm.init + ((int64_t)b * H + h) * (int64_t)(P * N);
-        }
-#pragma unroll
-        for (int pb = 0; pb < 4; ++pb) {
-            if (s0) {
-                const float4 v = *(const float4 *)(s0 + (16 * pb + r16) * N + 16 * w + 4 * kq);
-                Sr[pb] = f32x4{v.x, v.y, v.z, v.w};
-            } else {
-                Sr[pb] = zero4();
-            }
-        }
-    }
-    if (!kStateOnly) {
-#pragma unroll
-        for (int pb = 0; pb < 4; ++pb) {
-            half4 hh, ll;
-            split4(make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]), hh, ll);
-            *(half4 *)&T4.hi[(16 * pb + r16) * kTS + 16 * w + 4 * kq] = hh;
-            *(half4 *)&T4.lo[(16 * pb + r16) * kTS + 16 * w + 4 * kq] = ll;
-        }
-    }
-
-    // prefetch registers: 16 tokens of column c of x and B (perm order of the
-    // two 8-slot runs w and w + 4), the lane's own row of C, dt of token `lane`
-    float xr[16], br[16], dtr = 0.f;
-    float4 cr[4];
+    // ------------------------------------------------------------ producer
+    // A ring of kDepth register slots holds 16 tokens of column c of x and B
+    // (perm order of the runs w, w + 4) and dt of token `lane` for the next
+    // kDepth chunks, so each chunk's loads are issued kDepth iterations
+    // before it is staged.  Slot of chunk k: (k - kbeg) % kDepth.
+    constexpr int kDepth = 3;
+    float xr[kDepth][16], br[kDepth][16], dtr[kDepth];
     const int rowHP4 = (int)(rowHP * 4), rowGN4 = (int)(rowGN * 4); // token strides, bytes
-    auto prefetch = [&](int k) {
+    const float Ah2 = prm.A[h] * kLog2e;                                 // A in log2 units
+    const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
+    auto p_load = [&](int k, auto slot_c) {
+        constexpr int sl = decltype(slot_c)::value;
         const int64_t t0 = (int64_t)k * T;
         const int tv = (int)min((int64_t)T, prm.L - t0);
         const auto rx = buf_rsrc(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P);
@@ -134,35 +119,24 @@ __global__ __launch_bounds__(kThreads, 2) void k_fwd_seg(FwdParams prm, SegParam
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int t = perm_token((w + 4 * rr) * 8 + i); // wave-uniform
-                xr[rr * 8 + i] = t < tv ? buf_load(rx, 4 * c, t * rowHP4) : 0.f;
-                br[rr * 8 + i] = t < tv ? buf_load(rb, 4 * c, t * rowGN4) : 0.f;
+                xr[sl][rr * 8 + i] = t < tv ? buf_load(rx, 4 * c, t * rowHP4) : 0.f;
+                br[sl][rr * 8 + i] = t < tv ? buf_load(rb, 4 * c, t * rowGN4) : 0.f;
             }
-        if (!kStateOnly) {
-            const float *cb = prm.C + (((int64_t)b * prm.L + t0 + own) * G + g) * N;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                cr[j] = own < tv ? *(const float4 *)(cb + 32 * (j >> 1) + 8 * kq + 4 * (j & 1))
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        dtr = lane < tv ? prm.dt[((int64_t)b * prm.L + t0 + lane) * H + h] : 0.f;
+        dtr[sl] = lane < tv ? prm.dt[((int64_t)b * prm.L + t0 + lane) * H + h] : 0.f;
     };
-    if (kbeg < kend) prefetch(kbeg);
-
-    float log_decay_sum = 0.f;
-    for (int k = kbeg; k < kend; ++k) {
-        const int64_t t0 = (int64_t)k * T;
-        const int tv = (int)min((int64_t)T, prm.L - t0);
-
-        // ---- staging: discretise (every wave, lane = token), fill T1..T3
+    // discretise (lane = token), cumsum in log2 units, fill the stage tiles
+    auto p_stage = [&](int k, int s, auto slot_c) {
+        constexpr int sl = decltype(slot_c)::value;
+        const int tv = (int)min((int64_t)T, prm.L - (int64_t)k * T);
         float q = 0.f, a = 0.f;
         if (lane < tv) {
-            q = discretize_dt(dtr, bias, prm.softplus != 0, prm.lo, prm.hi);
+            q = discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
             a = Ah2 * q;
         }
-        const float cs = wave_inclusive_scan(a); // log2 units
+        const float cs = wave_inclusive_scan(a);
         const float cs_last = readlane_f(cs, T - 1);
-        log_decay_sum += cs_last;
-        if (!kStateOnly && w == 0) s_cs[lane] = cs;
+        if (w == 0) s_cs[s][lane] = cs;
+        const SplitTile t1 = T1(s), t2 = T2(s), t3 = T3(s);
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr) {
             const int run = w + 4 * rr;
@@ -170,149 +144,244 @@ __global__ __launch_bounds__(kThreads, 2) void k_fwd_seg(FwdParams prm, SegParam
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int t = perm_token(run * 8 + i);
-                const float bv = br[rr * 8 + i];
-                xv[i] = xr[rr * 8 + i] * readlane_f(q, t);
+                const float bv = br[sl][rr * 8 + i];
+                xv[i] = xr[sl][rr * 8 + i] * readlane_f(q, t);
                 dv[i] = bv * exp2_f(cs_last - readlane_f(cs, t));
                 if (!kStateOnly) {
                     _Float16 hh, ll;
                     split_f16(bv, hh, ll);
-                    T1.hi[t * kTS + c] = hh;
-                    T1.lo[t * kTS + c] = ll;
+                    t1.hi[t * kTS + c] = hh;
+                    t1.lo[t * kTS + c] = ll;
                 }
             }
             const Frag fx = pack_frag(xv), fd = pack_frag(dv);
-            *(half8 *)&T2.hi[c * kTS + run * 8] = fx.h;
-            *(half8 *)&T2.lo[c * kTS + run * 8] = fx.l;
-            *(half8 *)&T3.hi[c * kTS + run * 8] = fd.h;
-            *(half8 *)&T3.lo[c * kTS + run * 8] = fd.l;
+            *(half8 *)&t2.hi[c * kTS + run * 8] = fx.h;
+            *(half8 *)&t2.lo[c * kTS + run * 8] = fx.l;
+            *(half8 *)&t3.hi[c * kTS + run * 8] = fd.h;
+            *(half8 *)&t3.lo[c * kTS + run * 8] = fd.l;
         }
-        Frag Cown[2];
-        if (!kStateOnly) {
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const float4 v0 = cr[2 * ks], v1 = cr[2 * ks + 1];
-                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-                Cown[ks] = pack_frag(vv);
-            }
-        }
-        if (k + 1 < kend) prefetch(k + 1);
-        lds_barrier(); // the prefetch of chunk k + 1 stays in flight
+    };
 
-        // ---- output: y^T[p][t] for t = own
-        if (!kStateOnly) {
-            const float cs_own = s_cs[own];
-            Frag WT[2];
-            {
-                float wv[2][8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    f32x4 cb = zero4();
-                    if (j <= w)
-#pragma unroll
-                        for (int ks = 0; ks < 2; ++ks)
-                            cb = mma3f(frag(T1, 16 * j + r16, ks), Cown[ks], cb);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int s = 16 * j + 4 * kq + i;
-                        const float e = (j <= w && s <= own) ? exp2_f(cs_own - s_cs[s]) : 0.f;
-                        wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
-                    }
-                }
-                WT[0] = pack_frag(wv[0]);
-                WT[1] = pack_frag(wv[1]);
-            }
-            f32x4 acc[4];
-#pragma unroll
-            for (int pb = 0; pb < 4; ++pb) {
-                acc[pb] = zero4();
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    acc[pb] = mma3f(frag(T4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
-            }
-            const float ecs = exp2_f(cs_own);
-#pragma unroll
-            for (int pb = 0; pb < 4; ++pb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[pb][i] *= ecs;
-#pragma unroll
-            for (int m = 0; m < 2; ++m)
-                if (2 * m <= w)
-#pragma unroll
-                    for (int pb = 0; pb < 4; ++pb)
-                        acc[pb] = mma3f(frag(T2, 16 * pb + r16, m), WT[m], acc[pb]);
-            if (own < tv) {
-                const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P;
-#pragma unroll
-                for (int pb = 0; pb < 4; ++pb) {
-                    const int p = 16 * pb + 4 * kq;
-                    float4 v = make_float4(acc[pb][0], acc[pb][1], acc[pb][2], acc[pb][3]);
-                    if (prm.has_D) {
-                        const float4 xv = *(const float4 *)(prm.x + row + p);
-                        float4 d;
-                        if (prm.d_per_channel)
-                            d = *(const float4 *)(prm.D + h * P + p);
-                        else
-                            d = make_float4(prm.D[h], prm.D[h], prm.D[h], prm.D[h]);
-                        v.x += d.x * xv.x;
-                        v.y += d.y * xv.y;
-                        v.z += d.z * xv.z;
-                        v.w += d.w * xv.w;
-                    }
-                    if (prm.pre_gate) *(float4 *)(prm.pre_gate + row + p) = v;
-                    if (prm.has_z) {
-                        const float4 zv = *(const float4 *)(prm.z + row + p);
-                        v.x *= silu_f(zv.x);
-                        v.y *= silu_f(zv.y);
-                        v.z *= silu_f(zv.z);
-                        v.w *= silu_f(zv.w);
-                    }
-                    *(float4 *)(prm.out + row + p) = v;
-                }
-            }
+    // ------------------------------------------------------------ producer role
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    static_assert(kDepth == 3, "the unrolled ring below assumes three slots");
+    // The two roles run separate loops with the same number of barriers (one
+    // after the prologue, one per chunk), so the compiler can give the
+    // producer's load ring and the consumer's state the same registers.
+    if (producer) {
+        if (kbeg < kend) p_load(kbeg, S0{});
+        if (kbeg + 1 < kend) p_load(kbeg + 1, S1{});
+        if (kbeg + 2 < kend) p_load(kbeg + 2, S2{});
+        if (kbeg < kend) {
+            p_stage(kbeg, 0, S0{});
+            if (kbeg + 3 < kend) p_load(kbeg + 3, S0{});
         }
+        lds_barrier();
+        // stage chunk k + 1 into the other buffer while the consumers work
+        // on chunk k; chunk k + 1 sits in slot (k + 1 - kbeg) % 3
+        auto p_iter = [&](int k, auto slot_next) {
+            const int s = (k - kbeg) & 1;
+            if (k + 1 < kend) {
+                p_stage(k + 1, s ^ 1, slot_next);
+                if (k + 1 + kDepth < kend) p_load(k + 1 + kDepth, slot_next);
+            }
+            lds_barrier();
+        };
+        for (int k0 = kbeg; k0 < kend; k0 += kDepth) {
+            p_iter(k0, S1{});
+            if (k0 + 1 < kend) p_iter(k0 + 1, S2{});
+            if (k0 + 2 < kend) p_iter(k0 + 2, S0{});
+        }
+        return;
+    }
 
-        // ---- state update: S <- exp(cs_last) S + U, U^T[n][p] = T3 x T2
-        {
-            f32x4 U[4];
-#pragma unroll
-            for (int pb = 0; pb < 4; ++pb) U[pb] = zero4();
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                const Frag a3 = frag(T3, 16 * w + r16, m);
-#pragma unroll
-                for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag(T2, 16 * pb + r16, m), U[pb]);
-            }
-            const float alpha = exp2_f(cs_last);
-#pragma unroll
-            for (int pb = 0; pb < 4; ++pb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) Sr[pb][i] = alpha * Sr[pb][i] + U[pb][i];
-        }
-        lds_barrier(); // every read of T1..T4 for this chunk is done
-        if (!kStateOnly) {
-#pragma unroll
+    // ------------------------------------------------------------ consumer role
+    // One straight-line copy per consumer wave: with the wave index a
+    // compile-time constant, the causal tile skips are static and the
+    // products of a chunk form one basic block the scheduler can interleave.
+    auto consumer = [&](auto wave_c) {
+        constexpr int W = decltype(wave_c)::value;
+        const int own = 16 * W + r16; // token row of this lane
+        // state: Sr[pb][i] = S[p = 16 pb + l % 16][n = 16 W + 4 (l / 16) + i]
+        f32x4 Sr[4];
+        float4 cr[4]; // C row `own` of the next chunk
+        auto c_load = [&](int k) {
+            const int64_t t0 = (int64_t)k * T;
+            const int tv = (int)min((int64_t)T, prm.L - t0);
+            const float *cb = prm.C + (((int64_t)b * prm.L + t0 + own) * G + g) * N;
+    #pragma unroll
+            for (int j = 0; j < 4; ++j)
+                cr[j] = own < tv ? *(const float4 *)(cb + 32 * (j >> 1) + 8 * kq + 4 * (j & 1))
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        };
+        auto write_T4 = [&](int s) {
+            const SplitTile t4 = T4(s);
+    #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
                 half4 hh, ll;
                 split4(make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]), hh, ll);
-                *(half4 *)&T4.hi[(16 * pb + r16) * kTS + 16 * w + 4 * kq] = hh;
-                *(half4 *)&T4.lo[(16 * pb + r16) * kTS + 16 * w + 4 * kq] = ll;
+                *(half4 *)&t4.hi[(16 * pb + r16) * kTS + 16 * W + 4 * kq] = hh;
+                *(half4 *)&t4.lo[(16 * pb + r16) * kTS + 16 * W + 4 * kq] = ll;
+            }
+        };
+
+        {
+            const float *s0 = nullptr;
+            if (!kStateOnly) {
+                if (sp.seg_in)
+                    s0 = sp.seg_in + (((int64_t)b * H + h) * sp.nseg + sg) * (int64_t)(P * N);
+                else if (prm.init)
+                    s0 = prm.init + ((int64_t)b * H + h) * (int64_t)(P * N);
+            }
+    #pragma unroll
+            for (int pb = 0; pb < 4; ++pb) {
+                if (s0) {
+                    const float4 v = *(const float4 *)(s0 + (16 * pb + r16) * N + 16 * W + 4 * kq);
+                    Sr[pb] = f32x4{v.x, v.y, v.z, v.w};
+                } else {
+                    Sr[pb] = zero4();
+                }
+            }
+            if (!kStateOnly) {
+                write_T4(0);
+                if (kbeg < kend) c_load(kbeg);
             }
         }
-    }
+        lds_barrier();
 
-    float *dst = nullptr;
-    if (kStateOnly) {
-        const int64_t si = ((int64_t)b * H + h) * sp.nseg + sg;
-        dst = sp.seg_state + si * (int64_t)(P * N);
-        if (tid == 0) sp.seg_log_decay[si] = log_decay_sum * kLn2; // natural units
-    } else if (sp.write_final && prm.final_state) {
-        dst = prm.final_state + ((int64_t)b * H + h) * (int64_t)(P * N);
-    }
-    if (dst) {
-#pragma unroll
-        for (int pb = 0; pb < 4; ++pb)
-            *(float4 *)(dst + (16 * pb + r16) * N + 16 * w + 4 * kq) =
-                make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
+        float log_decay_sum = 0.f;
+        for (int k = kbeg; k < kend; ++k) {
+            const int s = (k - kbeg) & 1;
+            const int64_t t0 = (int64_t)k * T;
+            const int tv = (int)min((int64_t)T, prm.L - t0);
+            const float cs_last = s_cs[s][T - 1];
+            log_decay_sum += cs_last;
+            const SplitTile t2 = T2(s), t3 = T3(s);
+            if (!kStateOnly) {
+                Frag Cown[2];
+    #pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const float4 v0 = cr[2 * ks], v1 = cr[2 * ks + 1];
+                    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                    Cown[ks] = pack_frag(vv);
+                }
+                if (k + 1 < kend) c_load(k + 1);
+                const SplitTile t1 = T1(s), t4 = T4(s);
+                const float cs_own = s_cs[s][own];
+                // W^T tiles: C_t . B_s exp2(cs_t - cs_s), s <= t, t = own
+                Frag WT[2];
+                {
+                    float wv[2][8];
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        f32x4 cb = zero4();
+                        if (j <= W)
+    #pragma unroll
+                            for (int ks = 0; ks < 2; ++ks)
+                                cb = mma3f(frag(t1, 16 * j + r16, ks), Cown[ks], cb);
+    #pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int so = 16 * j + 4 * kq + i;
+                            const float e = (j <= W && so <= own) ? exp2_f(cs_own - s_cs[s][so]) : 0.f;
+                            wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
+                        }
+                    }
+                    WT[0] = pack_frag(wv[0]);
+                    WT[1] = pack_frag(wv[1]);
+                }
+                // y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] (q x)_s
+                f32x4 acc[4];
+    #pragma unroll
+                for (int pb = 0; pb < 4; ++pb) {
+                    acc[pb] = zero4();
+    #pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        acc[pb] = mma3f(frag(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
+                }
+                const float ecs = exp2_f(cs_own);
+    #pragma unroll
+                for (int pb = 0; pb < 4; ++pb)
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[pb][i] *= ecs;
+    #pragma unroll
+                for (int m = 0; m < 2; ++m)
+                    if (2 * m <= W)
+    #pragma unroll
+                        for (int pb = 0; pb < 4; ++pb)
+                            acc[pb] = mma3f(frag(t2, 16 * pb + r16, m), WT[m], acc[pb]);
+                if (own < tv) {
+                    const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P;
+    #pragma unroll
+                    for (int pb = 0; pb < 4; ++pb) {
+                        const int p = 16 * pb + 4 * kq;
+                        float4 v = make_float4(acc[pb][0], acc[pb][1], acc[pb][2], acc[pb][3]);
+                        if (prm.has_D) {
+                            const float4 xv = *(const float4 *)(prm.x + row + p);
+                            float4 d;
+                            if (prm.d_per_channel)
+                                d = *(const float4 *)(prm.D + h * P + p);
+                            else
+                                d = make_float4(prm.D[h], prm.D[h], prm.D[h], prm.D[h]);
+                            v.x += d.x * xv.x;
+                            v.y += d.y * xv.y;
+                            v.z += d.z * xv.z;
+                            v.w += d.w * xv.w;
+                        }
+                        if (prm.pre_gate) *(float4 *)(prm.pre_gate + row + p) = v;
+                        if (prm.has_z) {
+                            const float4 zv = *(const float4 *)(prm.z + row + p);
+                            v.x *= silu_f(zv.x);
+                            v.y *= silu_f(zv.y);
+                            v.z *= silu_f(zv.z);
+                            v.w *= silu_f(zv.w);
+                        }
+                        *(float4 *)(prm.out + row + p) = v;
+                    }
+                }
+            }
+            // S <- exp2(cs_last) S + U, U^T[n][p] = T3 x T2
+            {
+                f32x4 U[4];
+    #pragma unroll
+                for (int pb = 0; pb < 4; ++pb) U[pb] = zero4();
+    #pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const Frag a3 = frag(t3, 16 * W + r16, m);
+    #pragma unroll
+                    for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag(t2, 16 * pb + r16, m), U[pb]);
+                }
+                const float alpha = exp2_f(cs_last);
+    #pragma unroll
+                for (int pb = 0; pb < 4; ++pb)
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i) Sr[pb][i] = alpha * Sr[pb][i] + U[pb][i];
+            }
+            if (!kStateOnly) write_T4(s ^ 1);
+            lds_barrier(); // buffer s is free, buffer s ^ 1 and T4(s ^ 1) are complete
+        }
+
+        float *dst = nullptr;
+        if (kStateOnly) {
+            const int64_t si = ((int64_t)b * H + h) * sp.nseg + sg;
+            dst = sp.seg_state + si * (int64_t)(P * N);
+            if (tid == 0) sp.seg_log_decay[si] = log_decay_sum * kLn2; // natural units
+        } else if (sp.write_final && prm.final_state) {
+            dst = prm.final_state + ((int64_t)b * H + h) * (int64_t)(P * N);
+        }
+        if (dst) {
+    #pragma unroll
+            for (int pb = 0; pb < 4; ++pb)
+                *(float4 *)(dst + (16 * pb + r16) * N + 16 * W + 4 * kq) =
+                    make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
+        }
+    };
+    switch (w) {
+    case 0: consumer(std::integral_constant<int, 0>{}); break;
+    case 1: consumer(std::integral_constant<int, 1>{}); break;
+    case 2: consumer(std::integral_constant<int, 2>{}); break;
+    default: consumer(std::integral_constant<int, 3>{}); break;
     }
 }
 
