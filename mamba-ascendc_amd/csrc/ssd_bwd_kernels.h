@@ -166,37 +166,74 @@ __global__ __launch_bounds__(kThreads) void k_state_pass_bwd(float *ds, const fl
 // --------------------------------------------------------------------------
 // chunk backward, one workgroup per (k, g, b), heads of the group in order
 // --------------------------------------------------------------------------
+// C_t . B_s is formed once per (b, g, k) into an fp32 LDS tile and read back
+// per head in both orientations; global tiles are read through buffer
+// resources (per-lane VGPR offset + wave-uniform SGPR offset); every barrier
+// orders LDS only (the kernel shares nothing else between waves).  Exponents
+// are taken in the log2 domain (cs2 = cumsum of A q log2(e)).
 __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
-    constexpr int T = 64, P = 64, N = 64;
+    constexpr int T = 64, P = 64, N = 64, CBS = 68; // CBS: fp32 row stride of s_cb
     __shared__ __attribute__((aligned(16))) _Float16 lds[6 * kTile]; // three split tiles
+    __shared__ __attribute__((aligned(16))) float s_cb[T * CBS];   // C_t . B_s at [t][s], s-block <= t-block
     __shared__ float s_q[T], s_cs[T], s_dqdu[T], s_dte[T], s_ecs[T];
     __shared__ float s_dcs1[T], s_goff[T], s_rdte[T], s_da[T], s_ddt[T];
     __shared__ float s_red[4], s_dD[4][P];
 
     const int k = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int r16 = lane & 15, kq = lane >> 4;
     const int own = 16 * w + r16; // operand row owned by this lane
+    const int c = lane;           // staged column of this lane
     const int64_t t0 = (int64_t)k * T;
     const int tv = (int)min((int64_t)T, prm.L - t0);
+    const bool full = tv == T;
     const int H = prm.H, G = prm.G;
-    const int64_t rowHP = (int64_t)H * P, rowGN = (int64_t)G * N;
-    const float *Bg = prm.B + (((int64_t)b * prm.L + t0) * G + g) * N;
-    const float *Cg = prm.C + (((int64_t)b * prm.L + t0) * G + g) * N;
+    const int rowHP4 = H * P * 4, rowGN4 = G * N * 4; // token strides, bytes
+    const auto rB = buf_rsrc(prm.B + (((int64_t)b * prm.L + t0) * G + g) * N);
+    const auto rC = buf_rsrc(prm.C + (((int64_t)b * prm.L + t0) * G + g) * N);
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
 
     SplitTile tA = tile_at(lds, 0), tB = tile_at(lds, 1), tC = tile_at(lds, 2);
 
-    // ---- group prologue: C.B^T in both orientations (kept in registers)
-    stage_rows(tA, [&](int t, int c4) {
-        return t < tv ? *(const float4 *)(Bg + (int64_t)t * rowGN + c4) : z4;
-    });
-    stage_rows(tB, [&](int t, int c4) {
-        return t < tv ? *(const float4 *)(Cg + (int64_t)t * rowGN + c4) : z4;
-    });
-    __syncthreads();
+    // token-major staging of a 64 x 64 tile: lane (tid / 16, tid % 16) reads
+    // float4 rows tid / 16 + 16 j; f maps (value, token, column) -> value
+    const int rt = tid >> 4, rc4 = (tid & 15) * 4;
+    auto stage_rows_buf = [&](SplitTile d, __amdgpu_buffer_rsrc_t r, int row4, auto f) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = rt + 16 * j;
+            float4 v = (full || t < tv) ? buf_load4(r, rt * row4 + rc4 * 4, 16 * j * row4) : z4;
+            v = f(v, t, rc4);
+            half4 vh, vl;
+            split4(v, vh, vl);
+            *(half4 *)&d.hi[t * kTS + rc4] = vh;
+            *(half4 *)&d.lo[t * kTS + rc4] = vl;
+        }
+    };
+    // column staging in perm order: tile[c][slot] = f(value of token(slot), token)
+    auto stage_cols_buf = [&](SplitTile d, __amdgpu_buffer_rsrc_t r, int row4, auto f) {
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int run = w + 4 * rr;
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int t = perm_token(run * 8 + i); // wave-uniform
+                v[i] = t < tv ? f(buf_load(r, 4 * c + t * row4, 0), t) : 0.f;
+            }
+            const Frag fr = pack_frag(v);
+            *(half8 *)&d.hi[c * kTS + run * 8] = fr.h;
+            *(half8 *)&d.lo[c * kTS + run * 8] = fr.l;
+        }
+    };
+    auto ident4 = [](float4 v, int, int) { return v; };
+    auto ident1 = [](float v, int) { return v; };
+
+    // ---- group prologue: C.B^T into s_cb, B own-row operand
+    stage_rows_buf(tA, rB, rowGN4, ident4);
+    stage_rows_buf(tB, rC, rowGN4, ident4);
+    lds_barrier();
     Frag Bown[2];
-    f32x4 cbT[4], cbS[4];
     {
         Frag Cown[2];
 #pragma unroll
@@ -204,16 +241,13 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
             Bown[ks] = frag(tA, own, ks);
             Cown[ks] = frag(tB, own, ks);
         }
+        // rows t = 16 w + 4 kq + i, columns s = 16 j + r16, for s-blocks j <= w
+        for (int j = 0; j <= w; ++j) {
+            f32x4 cb = zero4();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            cbT[j] = zero4();
-            cbS[j] = zero4();
-            if (j <= w) // cbT[j][r] = C_t . B_s, t = own, s = 16 j + 4 kq + r
+            for (int ks = 0; ks < 2; ++ks) cb = mma3f(Cown[ks], frag(tA, 16 * j + r16, ks), cb);
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) cbT[j] = mma3f(frag(tA, 16 * j + r16, ks), Cown[ks], cbT[j]);
-            if (j >= w) // cbS[j][r] = C_t . B_s, s = own, t = 16 j + 4 kq + r
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) cbS[j] = mma3f(frag(tB, 16 * j + r16, ks), Bown[ks], cbS[j]);
+            for (int i = 0; i < 4; ++i) s_cb[(16 * w + 4 * kq + i) * CBS + 16 * j + r16] = cb[i];
         }
     }
     f32x4 dBa[4], dCa[4];
@@ -222,36 +256,41 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
         dBa[i] = zero4();
         dCa[i] = zero4();
     }
+    const float bias0 = 0.f;
+    (void)bias0;
 
     for (int rh = 0; rh < prm.R; ++rh) {
         const int h = g * prm.R + rh;
-        __syncthreads(); // previous readers of the tiles and per-token arrays are done
+        lds_barrier(); // previous readers of the tiles and per-token arrays are done
         if (w == 0) {
-            const float cs = bwd_prologue(prm, b, h, t0, tv, s_q, s_cs, s_dqdu);
-            const float last = __shfl(cs, T - 1, 64);
-            s_dte[lane] = __expf(last - cs);
-            s_ecs[lane] = __expf(cs);
+            float q = 0.f, a = 0.f, dq = 0.f;
+            if (lane < tv) {
+                const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
+                const float dtv = prm.dt[((int64_t)b * prm.L + t0 + lane) * H + h];
+                q = discretize_dt(dtv, bias, prm.softplus != 0, prm.lo, prm.hi);
+                dq = discretize_grad(dtv, bias, prm.softplus != 0, prm.lo, prm.hi);
+                a = prm.A[h] * kLog2e * q;
+            }
+            const float cs = wave_inclusive_scan(a); // log2 units
+            const float last = readlane_f(cs, T - 1);
+            s_q[lane] = q;
+            s_cs[lane] = cs;
+            s_dqdu[lane] = dq;
+            s_dte[lane] = exp2_f(last - cs);
+            s_ecs[lane] = exp2_f(cs);
         }
-        __syncthreads();
+        lds_barrier();
         const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
-        const float *xh = prm.x + xo;
-        const float *doh = prm.dout ? prm.dout + xo : nullptr;
-        const float *zh = prm.has_z ? prm.z + xo : nullptr;
-        auto gy1 = [&](int t, int c) -> float {
-            if (t >= tv || !doh) return 0.f;
-            const int64_t o = (int64_t)t * rowHP + c;
-            float v = doh[o];
-            if (zh) v *= silu_f(zh[o]);
-            return v;
-        };
+        const auto rX = buf_rsrc(prm.x + xo);
+        const bool has_dout = prm.dout != nullptr;
+        const auto rDo = buf_rsrc(has_dout ? prm.dout + xo : prm.x + xo);
+        const auto rZ = buf_rsrc(prm.has_z ? prm.z + xo : prm.x + xo);
 
         // ---- phase 1: dW in both orientations, W and the decay masks
-        stage_rows(tA, [&](int t, int c4) {
-            if (t >= tv || !doh) return z4;
-            const int64_t o = (int64_t)t * rowHP + c4;
-            float4 v = *(const float4 *)(doh + o);
-            if (zh) {
-                const float4 zz = *(const float4 *)(zh + o);
+        stage_rows_buf(tA, rDo, rowHP4, [&](float4 v, int t, int c4) {
+            if (!has_dout) return z4;
+            if (prm.has_z) {
+                const float4 zz = (full || t < tv) ? buf_load4(rZ, rt * rowHP4 + c4 * 4, (t - rt) * rowHP4) : z4;
                 v.x *= silu_f(zz.x);
                 v.y *= silu_f(zz.y);
                 v.z *= silu_f(zz.z);
@@ -259,13 +298,11 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
             }
             return v;
         });
-        stage_rows(tB, [&](int t, int c4) {
-            if (t >= tv) return z4;
-            float4 v = *(const float4 *)(xh + (int64_t)t * rowHP + c4);
+        stage_rows_buf(tB, rX, rowHP4, [&](float4 v, int t, int) {
             const float q = s_q[t];
             return make_float4(v.x * q, v.y * q, v.z * q, v.w * q);
         });
-        __syncthreads();
+        lds_barrier();
         Frag GYo[2], XDo[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -274,55 +311,75 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
         }
         Frag WS[2], DCT[2], DCS[2];
         {
-            f32x4 dwT[4], dwS[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                dwT[j] = zero4();
-                dwS[j] = zero4();
-                if (j <= w) // dwT[j][r] = gy_t . xdt_s, t = own, s = 16 j + 4 kq + r
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) dwT[j] = mma3f(frag(tB, 16 * j + r16, ks), GYo[ks], dwT[j]);
-                if (j >= w) // dwS[j][r] = gy_t . xdt_s, s = own, t = 16 j + 4 kq + r
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) dwS[j] = mma3f(frag(tA, 16 * j + r16, ks), XDo[ks], dwS[j]);
-            }
             const float cs_own = s_cs[own];
-            float rows = 0.f, cols = 0.f;
-            float ws[2][8], dct[2][8], dcs_[2][8];
+            // T orientation (t = own, s = 16 j + 4 kq + i, s-blocks j <= w):
+            // dW[t][s], then dCB = dW * exp2(cs_t - cs_s) and rowsum(dW o W)
+            float rows = 0.f;
+            {
+                float dct[2][8];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 4; ++j) {
+                    f32x4 dw = zero4();
+                    float4 cb = z4;
+                    if (j <= w) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int u = 16 * j + 4 * kq + r; // the other token of the pair
-                    const int slot = (j & 1) * 4 + r;
-                    // T orientation: t = own, s = u
-                    const float eT = (j <= w && u <= own) ? __expf(cs_own - s_cs[u]) : 0.f;
-                    rows += dwT[j][r] * cbT[j][r] * eT;
-                    dct[j >> 1][slot] = dwT[j][r] * eT;
-                    // S orientation: s = own, t = u
-                    const float eS = (j >= w && own <= u) ? __expf(s_cs[u] - cs_own) : 0.f;
-                    const float wsv = cbS[j][r] * eS;
-                    cols += dwS[j][r] * wsv;
-                    ws[j >> 1][slot] = wsv;
-                    dcs_[j >> 1][slot] = dwS[j][r] * eS;
+                        for (int ks = 0; ks < 2; ++ks) dw = mma3f(frag(tB, 16 * j + r16, ks), GYo[ks], dw);
+                        cb = *(const float4 *)&s_cb[own * CBS + 16 * j + 4 * kq];
+                    }
+                    const float cbv[4] = {cb.x, cb.y, cb.z, cb.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int u = 16 * j + 4 * kq + i;
+                        const float e = (j <= w && u <= own) ? exp2_f(cs_own - s_cs[u]) : 0.f;
+                        rows += dw[i] * cbv[i] * e;
+                        dct[j >> 1][(j & 1) * 4 + i] = dw[i] * e;
+                    }
                 }
+                DCT[0] = pack_frag(dct[0]);
+                DCT[1] = pack_frag(dct[1]);
+            }
+            // S orientation (s = own, t = 16 j + 4 kq + i, t-blocks j >= w):
+            // W[t][s], dCB, colsum(dW o W)
+            float cols = 0.f;
+            {
+                float ws[2][8], dcs_[2][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f32x4 dw = zero4();
+                    if (j >= w)
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) dw = mma3f(frag(tA, 16 * j + r16, ks), XDo[ks], dw);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int u = 16 * j + 4 * kq + i;
+                        const float cbS = j >= w ? s_cb[u * CBS + own] : 0.f;
+                        const float e = (j >= w && own <= u) ? exp2_f(s_cs[u] - cs_own) : 0.f;
+                        const float wsv = cbS * e;
+                        cols += dw[i] * wsv;
+                        ws[j >> 1][(j & 1) * 4 + i] = wsv;
+                        dcs_[j >> 1][(j & 1) * 4 + i] = dw[i] * e;
+                    }
+                }
+                WS[0] = pack_frag(ws[0]);
+                WS[1] = pack_frag(ws[1]);
+                DCS[0] = pack_frag(dcs_[0]);
+                DCS[1] = pack_frag(dcs_[1]);
+            }
             rows = sum_kq(rows);
             cols = sum_kq(cols);
             if (kq == 0) s_dcs1[own] = rows - cols;
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                WS[m] = pack_frag(ws[m]);
-                DCT[m] = pack_frag(dct[m]);
-                DCS[m] = pack_frag(dcs_[m]);
-            }
         }
-        __syncthreads(); // phase-1 tiles consumed
+        lds_barrier(); // phase-1 tiles consumed
 
         // ---- phase 2a: the token-contracted products
-        stage_cols<true>(tA, gy1);
-        stage_cols<true>(tB, [&](int t, int c) { return t < tv ? Bg[(int64_t)t * rowGN + c] : 0.f; });
-        stage_cols<true>(tC, [&](int t, int c) { return t < tv ? Cg[(int64_t)t * rowGN + c] : 0.f; });
-        __syncthreads();
+        stage_cols_buf(tA, rDo, rowHP4, [&](float v, int t) {
+            if (!has_dout) return 0.f;
+            if (prm.has_z) v *= silu_f(buf_load(rZ, 4 * c, t * rowHP4));
+            return v;
+        });
+        stage_cols_buf(tB, rB, rowGN4, ident1);
+        stage_cols_buf(tC, rC, rowGN4, ident1);
+        lds_barrier();
         f32x4 dxa[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) dxa[i] = zero4();
@@ -339,24 +396,24 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
                 for (int nb = 0; nb < 4; ++nb) dCa[nb] = mma3f(DCT[m], frag(tB, 16 * nb + r16, m), dCa[nb]);
             }
         }
-        __syncthreads();
+        lds_barrier();
 
         // ---- phase 2b: the state-side products
         const int64_t so = (((int64_t)b * H + h) * prm.K + k) * (int64_t)(P * N);
-        const float *Sk = prm.states + so;
-        const float *dUk = prm.dstates + so;
+        const auto rS = buf_rsrc(prm.states + so);
+        const auto rU = buf_rsrc(prm.dstates + so);
         float sdu = 0.f;
         {
             // tA[n][p] = S[p][n], tB[n][p] = dU[p][n] (same thread mapping)
-            const int c = tid & 63, tb = tid >> 6;
 #pragma unroll
-            for (int run = tb; run < 8; run += 4) {
+            for (int rr = 0; rr < 2; ++rr) {
+                const int run = w + 4 * rr;
                 float sv[8], dv[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const int p = run * 8 + i;
-                    sv[i] = Sk[p * N + c];
-                    dv[i] = dUk[p * N + c];
+                    sv[i] = buf_load(rS, 4 * c, p * N * 4);
+                    dv[i] = buf_load(rU, 4 * c, p * N * 4);
                     sdu += sv[i] * dv[i];
                 }
                 const Frag fs = pack_frag(sv), fd = pack_frag(dv);
@@ -366,54 +423,92 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
                 *(half8 *)&tB.lo[c * kTS + run * 8] = fd.l;
             }
         }
-        stage_rows(tC, [&](int p, int n4) { return *(const float4 *)(dUk + p * N + n4); });
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { // tC[p][n] = dU rows
+            const int p = rt + 16 * j;
+            const float4 v = buf_load4(rU, rt * N * 4 + rc4 * 4, 16 * j * N * 4);
+            half4 vh, vl;
+            split4(v, vh, vl);
+            *(half4 *)&tC.hi[p * kTS + rc4] = vh;
+            *(half4 *)&tC.lo[p * kTS + rc4] = vl;
+        }
         sdu = wave_sum(sdu);
         if (lane == 0) s_red[w] = sdu;
-        __syncthreads();
+        lds_barrier();
         {
-            f32x4 xs[4], bs[4], co[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xs[i] = zero4();
-                bs[i] = zero4();
-                co[i] = zero4();
-            }
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
+            // one product at a time keeps a single 16-register temporary live
+            const int vrowx = (16 * w + 4 * kq) * rowHP4 + 4 * r16; // row t = 16 w + 4 kq (+ r)
+            const int vrowc = (16 * w + 4 * kq) * rowGN4 + 4 * r16;
+            float rpart[4] = {0.f, 0.f, 0.f, 0.f}, gpart[4] = {0.f, 0.f, 0.f, 0.f};
+            {
+                f32x4 xs[4]; // [t][p] = B_t . dU[p]
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    xs[i] = mma3f(Bown[ks], frag(tC, 16 * i + r16, ks), xs[i]); // [t][p] = B_t . dU[p]
-                    bs[i] = mma3f(XDo[ks], frag(tB, 16 * i + r16, ks), bs[i]);  // [t][n] = xdt_t . dU[:, n]
-                    co[i] = mma3f(GYo[ks], frag(tA, 16 * i + r16, ks), co[i]);  // [t][n] = gy_t . S[:, n]
+                    xs[i] = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) xs[i] = mma3f(Bown[ks], frag(tC, 16 * i + r16, ks), xs[i]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * w + 4 * kq + r;
+                    const bool valid = full || t < tv;
+                    const float dte = s_dte[t], q = s_q[t];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float xv = valid ? buf_load(rX, vrowx + r * rowHP4 + 64 * i, 0) : 0.f;
+                        rpart[r] += xv * q * xs[i][r];
+                        dxa[i][r] += xs[i][r] * dte;
+                    }
+                }
+            }
+            {
+                f32x4 bs[4]; // [t][n] = xdt_t . dU[:, n]
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    bs[i] = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) bs[i] = mma3f(XDo[ks], frag(tB, 16 * i + r16, ks), bs[i]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float dte = s_dte[16 * w + 4 * kq + r];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dBa[i][r] += bs[i][r] * dte;
+                }
+            }
+            {
+                f32x4 co[4]; // [t][n] = gy_t . S[:, n]
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    co[i] = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) co[i] = mma3f(GYo[ks], frag(tA, 16 * i + r16, ks), co[i]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * w + 4 * kq + r;
+                    const bool valid = full || t < tv;
+                    const float ecs = s_ecs[t];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float dco = co[i][r] * ecs;
+                        dCa[i][r] += dco;
+                        const float cv = valid ? buf_load(rC, vrowc + r * rowGN4 + 64 * i, 0) : 0.f;
+                        gpart[r] += dco * cv;
+                    }
                 }
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * w + 4 * kq + r;
-                const bool valid = t < tv;
-                const float dte = s_dte[t], ecs = s_ecs[t], q = s_q[t];
-                float rpart = 0.f, gpart = 0.f;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int c = 16 * i + r16;
-                    const float xv = valid ? xh[(int64_t)t * rowHP + c] : 0.f;
-                    rpart += xv * q * xs[i][r];
-                    dxa[i][r] += xs[i][r] * dte;
-                    dBa[i][r] += bs[i][r] * dte;
-                    const float dco = co[i][r] * ecs;
-                    dCa[i][r] += dco;
-                    const float cv = valid ? Cg[(int64_t)t * rowGN + c] : 0.f;
-                    gpart += dco * cv;
-                }
-                rpart = sum16(rpart);
-                gpart = sum16(gpart);
+                const float rp = sum16(rpart[r]), gp = sum16(gpart[r]);
                 if (r16 == 0) {
-                    s_goff[t] = gpart;
-                    s_rdte[t] = rpart * dte;
+                    s_goff[t] = gp;
+                    s_rdte[t] = rp * s_dte[t];
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
 
         // ---- dcs -> da (reverse cumsum), dA partial
         if (w == 0) {
@@ -421,46 +516,46 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
             const float rd = s_rdte[lane];
             const float rd_tot = wave_sum(rd);
             float dcs = s_dcs1[lane] + s_goff[lane] - rd;
-            if (lane == T - 1) dcs += rd_tot + __expf(s_cs[T - 1]) * sdu_tot;
+            if (lane == T - 1) dcs += rd_tot + exp2_f(s_cs[T - 1]) * sdu_tot;
             const float da = wave_suffix_scan(dcs);
             s_da[lane] = da;
             const float dA_p = wave_sum(da * s_q[lane]);
             if (lane == 0) prm.part_dA[((int64_t)b * H + h) * prm.K + k] = dA_p;
         }
-        __syncthreads();
+        lds_barrier();
 
         // ---- epilogue: dx, ddt, dz and the D partial
         {
             const float Ah = prm.A[h];
             float dDp[4] = {0.f, 0.f, 0.f, 0.f};
-            const float *pg = prm.has_z ? prm.pre_gate + xo : nullptr;
+            const auto rPg = buf_rsrc(prm.has_z ? prm.pre_gate + xo : prm.x + xo);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * w + 4 * kq + r;
-                const bool valid = t < tv;
+                const bool valid = full || t < tv;
                 const float q = s_q[t];
                 float dqp = 0.f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int c = 16 * i + r16;
-                    const int64_t o = (int64_t)t * rowHP + c;
-                    const float xv = valid ? xh[o] : 0.f;
-                    const float dov = (valid && doh) ? doh[o] : 0.f;
+                    const int cc = 16 * i + r16;
+                    const int vo = (16 * w + 4 * kq + r) * rowHP4 + 4 * r16 + 64 * i, uo = 0;
+                    const float xv = valid ? buf_load(rX, vo, uo) : 0.f;
+                    const float dov = (valid && has_dout) ? buf_load(rDo, vo, uo) : 0.f;
                     float gyv = dov;
-                    if (zh && valid) {
-                        const float zv = zh[o], sg = sigmoid_f(zv);
+                    if (prm.has_z && valid) {
+                        const float zv = buf_load(rZ, vo, uo), sg = sigmoid_f(zv);
                         gyv = dov * zv * sg;
-                        prm.dz[xo + o] = dov * pg[o] * sg * (1.f + zv * (1.f - sg));
+                        prm.dz[xo + (int64_t)t * H * P + cc] = dov * buf_load(rPg, vo, uo) * sg * (1.f + zv * (1.f - sg));
                     }
                     const float dxdt = dxa[i][r];
                     dqp += xv * dxdt;
                     float dxv = q * dxdt;
                     if (prm.has_D) {
-                        const float Dv = prm.d_per_channel ? prm.D[h * P + c] : prm.D[h];
+                        const float Dv = prm.d_per_channel ? prm.D[h * P + cc] : prm.D[h];
                         dxv += Dv * gyv;
                         dDp[i] += gyv * xv;
                     }
-                    if (valid) prm.dx[xo + o] = dxv;
+                    if (valid) prm.dx[xo + (int64_t)t * H * P + cc] = dxv;
                 }
                 dqp = sum16(dqp);
                 if (r16 == 0) {
@@ -480,7 +575,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_chunk(BwdParams prm) {
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (w == 0) {
             const int64_t pi = ((int64_t)b * H + h) * prm.K + k;
             const float db = wave_sum(s_ddt[lane]);

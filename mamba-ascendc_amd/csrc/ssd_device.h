@@ -251,6 +251,10 @@ __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int lane_byt
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane_bytes, uniform_bytes, 0));
 }
 
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int lane_bytes, int uniform_bytes) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, uniform_bytes, 0));
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
