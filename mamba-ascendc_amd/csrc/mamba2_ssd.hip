@@ -12,6 +12,7 @@
 #include <cstring>
 
 #include "../../include/mamba2_ssd.h"
+#include "ssd_bwd_fused.h"
 #include "ssd_bwd_kernels.h"
 #include "ssd_fwd_fused.h"
 #include "ssd_fwd_kernels.h"
@@ -284,7 +285,8 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
 }
 
 // Backward workspace: states [B,H,K,P,N] | log decay [B,H,K] | dstates [B,H,K,P,N]
-// | dA partials [B,H,K] | ddt_bias partials [B,H,K] | dD partials [B,H,K,P].
+// | dA partials [B,H,K] | ddt_bias partials [B,H,K,slots] | dD partials
+// [B,H,K,slots,P] (slots = one per consumer wave of the chunk kernel).
 struct BwdLayout {
     size_t states, log_decay, dstates, part_dA, part_db, part_dD, total;
 };
@@ -303,12 +305,15 @@ BwdLayout bwd_layout(const Mamba2SsdShape *s) {
     l.part_dA = off;
     off += align256(bhk * sizeof(float));
     l.part_db = off;
-    off += align256(bhk * sizeof(float));
+    off += align256(bhk * ssd::kBwsSlots * sizeof(float));
     l.part_dD = off;
-    off += align256(bhk * (size_t)s->headdim * sizeof(float));
+    off += align256(bhk * ssd::kBwsSlots * (size_t)s->headdim * sizeof(float));
     l.total = off;
     return l;
 }
+
+// Work units of the chunk backward kernel (one workgroup per CU at a time).
+constexpr int64_t kBwdUnits = 1024;
 
 bool bwd_supported(const Mamba2SsdShape *s) { return s->headdim == 64 && s->dstate == 64; }
 
@@ -427,12 +432,18 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     hipLaunchKernelGGL(ssd::k_state_pass_bwd, state_grid, dim3(ssd::kThreads), 0, st, bp.dstates,
                        fp.chunk_log_decay, a->dfinal_state, a->dinitial_states, K, PN);
     if (int rc = launch_status("k_state_pass_bwd", tr, st)) return rc;
-    hipLaunchKernelGGL(ssd::k_bwd_chunk, dim3(K, (unsigned)s->ngroups, B), dim3(ssd::kThreads), 0,
-                       st, bp);
-    if (int rc = launch_status("k_bwd_chunk", tr, st)) return rc;
-    hipLaunchKernelGGL(ssd::k_bwd_finalize, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
+    // chunk backward: (b, g, run of chunks) work units, about kBwdUnits of them
+    const int64_t bg = (int64_t)B * s->ngroups;
+    int64_t nseg = (kBwdUnits + bg - 1) / bg;
+    nseg = nseg < K ? nseg : K;
+    const int M = (int)((K + nseg - 1) / nseg);
+    nseg = (K + M - 1) / M;
+    hipLaunchKernelGGL(ssd::k_bwd_ws, dim3((unsigned)(bg * nseg)), dim3(ssd::kBwsThreads), 0, st, bp,
+                       (int)nseg, M);
+    if (int rc = launch_status("k_bwd_ws", tr, st)) return rc;
+    hipLaunchKernelGGL(ssd::k_bwd_finalize_slots, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
                        bp.part_dbias, bp.part_dD, a->dA, a->ddt_bias, a->dD, B, H, K, 64,
-                       bp.has_D, bp.d_per_channel);
+                       ssd::kBwsSlots, bp.has_D, bp.d_per_channel);
     if (int rc = launch_status("k_bwd_finalize", tr, st)) return rc;
     return ok();
 }

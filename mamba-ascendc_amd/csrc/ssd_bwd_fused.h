@@ -1,0 +1,580 @@
+// Warp-specialized chunk backward of the Mamba-2 SSD hot path (M1 spec:
+// headdim = dstate = 64, execution chunk T = 64).
+//
+// One workgroup owns one (batch b, group g, run of chunks) and walks its
+// (chunk, head) steps in order: for each chunk, the R heads of the group.
+// dB and dC of a chunk are sums over the group's heads; they stay in the
+// consumer registers across the chunk's heads and are written once, so the
+// reduction order is fixed (deterministic, no atomics).
+//
+// Roles: waves 4..7 (producers) load the global tiles of the next steps into
+// registers and stage them into LDS as split fp16; waves 0..3 (consumers) own
+// 16 token rows each and run the products.  Each tile is kept in LDS once,
+// token-major (rows = the tile's leading index); operands that contract over
+// that index are read with the gfx950 transposing LDS read (ds_read_b64_tr_b16)
+// instead of a second, transposed copy.
+//
+// Per step (head h of chunk k), with xdt = q x, gy = dout (* silu z),
+// cs the chunk cumsum of A q, W[t][s] = (C_t . B_s) exp(cs_t - cs_s) [s <= t],
+// dCB = dW o exp-mask, S the state entering the chunk, dU = dL/d(state leaving):
+//   phase A (tiles x, gy, B, C):
+//     dW[t][s] = gy_t . xdt_s in both orientations, W, dCB, the dcs row/col sums,
+//     dxdt  = W^T gy,  dC += dCB B,  dB += dCB^T C
+//   phase B (tiles S, dU):
+//     dxdt += decay (B dU^T),  dC += exp(cs) (gy S),  dB += decay q (x dU),
+//     dcs  += g_off - decay r  (g_off = sum_n dC_off C, r = xdt . (B dU^T))
+//   epilogue (run at the start of the next step's phase A, once every wave's
+//   dcs is in LDS): da = reverse cumsum of dcs (+ the chunk-end terms),
+//     dq = A da + x . dxdt, ddt = dq dq/ddt, dx = q dxdt + D gy, dz,
+//     and per-(b, h, k, wave) partials of dA, ddt_bias and dD.
+// The LDS tiles are single-buffered: producers stage S, dU of step n while
+// consumers run phase A(n), and x, gy (and B, C of a new chunk) of step n + 1
+// while consumers run phase B(n); two workgroup barriers per step separate
+// the phases.  Producer registers hold the global loads one step ahead.
+//
+// The gradient is that of mamba_ascendc/csrc/ops/mamba2_ssd_bwd/design.md:73-107
+// and mamba_ascendc/csrc/ops/mamba2_ssd_dt_bwd/design.md:61-78; the fusion,
+// role split and layouts are this file's own.
+#pragma once
+
+#include <type_traits>
+
+#include "ssd_bwd_kernels.h"
+
+namespace ssd {
+
+constexpr int kBwsThreads = 512;  // 4 consumer + 4 producer waves
+constexpr int kBwsSlots = 4;      // partial sums per (b, h, k): one per consumer wave
+
+// ds_read_b64_tr_b16 on a split-tile array stored with the contraction index
+// along rows (tile[k][c]).  Each 16-lane group names rows k0..k0+3 (k0 may
+// differ between groups); lane l receives tile[k0 + e][c0 + l % 16], e = 0..3.
+__device__ __forceinline__ half4 tr4(const _Float16 *arr, int k0, int c0) {
+    const int m = threadIdx.x & 15;
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    auto p = (__attribute__((address_space(3))) v4s *)(arr + (k0 + (m >> 2)) * kTS + c0 + 4 * (m & 3));
+    return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
+}
+
+__device__ __forceinline__ half8 cat8(half4 a, half4 b) {
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Operand of columns c0 .. c0 + 15 contracting over the tile's rows in
+// natural order (k = 32 ks + 8 (l / 16) + 0..7).
+__device__ __forceinline__ Frag frag_tn(SplitTile s, int ks, int c0) {
+    const int k0 = 32 * ks + 8 * ((threadIdx.x & 63) >> 4);
+    Frag f;
+    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 4, c0));
+    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 4, c0));
+    return f;
+}
+
+// The same in the k order of operands taken from MFMA outputs (perm32):
+// slots 0..3 are rows 32 m + 4 (l / 16) + 0..3, slots 4..7 rows 32 m + 16 + ...
+__device__ __forceinline__ Frag frag_tp(SplitTile s, int m, int c0) {
+    const int k0 = 32 * m + 4 * ((threadIdx.x & 63) >> 4);
+    Frag f;
+    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 16, c0));
+    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 16, c0));
+    return f;
+}
+
+// fp32 values of rows row0 + 4 (l / 16) + r, column c0 + l % 16 (r = 0..3):
+// the MFMA accumulator layout of a 16-row block.
+__device__ __forceinline__ f32x4 tile_acc(SplitTile s, int row0, int c0) {
+    const int k0 = row0 + 4 * ((threadIdx.x & 63) >> 4);
+    const half4 h = tr4(s.hi, k0, c0), l = tr4(s.lo, k0, c0);
+    return f32x4{(float)h[0] + (float)l[0], (float)h[1] + (float)l[1], (float)h[2] + (float)l[2],
+                 (float)h[3] + (float)l[3]};
+}
+
+__global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg, int M) {
+    constexpr int T = 64, P = 64, N = 64;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[12 * kTile];
+    // per-token values of a step, double buffered by step parity
+    __shared__ __attribute__((aligned(16))) float s_q[2][T], s_cs[2][T], s_dqdu[2][T], s_dte[2][T],
+        s_ecs[2][T];
+    __shared__ float s_dcs[2][T], s_rd[2][T], s_sdu[2][4];
+
+    const SplitTile Xt = tile_at(lds, 0), Gt = tile_at(lds, 1), St = tile_at(lds, 2),
+                    Ut = tile_at(lds, 3), Bt = tile_at(lds, 4), Ct = tile_at(lds, 5);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int sg = blockIdx.x % nseg, bg = blockIdx.x / nseg;
+    const int g = bg % prm.G, b = bg / prm.G;
+    const int R = prm.R, H = prm.H, G = prm.G, K = prm.K;
+    const int kbeg = sg * M, kend = min(kbeg + M, K);
+    const int NS = (kend - kbeg) * R;
+    if (NS <= 0) return;
+    const int rowHP4 = H * P * 4, rowGN4 = G * N * 4; // token strides, bytes
+    auto tvalid = [&](int k) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
+
+    // ------------------------------------------------------------ producers
+    if (wave >= 4) {
+        const int pt = tid - 4 * kWave, pw = wave - 4;
+        const int rt = pt >> 4, c4 = (pt & 15) * 4; // rows rt + 16 j, columns c4 .. c4 + 3
+        const bool has_dout = prm.dout != nullptr, has_z = prm.has_z != 0;
+        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 xr[4], gr[4], zr[4], sr[4], ur[4], br[4], cr[4];
+        float dtr = 0.f;
+        auto load_xg = [&](int n) {
+            const int k = kbeg + n / R, h = g * R + n % R, tv = tvalid(k);
+            const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
+            const auto rx = buf_rsrc(prm.x + xo);
+            const auto rd = buf_rsrc(has_dout ? prm.dout + xo : prm.x + xo);
+            const auto rz = buf_rsrc(has_z ? prm.z + xo : prm.x + xo);
+            const int lo = rt * rowHP4 + c4 * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = rt + 16 * j < tv;
+                xr[j] = ok ? buf_load4(rx, lo, 16 * j * rowHP4) : z4;
+                gr[j] = (ok && has_dout) ? buf_load4(rd, lo, 16 * j * rowHP4) : z4;
+                if (has_z) zr[j] = ok ? buf_load4(rz, lo, 16 * j * rowHP4) : z4;
+            }
+            if (pw == 0)
+                dtr = lane < tv ? prm.dt[((int64_t)b * prm.L + (int64_t)k * T + lane) * H + h] : 0.f;
+        };
+        auto load_bc = [&](int k) {
+            const int tv = tvalid(k);
+            const int64_t o = (((int64_t)b * prm.L + (int64_t)k * T) * G + g) * N;
+            const auto rb = buf_rsrc(prm.B + o), rc = buf_rsrc(prm.C + o);
+            const int lo = rt * rowGN4 + c4 * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = rt + 16 * j < tv;
+                br[j] = ok ? buf_load4(rb, lo, 16 * j * rowGN4) : z4;
+                cr[j] = ok ? buf_load4(rc, lo, 16 * j * rowGN4) : z4;
+            }
+        };
+        auto load_su = [&](int n) {
+            const int k = kbeg + n / R, h = g * R + n % R;
+            const int64_t so = (((int64_t)b * H + h) * K + k) * (int64_t)(P * N);
+            const auto rs = buf_rsrc(prm.states + so), ru = buf_rsrc(prm.dstates + so);
+            const int lo = (rt * N + c4) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sr[j] = buf_load4(rs, lo, 16 * j * N * 4);
+                ur[j] = buf_load4(ru, lo, 16 * j * N * 4);
+            }
+        };
+        auto put = [&](SplitTile d, int row, float4 v) {
+            half4 vh, vl;
+            split4(v, vh, vl);
+            *(half4 *)&d.hi[row * kTS + c4] = vh;
+            *(half4 *)&d.lo[row * kTS + c4] = vl;
+        };
+        auto stage_xg = [&](int n) {
+            const int par = n & 1, k = kbeg + n / R, h = g * R + n % R, tv = tvalid(k);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                put(Xt, rt + 16 * j, xr[j]);
+                float4 v = gr[j];
+                if (has_z) {
+                    v.x *= silu_f(zr[j].x);
+                    v.y *= silu_f(zr[j].y);
+                    v.z *= silu_f(zr[j].z);
+                    v.w *= silu_f(zr[j].w);
+                }
+                put(Gt, rt + 16 * j, v);
+            }
+            if (pw == 0) {
+                float q = 0.f, a = 0.f, dq = 0.f;
+                if (lane < tv) {
+                    const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
+                    q = discretize_dt(dtr, bias, prm.softplus != 0, prm.lo, prm.hi);
+                    dq = discretize_grad(dtr, bias, prm.softplus != 0, prm.lo, prm.hi);
+                    a = prm.A[h] * kLog2e * q;
+                }
+                const float cs = wave_inclusive_scan(a); // log2 units
+                const float last = readlane_f(cs, T - 1);
+                s_q[par][lane] = q;
+                s_cs[par][lane] = cs;
+                s_dqdu[par][lane] = dq;
+                s_dte[par][lane] = exp2_f(last - cs);
+                s_ecs[par][lane] = exp2_f(cs);
+            }
+        };
+        auto stage_bc = [&]() {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                put(Bt, rt + 16 * j, br[j]);
+                put(Ct, rt + 16 * j, cr[j]);
+            }
+        };
+        auto stage_su = [&](int n) {
+            float sdu = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                put(St, rt + 16 * j, sr[j]);
+                put(Ut, rt + 16 * j, ur[j]);
+                sdu += sr[j].x * ur[j].x + sr[j].y * ur[j].y + sr[j].z * ur[j].z + sr[j].w * ur[j].w;
+            }
+            sdu = wave_sum(sdu);
+            if (lane == 0) s_sdu[n & 1][pw] = sdu;
+        };
+
+        load_xg(0);
+        load_bc(kbeg);
+        load_su(0);
+        stage_xg(0);
+        stage_bc();
+        if (NS > 1) {
+            load_xg(1);
+            if (1 % R == 0) load_bc(kbeg + 1);
+        }
+        lds_barrier();
+        // every step: two barriers, as in the consumer loop
+        for (int n = 0; n < NS; ++n) {
+            stage_su(n);
+            if (n + 1 < NS) load_su(n + 1);
+            lds_barrier();
+            if (n + 1 < NS) {
+                stage_xg(n + 1);
+                if ((n + 1) % R == 0) stage_bc();
+            }
+            if (n + 2 < NS) {
+                load_xg(n + 2);
+                if ((n + 2) % R == 0) load_bc(kbeg + (n + 2) / R);
+            }
+            lds_barrier();
+        }
+        return;
+    }
+
+    // ------------------------------------------------------------ consumers
+    auto consumer = [&](auto wave_c) {
+        constexpr int W = decltype(wave_c)::value;
+        const int own = 16 * W + r16;   // operand row of this lane
+        const int trow = 16 * W + 4 * kq; // first of the 4 accumulator rows of this lane
+        f32x4 dBa[4], dCa[4];
+        // carried from phase B of a step to its epilogue
+        f32x4 dxa[4], xa[4], ga[4];
+        float dqp[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dBa[i] = zero4();
+            dCa[i] = zero4();
+        }
+
+        auto epilogue = [&](int n) {
+            const int k = kbeg + n / R, h = g * R + n % R, par = n & 1;
+            const int64_t t0 = (int64_t)k * T;
+            const int tv = tvalid(k);
+            const int64_t bhk = ((int64_t)b * H + h) * K + k;
+            float v = s_dcs[par][lane];
+            const float rd_tot = wave_sum(s_rd[par][lane]);
+            const float sdu = s_sdu[par][0] + s_sdu[par][1] + s_sdu[par][2] + s_sdu[par][3];
+            if (lane == T - 1) v += rd_tot + exp2_f(s_cs[par][T - 1]) * sdu;
+            const float da = wave_suffix_scan(v);
+            if (W == 0) {
+                const float dA_p = wave_sum(da * s_q[par][lane]);
+                if (lane == 0) prm.part_dA[bhk] = dA_p;
+            }
+            const float Ah = prm.A[h];
+            const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
+            float dbias = 0.f, dDp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int t = trow + rr;
+                const bool valid = t < tv;
+                const float da_t = __shfl(da, t, kWave);
+                const float q_t = s_q[par][t];
+                const float ddt = valid ? (Ah * da_t + dqp[rr]) * s_dqdu[par][t] : 0.f;
+                if (r16 == 0) {
+                    if (valid) prm.ddt[((int64_t)b * prm.L + t0 + t) * H + h] = ddt;
+                    dbias += ddt;
+                }
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) {
+                    const int c = 16 * pb + r16;
+                    const float gyv = ga[pb][rr], xv = xa[pb][rr];
+                    float dxv = q_t * dxa[pb][rr];
+                    if (prm.has_D) {
+                        const float Dv = prm.d_per_channel ? prm.D[h * P + c] : prm.D[h];
+                        dxv += Dv * gyv;
+                        dDp[pb] += gyv * xv;
+                    }
+                    if (valid) {
+                        const int64_t o = xo + (int64_t)t * H * P + c;
+                        prm.dx[o] = dxv;
+                        if (prm.has_z) {
+                            const float zv = prm.z[o], sgm = sigmoid_f(zv);
+                            const float dov = prm.dout ? prm.dout[o] : 0.f;
+                            prm.dz[o] = dov * prm.pre_gate[o] * sgm * (1.f + zv * (1.f - sgm));
+                        }
+                    }
+                }
+            }
+            dbias = wave_sum(dbias);
+            if (lane == 0) prm.part_dbias[bhk * kBwsSlots + W] = dbias;
+            if (prm.has_D) {
+                if (prm.d_per_channel) {
+#pragma unroll
+                    for (int pb = 0; pb < 4; ++pb) {
+                        const float vv = sum_kq(dDp[pb]);
+                        if (kq == 0) prm.part_dD[(bhk * kBwsSlots + W) * P + 16 * pb + r16] = vv;
+                    }
+                } else {
+                    const float tot = wave_sum(dDp[0] + dDp[1] + dDp[2] + dDp[3]);
+                    if (lane == 0) prm.part_dD[bhk * kBwsSlots + W] = tot;
+                }
+            }
+        };
+
+        lds_barrier(); // first tiles staged
+        for (int n = 0; n < NS; ++n) {
+            const int k = kbeg + n / R, r = n % R, par = n & 1;
+            if (n > 0) epilogue(n - 1);
+
+            // ---------------- phase A: x, gy, B, C
+            const float *q_ = s_q[par], *cs_ = s_cs[par];
+            Frag Bo[2], Co[2], Go[2], Xo[2];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                Bo[ks] = frag(Bt, own, ks);
+                Co[ks] = frag(Ct, own, ks);
+                Go[ks] = frag(Gt, own, ks);
+                Xo[ks] = frag(Xt, own, ks);
+            }
+            const float cs_own = cs_[own], q_own = q_[own];
+            Frag DCT[2], DCS[2], WS[2];
+            float rows = 0.f, cols = 0.f;
+            {
+                // T orientation: t = own, s = 16 j + 4 kq + i, s-blocks j <= W
+                float dct[2][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (j <= W) {
+                        f32x4 cb = zero4(), dw = zero4();
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) {
+                            cb = mma3f(frag(Bt, 16 * j + r16, ks), Co[ks], cb);
+                            dw = mma3f(frag(Xt, 16 * j + r16, ks), Go[ks], dw);
+                        }
+                        const float4 qv = *(const float4 *)&q_[16 * j + 4 * kq];
+                        const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
+                        const float qa[4] = {qv.x, qv.y, qv.z, qv.w}, ca[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const bool in = j < W || 4 * kq + i <= r16;
+                            const float e = in ? exp2_f(cs_own - ca[i]) : 0.f;
+                            const float dwv = dw[i] * qa[i];
+                            rows += dwv * cb[i] * e;
+                            dct[j >> 1][(j & 1) * 4 + i] = dwv * e;
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) dct[j >> 1][(j & 1) * 4 + i] = 0.f;
+                    }
+                }
+                DCT[0] = pack_frag(dct[0]);
+                DCT[1] = pack_frag(dct[1]);
+            }
+            {
+                // S orientation: s = own, t = 16 j + 4 kq + i, t-blocks j >= W
+                float ws[2][8], dcs[2][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (j >= W) {
+                        f32x4 cb = zero4(), dw = zero4();
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) {
+                            cb = mma3f(frag(Ct, 16 * j + r16, ks), Bo[ks], cb);
+                            dw = mma3f(frag(Gt, 16 * j + r16, ks), Xo[ks], dw);
+                        }
+                        const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
+                        const float ca[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const bool in = j > W || r16 <= 4 * kq + i;
+                            const float e = in ? exp2_f(ca[i] - cs_own) : 0.f;
+                            const float dwv = dw[i] * q_own, wsv = cb[i] * e;
+                            cols += dwv * wsv;
+                            ws[j >> 1][(j & 1) * 4 + i] = wsv;
+                            dcs[j >> 1][(j & 1) * 4 + i] = dwv * e;
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            ws[j >> 1][(j & 1) * 4 + i] = 0.f;
+                            dcs[j >> 1][(j & 1) * 4 + i] = 0.f;
+                        }
+                    }
+                }
+                WS[0] = pack_frag(ws[0]);
+                WS[1] = pack_frag(ws[1]);
+                DCS[0] = pack_frag(dcs[0]);
+                DCS[1] = pack_frag(dcs[1]);
+            }
+            rows = sum_kq(rows);
+            cols = sum_kq(cols);
+            if (kq == 0) s_dcs[par][own] = rows - cols;
+
+            // dxdt = W^T gy (rows s of this wave)
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) dxa[pb] = zero4();
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+                if (2 * m + 1 >= W)
+#pragma unroll
+                    for (int pb = 0; pb < 4; ++pb) dxa[pb] = mma3f(WS[m], frag_tp(Gt, m, 16 * pb), dxa[pb]);
+            // dC += dCB B (rows t), dB += dCB^T C (rows s)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                if (2 * m <= W)
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb) dCa[nb] = mma3f(DCT[m], frag_tp(Bt, m, 16 * nb), dCa[nb]);
+                if (2 * m + 1 >= W)
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb) dBa[nb] = mma3f(DCS[m], frag_tp(Ct, m, 16 * nb), dBa[nb]);
+            }
+            f32x4 ca[4];
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) {
+                xa[pb] = tile_acc(Xt, 16 * W, 16 * pb);
+                ga[pb] = tile_acc(Gt, 16 * W, 16 * pb);
+                ca[pb] = tile_acc(Ct, 16 * W, 16 * pb);
+            }
+            lds_barrier(); // phase-A tiles free; S, dU staged
+
+            // ---------------- phase B: S, dU
+            float tq[4], tdte[4], tecs[4];
+            {
+                const float4 a = *(const float4 *)&s_q[par][trow];
+                const float4 d = *(const float4 *)&s_dte[par][trow];
+                const float4 e = *(const float4 *)&s_ecs[par][trow];
+                tq[0] = a.x, tq[1] = a.y, tq[2] = a.z, tq[3] = a.w;
+                tdte[0] = d.x, tdte[1] = d.y, tdte[2] = d.z, tdte[3] = d.w;
+                tecs[0] = e.x, tecs[1] = e.y, tecs[2] = e.z, tecs[3] = e.w;
+            }
+            float rpart[4] = {0.f, 0.f, 0.f, 0.f}, gpart[4] = {0.f, 0.f, 0.f, 0.f};
+            {
+                // B dU^T: [t][p]
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) {
+                    f32x4 rm = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) rm = mma3f(Bo[ks], frag(Ut, 16 * pb + r16, ks), rm);
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        dxa[pb][rr] += tdte[rr] * rm[rr];
+                        rpart[rr] += xa[pb][rr] * rm[rr];
+                    }
+                }
+            }
+            {
+                // gy S: [t][n]
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) {
+                    f32x4 co = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) co = mma3f(Go[ks], frag_tn(St, ks, 16 * nb), co);
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const float vv = tecs[rr] * co[rr];
+                        dCa[nb][rr] += vv;
+                        gpart[rr] += vv * ca[nb][rr];
+                    }
+                }
+            }
+            {
+                // x dU: [t][n]
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) {
+                    f32x4 bs = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) bs = mma3f(Xo[ks], frag_tn(Ut, ks, 16 * nb), bs);
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) dBa[nb][rr] += tdte[rr] * tq[rr] * bs[rr];
+                }
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const float rd = sum16(rpart[rr]) * tq[rr] * tdte[rr];
+                const float gp = sum16(gpart[rr]);
+                dqp[rr] = sum16(xa[0][rr] * dxa[0][rr] + xa[1][rr] * dxa[1][rr] +
+                                xa[2][rr] * dxa[2][rr] + xa[3][rr] * dxa[3][rr]);
+                if (r16 == 0) {
+                    s_dcs[par][trow + rr] += gp - rd;
+                    s_rd[par][trow + rr] = rd;
+                }
+            }
+            if (r == R - 1) {
+                const int64_t t0 = (int64_t)k * T;
+                const int tv = tvalid(k);
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int t = trow + rr;
+                    if (t < tv) {
+                        const int64_t o = (((int64_t)b * prm.L + t0 + t) * G + g) * N;
+#pragma unroll
+                        for (int nb = 0; nb < 4; ++nb) {
+                            prm.dB[o + 16 * nb + r16] = dBa[nb][rr];
+                            prm.dC[o + 16 * nb + r16] = dCa[nb][rr];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    dBa[i] = zero4();
+                    dCa[i] = zero4();
+                }
+            }
+            lds_barrier(); // phase-B tiles free; next x, gy (B, C) staged
+        }
+        epilogue(NS - 1);
+    };
+    switch (wave) {
+    case 0: consumer(std::integral_constant<int, 0>{}); break;
+    case 1: consumer(std::integral_constant<int, 1>{}); break;
+    case 2: consumer(std::integral_constant<int, 2>{}); break;
+    default: consumer(std::integral_constant<int, 3>{}); break;
+    }
+}
+
+// fixed-order reductions of the per-chunk partials, one workgroup per head:
+// dA from [B, H, K], ddt_bias and dD from [B, H, K, slots] (dD per channel:
+// [B, H, K, slots, P])
+__global__ __launch_bounds__(kThreads) void k_bwd_finalize_slots(
+    const float *part_dA, const float *part_dbias, const float *part_dD, float *dA, float *ddt_bias,
+    float *dD, int B, int H, int K, int P, int slots, int has_D, int d_per_channel) {
+    __shared__ float s_tmp[4];
+    __shared__ float s_col[4][64];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int n1 = B * K, ks = K * slots, n4 = B * ks;
+    float a = 0.f, db = 0.f, dd = 0.f;
+    for (int i = tid; i < n1; i += kThreads) a += part_dA[((int64_t)(i / K) * H + h) * K + i % K];
+    for (int i = tid; i < n4; i += kThreads) {
+        const int64_t pi = ((int64_t)(i / ks) * H + h) * ks + i % ks;
+        db += part_dbias[pi];
+        if (has_D && !d_per_channel) dd += part_dD[pi];
+    }
+    a = block_sum(a, s_tmp);
+    if (tid == 0) dA[h] = a;
+    db = block_sum(db, s_tmp);
+    if (tid == 0 && ddt_bias) ddt_bias[h] = db;
+    if (has_D && !d_per_channel) {
+        dd = block_sum(dd, s_tmp);
+        if (tid == 0) dD[h] = dd;
+    }
+    if (has_D && d_per_channel) {
+        for (int p0 = 0; p0 < P; p0 += 64) {
+            const int p = p0 + (tid & 63), grp = tid >> 6;
+            float v = 0.f;
+            if (p < P)
+                for (int i = grp; i < n4; i += 4) {
+                    const int64_t pi = ((int64_t)(i / ks) * H + h) * ks + i % ks;
+                    v += part_dD[pi * P + p];
+                }
+            s_col[grp][tid & 63] = v;
+            __syncthreads();
+            if (grp == 0 && p < P)
+                dD[h * P + p] = s_col[0][tid] + s_col[1][tid] + s_col[2][tid] + s_col[3][tid];
+            __syncthreads();
+        }
+    }
+}
+
+}  // namespace ssd
