@@ -228,18 +228,20 @@ def bench_forward(torch, lib, rt, api, hip, inp, shape, steps, warmup):
 
 
 def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup):
-    """fwd + M1 bwd through the C ABI with per-kernel events; upstream
-    gradients of the loss mean(y^2) + mean(final^2).  None if unsupported."""
+    """Training forward (saving the chunk-start states) + M1 bwd through the C
+    ABI with per-kernel events; upstream gradients of the loss mean(y^2) +
+    mean(final^2).  None if unsupported."""
     x, dt, A, B, C = (inp[k] for k in ("x", "dt", "A", "B", "C"))
     b, l, h, p, n, chunk, g = shape
     shp = rt.Mamba2SsdShape(b, l, h, p, g, n, chunk)
-    flags = rt.DT_SOFTPLUS
+    if p != 64 or n != 64:
+        return None
+    flags = rt.DT_SOFTPLUS | rt.SAVED_STATES
     fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0)
     rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shp), flags, ctypes.byref(fb)), "ws", lib)
     rt.check(lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(shp), flags, ctypes.byref(bb)), "ws", lib)
-    if p != 64 or n != 64:
-        return None
     P = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    states = torch.empty(b, h, (l + 63) // 64, p, n, device=x.device, dtype=torch.float32)
     out = torch.empty_like(x)
     final = torch.empty(b, h, p, n, device=x.device, dtype=torch.float32)
     ws = torch.empty(max(1, fb.value, bb.value), dtype=torch.uint8, device=x.device)
@@ -247,9 +249,9 @@ def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup):
     dout = torch.empty_like(x)
     dfinal = torch.empty_like(final)
     fargs = rt.Mamba2SsdFwdArgs(shp, flags, 0.0, math.inf, P(x), P(dt), P(A), P(B), P(C),
-                                None, None, None, None, P(out), P(final), None)
+                                None, None, None, None, P(out), P(final), None, P(states))
     bargs = rt.Mamba2SsdBwdArgs(shp, flags, 0.0, math.inf, P(x), P(dt), P(A), P(B), P(C),
-                                None, None, None, None, P(dout), P(dfinal), None,
+                                None, None, None, None, P(dout), P(dfinal), None, P(states),
                                 P(grads["x"]), P(grads["dt"]), P(grads["A"]), P(grads["B"]),
                                 P(grads["C"]), None, None, None, None)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -532,6 +534,7 @@ def main(argv=None):
     log(f"public API forward median {api_ms:.4f} ms")
 
     fwd_bwd_ms, bwd_note, api_fwd_bwd_ms, bwd_kern, bwd_ms = None, "skipped (--no-bwd)", None, {}, None
+    fwd_train_ms = None
     if not args.no_bwd:
         tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, args.steps, args.warmup)
         if tr is None:
@@ -539,8 +542,11 @@ def main(argv=None):
         else:
             fres, bres, bnames, bfinite, _ = tr
             bwd_ms = statistics.median(r[0] for r in bres)
+            fwd_train_ms = statistics.median(r[0] for r in fres)
             fwd_bwd_ms = statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres))
-            bwd_note = f"C-ABI fwd + M1 bwd, loss mean(y^2)+mean(final^2), grads finite={bfinite}"
+            bwd_note = ("C-ABI training fwd (saves chunk-start states) + M1 bwd, loss "
+                        f"mean(y^2)+mean(final^2), grads finite={bfinite}")
+            log(f"training forward (saving chunk states) median {fwd_train_ms:.4f} ms")
             for i, name in enumerate(bnames):
                 durs = [r[1][i] for r in bres]
                 bwd_kern[name] = {"avg_ms": round(statistics.fmean(durs), 6),
@@ -594,6 +600,7 @@ def main(argv=None):
             "seed": seed,
         },
         "fwd_bwd_ms": None if fwd_bwd_ms is None else round(fwd_bwd_ms, 5),
+        "fwd_train_ms": None if fwd_train_ms is None else round(fwd_train_ms, 5),
         "bwd_ms": None if bwd_ms is None else round(bwd_ms, 5),
         "fwd_bwd_note": bwd_note,
         "api_fwd_bwd_ms": None if api_fwd_bwd_ms is None else round(api_fwd_bwd_ms, 5),

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MAMBA2_SSD_ABI_VERSION 1
+#define MAMBA2_SSD_ABI_VERSION 2
 
 /* status codes */
 #define MAMBA2_SSD_OK 0
@@ -55,6 +55,9 @@ extern "C" {
 #define MAMBA2_SSD_HAS_Z (1u << 3)
 #define MAMBA2_SSD_HAS_DT_BIAS (1u << 4)
 #define MAMBA2_SSD_HAS_INITIAL (1u << 5)
+/* forward: write chunk_states; backward: read them instead of recomputing
+ * (headdim == dstate == 64 only) */
+#define MAMBA2_SSD_SAVED_STATES (1u << 6)
 
 typedef struct Mamba2SsdShape {
     int64_t batch;
@@ -77,6 +80,13 @@ typedef struct Mamba2SsdFwdArgs {
     float *final_state; /* [B, H, P, N] or NULL */
     float *pre_gate;    /* [B, L, H, P] y + D x before the z gate (written only
                            with HAS_Z; what the backward needs for dz), or NULL */
+    float *chunk_states; /* [B, H, ceil(L / 64), P, N]: the state entering each
+                            64-token chunk, for the backward; written iff
+                            SAVED_STATES, else NULL (the reference's training
+                            forward returns states_start the same way:
+                            mamba2.py:228,322,408-418 return_states_start,
+                            mamba_ascendc_ops/mamba2_ssd_chunk_mix/op_kernel/
+                            mamba2_ssd_state_epilogue_train_states.cpp:15) */
 } Mamba2SsdFwdArgs;
 
 typedef struct Mamba2SsdBwdArgs {
@@ -89,6 +99,8 @@ typedef struct Mamba2SsdBwdArgs {
     const float *dout;         /* [B, L, H, P]; NULL means zero */
     const float *dfinal_state; /* [B, H, P, N]; NULL means zero */
     const float *pre_gate;     /* [B, L, H, P] from the forward; required iff HAS_Z */
+    const float *chunk_states; /* [B, H, ceil(L / 64), P, N] from the forward;
+                                  required iff SAVED_STATES, else NULL */
     float *dx, *ddt, *dA, *dB, *dC;
     float *dD, *dz, *ddt_bias, *dinitial_states; /* required iff the feature is flagged */
 } Mamba2SsdBwdArgs;
@@ -111,7 +123,8 @@ int mamba2_ssd_fwd_traced(const Mamba2SsdFwdArgs *args, void *workspace, size_t 
                           void *stream, void *const *events, int nevents, const char **names,
                           int *nkernels);
 
-/* Bytes of device workspace mamba2_ssd_bwd_m1 needs for this shape/flags. */
+/* Bytes of device workspace mamba2_ssd_bwd_m1 needs for this shape/flags
+ * (less with SAVED_STATES: the chunk states are not recomputed). */
 int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes);
 
 /* M1 backward: gradients of the forward for the given upstream gradients.

@@ -17,7 +17,7 @@ _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIBRARY_NAME = "libmamba2_ssd.so"
 LIBRARY_PATH = os.environ.get("MAMBA2_SSD_LIBRARY", os.path.join(_PKG_ROOT, LIBRARY_NAME))
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DT_SOFTPLUS = 1 << 0
 HAS_D = 1 << 1
@@ -25,6 +25,7 @@ D_PER_CHANNEL = 1 << 2
 HAS_Z = 1 << 3
 HAS_DT_BIAS = 1 << 4
 HAS_INITIAL = 1 << 5
+SAVED_STATES = 1 << 6
 
 STATUS_NAMES = {
     0: "OK",
@@ -60,6 +61,7 @@ class Mamba2SsdFwdArgs(ctypes.Structure):
         ("out", _c_fp),
         ("final_state", _c_fp),
         ("pre_gate", _c_fp),
+        ("chunk_states", _c_fp),
     ]
 
 
@@ -71,7 +73,7 @@ class Mamba2SsdBwdArgs(ctypes.Structure):
         ("dt_limit_max", ctypes.c_float),
         ("x", _c_fp), ("dt", _c_fp), ("A", _c_fp), ("B", _c_fp), ("C", _c_fp),
         ("D", _c_fp), ("z", _c_fp), ("dt_bias", _c_fp), ("initial_states", _c_fp),
-        ("dout", _c_fp), ("dfinal_state", _c_fp), ("pre_gate", _c_fp),
+        ("dout", _c_fp), ("dfinal_state", _c_fp), ("pre_gate", _c_fp), ("chunk_states", _c_fp),
         ("dx", _c_fp), ("ddt", _c_fp), ("dA", _c_fp), ("dB", _c_fp), ("dC", _c_fp),
         ("dD", _c_fp), ("dz", _c_fp), ("ddt_bias", _c_fp), ("dinitial_states", _c_fp),
     ]

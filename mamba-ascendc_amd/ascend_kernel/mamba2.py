@@ -137,13 +137,22 @@ def _stream(device: torch.device):
 
 # ----------------------------------------------------------------------------- raw calls
 
+def _nchunks(x) -> int:
+    return (x.shape[1] + 63) // 64
+
+
 def _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softplus,
-             dt_limit_min, dt_limit_max, want_final=True, want_pre_gate=False):
-    """Returns (out, final_state or None, pre_gate or None); pre_gate (y + D x
-    before the z gate) is produced only when z is given and it is asked for."""
+             dt_limit_min, dt_limit_max, want_final=True, want_pre_gate=False,
+             want_states=False):
+    """Returns (out, final_state or None, pre_gate or None, chunk_states or None);
+    pre_gate (y + D x before the z gate) is produced only when z is given and it
+    is asked for; chunk_states [B, H, ceil(L/64), P, N] (the state entering each
+    64-token chunk, for the backward) only when asked for."""
     lib = rt.load_library()
     shape = _shape(x, B, chunk_size)
     flags = _flags(D, z, dt_bias, initial_states, dt_softplus)
+    if want_states:
+        flags |= rt.SAVED_STATES
     nbytes = ctypes.c_size_t(0)
     rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shape), flags, ctypes.byref(nbytes)),
              "mamba2_ssd_fwd_workspace_size", lib)
@@ -151,24 +160,28 @@ def _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softp
     b, _, h, p = x.shape
     final = torch.empty(b, h, p, B.shape[3], device=x.device, dtype=torch.float32) if want_final else None
     pre_gate = torch.empty_like(x) if (want_pre_gate and z is not None) else None
+    states = (torch.empty(b, h, _nchunks(x), p, B.shape[3], device=x.device, dtype=torch.float32)
+              if want_states else None)
     ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=x.device)
     args = rt.Mamba2SsdFwdArgs(
         shape, flags, float(dt_limit_min), _limit(dt_limit_max),
         _ptr(x), _ptr(dt), _ptr(A), _ptr(B), _ptr(C),
         _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(initial_states),
-        _ptr(out), _ptr(final), _ptr(pre_gate),
+        _ptr(out), _ptr(final), _ptr(pre_gate), _ptr(states),
     )
     with torch.cuda.device(x.device):
         rt.check(lib.mamba2_ssd_fwd(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(x.device)),
                  "mamba2_ssd_fwd", lib)
-    return out, final, pre_gate
+    return out, final, pre_gate, states
 
 
 def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, chunk_size,
-             dt_softplus, dt_limit_min, dt_limit_max, pre_gate=None):
+             dt_softplus, dt_limit_min, dt_limit_max, pre_gate=None, chunk_states=None):
     lib = rt.load_library()
     shape = _shape(x, B, chunk_size)
     flags = _flags(D, z, dt_bias, initial_states, dt_softplus)
+    if chunk_states is not None:
+        flags |= rt.SAVED_STATES
     nbytes = ctypes.c_size_t(0)
     rt.check(lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(shape), flags, ctypes.byref(nbytes)),
              "mamba2_ssd_bwd_m1_workspace_size", lib)
@@ -186,7 +199,7 @@ def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, 
         shape, flags, float(dt_limit_min), _limit(dt_limit_max),
         _ptr(x), _ptr(dt), _ptr(A), _ptr(B), _ptr(C),
         _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(initial_states),
-        _ptr(dout), _ptr(dfinal_state), _ptr(pre_gate),
+        _ptr(dout), _ptr(dfinal_state), _ptr(pre_gate), _ptr(chunk_states),
         _ptr(dx), _ptr(ddt), _ptr(dA), _ptr(dB), _ptr(dC),
         _ptr(dD), _ptr(dz), _ptr(ddt_bias), _ptr(dinit),
     )
@@ -207,7 +220,8 @@ _FWD_SCHEMA = (
 _BWD_SCHEMA = (
     "mamba2_ssd_bwd_m1(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor dout, "
     "Tensor? dfinal_state=None, Tensor? D=None, Tensor? z=None, Tensor? dt_bias=None, "
-    "Tensor? initial_states=None, Tensor? pre_gate=None, int chunk_size=64, "
+    "Tensor? initial_states=None, Tensor? pre_gate=None, Tensor? chunk_states=None, "
+    "int chunk_size=64, "
     "bool dt_softplus=False, float dt_limit_min=0.0, float dt_limit_max=3.402823466e+38) "
     "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
     "Tensor, Tensor)"
@@ -222,8 +236,8 @@ def _op_fwd_cuda(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=No
                  dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.402823466e+38):
     _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
                   dt_limit_min, dt_limit_max)
-    out, final, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
-                             dt_softplus, dt_limit_min, dt_limit_max)
+    out, final, _, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
+                                dt_softplus, dt_limit_min, dt_limit_max)
     return out, final
 
 
@@ -239,7 +253,7 @@ def _empty_like_or_none(t, ref):
 
 def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bias=None,
                  initial_states=None,
-                 pre_gate=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
+                 pre_gate=None, chunk_states=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
                  dt_limit_max=3.402823466e+38):
     op = "mamba2_ssd_bwd_m1"
     _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
@@ -257,15 +271,20 @@ def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bia
         _check_tensor(op, "pre_gate", pre_gate)
         if pre_gate.shape != x.shape:
             raise RuntimeError(f"{op}: pre_gate shape must match x")
+    if chunk_states is not None:
+        _check_tensor(op, "chunk_states", chunk_states)
+        want = (x.shape[0], x.shape[2], _nchunks(x), x.shape[3], B.shape[3])
+        if tuple(chunk_states.shape) != want:
+            raise RuntimeError(f"{op}: chunk_states must have shape [B,H,ceil(L/64),P,N] = {list(want)}")
     grads = _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
                      chunk_size, dt_softplus, dt_limit_min, dt_limit_max,
-                     pre_gate if z is not None else None)
+                     pre_gate if z is not None else None, chunk_states)
     return tuple(_empty_like_or_none(g, x) for g in grads)
 
 
 def _op_bwd_meta(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bias=None,
                  initial_states=None,
-                 pre_gate=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
+                 pre_gate=None, chunk_states=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
                  dt_limit_max=3.402823466e+38):
     like = lambda t: x.new_empty(0) if t is None else torch.empty_like(t)  # noqa: E731
     return (torch.empty_like(x), torch.empty_like(dt), torch.empty_like(A), torch.empty_like(B),
@@ -343,8 +362,9 @@ def _can_use_native_bwd_m1(x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_st
 
 
 class _Mamba2SsdAutogradM1(torch.autograd.Function):
-    """Autograd contract of mamba2.py:1661-1838: saves the inputs, recomputes
-    the forward intermediates in backward, returns 13 gradients."""
+    """Autograd contract of mamba2.py:1661-1838: saves the inputs, the
+    chunk-start states (and pre_gate with z), recomputes the other forward
+    intermediates in backward, returns 13 gradients."""
 
     @staticmethod
     def forward(ctx, x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus,
@@ -353,10 +373,12 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
                       initial_states, dt_limit_min, dt_limit_max)
         # the pre-gate output y + D x is saved when z is present (dz needs it),
         # as the reference's Train forward does (mamba2.py:1682-1770)
-        out, final_state, pre_gate = _fwd_raw(
+        # and so are the chunk-start states (the reference's training forward
+        # returns states_start for its backward, mamba2.py:228,322,408-418)
+        out, final_state, pre_gate, states = _fwd_raw(
             x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
             float(dt_limit_min), float(dt_limit_max), want_final=True,
-            want_pre_gate=z is not None)
+            want_pre_gate=z is not None, want_states=True)
         empty = x.new_empty(0)
         ctx.save_for_backward(
             x, dt, A, B, C,
@@ -365,6 +387,7 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
             dt_bias if dt_bias is not None else empty,
             initial_states if initial_states is not None else empty,
             pre_gate if pre_gate is not None else empty,
+            states,
         )
         ctx.has = (D is not None, z is not None, dt_bias is not None, initial_states is not None)
         ctx.chunk_size = int(chunk_size)
@@ -374,7 +397,7 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, dfinal_state):
-        x, dt, A, B, C, D, z, dt_bias, initial_states, pre_gate = ctx.saved_tensors
+        x, dt, A, B, C, D, z, dt_bias, initial_states, pre_gate, states = ctx.saved_tensors
         has_D, has_z, has_bias, has_init = ctx.has
         if dout is None:
             dout = torch.zeros_like(x)
@@ -382,7 +405,7 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
             x, dt, A, B, C, dout.contiguous(),
             None if dfinal_state is None else dfinal_state.contiguous(),
             D if has_D else None, z if has_z else None, dt_bias if has_bias else None,
-            initial_states if has_init else None, pre_gate if has_z else None,
+            initial_states if has_init else None, pre_gate if has_z else None, states,
             ctx.chunk_size, ctx.dt_softplus, ctx.dt_limit[0], ctx.dt_limit[1])
         dx, ddt, dA, dB, dC, dD, dz, ddt_bias, dinit = grads
         return (dx, ddt, dA, dB, dC, None,
@@ -428,7 +451,7 @@ def mamba2_ssd_fwd(
     else:
         _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
                       initial_states, lo, hi)
-        out, final_state, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
+        out, final_state, _, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
                                     dt_softplus, lo, hi, want_final=return_final_state)
     if return_final_state:
         return out, final_state

@@ -38,7 +38,8 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 constexpr uint32_t kKnownFlags = MAMBA2_SSD_DT_SOFTPLUS | MAMBA2_SSD_HAS_D |
                                  MAMBA2_SSD_D_PER_CHANNEL | MAMBA2_SSD_HAS_Z |
-                                 MAMBA2_SSD_HAS_DT_BIAS | MAMBA2_SSD_HAS_INITIAL;
+                                 MAMBA2_SSD_HAS_DT_BIAS | MAMBA2_SSD_HAS_INITIAL |
+                                 MAMBA2_SSD_SAVED_STATES;
 
 int check_shape(const Mamba2SsdShape *s, uint32_t flags) {
     if (!s) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "shape is NULL");
@@ -193,6 +194,13 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
                     "initial_states pointer and HAS_INITIAL flag disagree");
     if (!(a->dt_limit_min <= a->dt_limit_max))
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "dt_limit_min > dt_limit_max");
+    if (bool(f & MAMBA2_SSD_SAVED_STATES) != (a->chunk_states != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "chunk_states pointer and SAVED_STATES flag disagree");
+    if ((f & MAMBA2_SSD_SAVED_STATES) && !(s->headdim == 64 && s->dstate == 64))
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
+                    "SAVED_STATES needs headdim == dstate == 64 (got %lld, %lld)",
+                    (long long)s->headdim, (long long)s->dstate);
     const size_t need = fwd_ws_bytes(s);
     if (need && (!workspace || workspace_bytes < need))
         return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need,
@@ -212,6 +220,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     prm.out = a->out;
     prm.final_state = a->final_state;
     prm.pre_gate = (f & MAMBA2_SSD_HAS_Z) ? a->pre_gate : nullptr;
+    prm.chunk_states = a->chunk_states;
     prm.L = s->seqlen;
     prm.H = (int)s->nheads;
     prm.G = (int)s->ngroups;
@@ -284,20 +293,21 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     return ok();
 }
 
-// Backward workspace: states [B,H,K,P,N] | log decay [B,H,K] | dstates [B,H,K,P,N]
+// Backward workspace: states [B,H,K,P,N] (unless SAVED_STATES) | log decay [B,H,K]
+// | dstates [B,H,K,P,N]
 // | dA partials [B,H,K] | ddt_bias partials [B,H,K,slots] | dD partials
 // [B,H,K,slots,P] (slots = one per consumer wave of the chunk kernel).
 struct BwdLayout {
     size_t states, log_decay, dstates, part_dA, part_db, part_dD, total;
 };
 
-BwdLayout bwd_layout(const Mamba2SsdShape *s) {
+BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
     const size_t bhk = (size_t)s->batch * s->nheads * nchunks(s);
     const size_t pn = (size_t)s->headdim * s->dstate;
     BwdLayout l{};
     size_t off = 0;
-    l.states = off;
-    off += align256(bhk * pn * sizeof(float));
+    l.states = off; // absent when the forward's chunk states are passed in
+    if (!(flags & MAMBA2_SSD_SAVED_STATES)) off += align256(bhk * pn * sizeof(float));
     l.log_decay = off;
     off += align256(bhk * sizeof(float));
     l.dstates = off;
@@ -317,10 +327,15 @@ constexpr int64_t kBwdUnits = 1024;
 
 bool bwd_supported(const Mamba2SsdShape *s) { return s->headdim == 64 && s->dstate == 64; }
 
-size_t bwd_ws_bytes(const Mamba2SsdShape *s) {
+size_t bwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags) {
     if (!bwd_supported(s) || s->seqlen == 0) return 0;
-    return bwd_layout(s).total;
+    return bwd_layout(s, flags).total;
 }
+
+// The reverse state-gradient pass walks each (b, h) stream serially; with
+// fewer streams than this it runs as a chunk-parallel dS_off kernel plus an
+// elementwise reverse recurrence instead.
+constexpr int64_t kMinRevStreams = 512;
 
 int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes, void *stream,
              Trace *tr) {
@@ -350,13 +365,16 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
                     "initial_states / dinitial_states pointers and HAS_INITIAL flag disagree");
     if (!(a->dt_limit_min <= a->dt_limit_max))
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "dt_limit_min > dt_limit_max");
+    if (bool(f & MAMBA2_SSD_SAVED_STATES) != (a->chunk_states != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "chunk_states pointer and SAVED_STATES flag disagree");
     if (!bwd_supported(s))
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
                     "mamba2_ssd_bwd_m1 needs headdim == dstate == 64 (got %lld, %lld)",
                     (long long)s->headdim, (long long)s->dstate);
     if (s->seqlen == 0)
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "mamba2_ssd_bwd_m1 needs seqlen > 0");
-    const BwdLayout lay = bwd_layout(s);
+    const BwdLayout lay = bwd_layout(s, f);
     if (!workspace || workspace_bytes < lay.total)
         return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", lay.total,
                     workspace ? workspace_bytes : (size_t)0);
@@ -365,7 +383,8 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     const int B = (int)s->batch, H = (int)s->nheads, K = (int)nchunks(s);
     const int PN = 64 * 64;
 
-    // forward recompute of the chunk-start states
+    // parameters of the chunk-state recompute (skipped when the forward's
+    // chunk states are passed in)
     ssd::FwdParams fp{};
     fp.x = a->x;
     fp.dt = a->dt;
@@ -374,7 +393,8 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     fp.C = a->C;
     fp.dt_bias = a->dt_bias;
     fp.init = a->initial_states;
-    fp.states = (float *)(ws + lay.states);
+    const bool saved = (f & MAMBA2_SSD_SAVED_STATES) != 0;
+    fp.states = saved ? const_cast<float *>(a->chunk_states) : (float *)(ws + lay.states);
     fp.chunk_log_decay = (float *)(ws + lay.log_decay);
     fp.L = s->seqlen;
     fp.H = H;
@@ -422,16 +442,26 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     const dim3 chunk_grid(K, H, B);
     const dim3 state_grid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * H);
     if (int rc = record(tr, st, nullptr)) return rc;
-    hipLaunchKernelGGL((ssd::k_chunk_state<64, 64>), chunk_grid, dim3(ssd::kThreads), 0, st, fp);
-    if (int rc = launch_status("k_chunk_state", tr, st)) return rc;
-    hipLaunchKernelGGL(ssd::k_state_pass, state_grid, dim3(ssd::kThreads), 0, st, fp.states,
-                       fp.chunk_log_decay, fp.init, fp.states, (float *)nullptr, K, PN);
-    if (int rc = launch_status("k_state_pass", tr, st)) return rc;
-    hipLaunchKernelGGL(ssd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);
-    if (int rc = launch_status("k_bwd_dstate", tr, st)) return rc;
-    hipLaunchKernelGGL(ssd::k_state_pass_bwd, state_grid, dim3(ssd::kThreads), 0, st, bp.dstates,
-                       fp.chunk_log_decay, a->dfinal_state, a->dinitial_states, K, PN);
-    if (int rc = launch_status("k_state_pass_bwd", tr, st)) return rc;
+    if (!saved) {
+        // forward recompute of the chunk-start states
+        hipLaunchKernelGGL((ssd::k_chunk_state<64, 64>), chunk_grid, dim3(ssd::kThreads), 0, st, fp);
+        if (int rc = launch_status("k_chunk_state", tr, st)) return rc;
+        hipLaunchKernelGGL(ssd::k_state_pass, state_grid, dim3(ssd::kThreads), 0, st, fp.states,
+                           fp.chunk_log_decay, fp.init, fp.states, (float *)nullptr, K, PN);
+        if (int rc = launch_status("k_state_pass", tr, st)) return rc;
+    }
+    // state gradients dU_k (and dinitial_states)
+    if ((int64_t)B * H >= kMinRevStreams) {
+        hipLaunchKernelGGL(ssd::k_bwd_dstate_rev, dim3((unsigned)(B * H)), dim3(ssd::kWsThreads), 0,
+                           st, bp, a->dfinal_state, a->dinitial_states);
+        if (int rc = launch_status("k_bwd_dstate_rev", tr, st)) return rc;
+    } else {
+        hipLaunchKernelGGL(ssd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);
+        if (int rc = launch_status("k_bwd_dstate", tr, st)) return rc;
+        hipLaunchKernelGGL(ssd::k_state_pass_bwd, state_grid, dim3(ssd::kThreads), 0, st, bp.dstates,
+                           fp.chunk_log_decay, a->dfinal_state, a->dinitial_states, K, PN);
+        if (int rc = launch_status("k_state_pass_bwd", tr, st)) return rc;
+    }
     // chunk backward: (b, g, run of chunks) work units, about kBwdUnits of them
     const int64_t bg = (int64_t)B * s->ngroups;
     int64_t nseg = (kBwdUnits + bg - 1) / bg;
@@ -496,7 +526,7 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
 int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes) {
     if (int rc = check_shape(shape, flags)) return rc;
     if (!bytes) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "bytes is NULL");
-    *bytes = bwd_ws_bytes(shape);
+    *bytes = bwd_ws_bytes(shape, flags);
     return ok();
 }
 

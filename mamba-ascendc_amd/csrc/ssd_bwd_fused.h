@@ -40,6 +40,7 @@
 #include <type_traits>
 
 #include "ssd_bwd_kernels.h"
+#include "ssd_fwd_fused.h"
 
 namespace ssd {
 
@@ -531,6 +532,165 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     case 1: consumer(std::integral_constant<int, 1>{}); break;
     case 2: consumer(std::integral_constant<int, 2>{}); break;
     default: consumer(std::integral_constant<int, 3>{}); break;
+    }
+}
+
+// Reverse state-gradient pass, one workgroup per (b, h) stream walking the
+// chunks from last to first with the state gradient g in registers:
+//   dU_k = g;   g <- dSoff_k + exp(cs_last_k) g,   dSoff_k = (gy exp(cs))^T C
+// starting from g = dfinal_state; g at the end is dinitial_states.  dU_k (the
+// gradient of the state leaving chunk k) goes to prm.dstates.  The per-chunk
+// dS_off never reaches HBM.  Producer waves stage gy exp(cs) and C of the next
+// chunk (token-major, split fp16) while the consumer waves run the product
+// dSoff^T[n][p] = sum_t C[t][n] (gy exp(cs))[t][p], read transposed from LDS.
+// The recurrence is that of mamba_ascendc/csrc/ops/mamba2_ssd_state_passing_bwd
+// (state_passing_bwd/design.md:44-61) with the dS_off product fused in.
+__global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, const float *dfinal,
+                                                                float *dinit) {
+    constexpr int T = 64, P = 64, N = 64;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[8 * kTile]; // GE(s), CT(s), s = 0, 1
+    __shared__ float s_alpha[2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int w = wave & 3, r16 = lane & 15, kq = lane >> 4;
+    auto GE = [&](int s) { return tile_at(lds, 2 * s); };
+    auto CT = [&](int s) { return tile_at(lds, 2 * s + 1); };
+    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, prm.R);
+    const int r = u % prm.R, bg = u / prm.R;
+    const int g = bg % prm.G, b = bg / prm.G, h = g * prm.R + r;
+    const int H = prm.H, G = prm.G, K = prm.K;
+    const int rowHP4 = H * P * 4, rowGN4 = G * N * 4;
+    auto tvalid = [&](int k) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
+
+    if (wave >= 4) {
+        // ---------------------------------------------------------- producers
+        // ring of kDepth register slots; step i (chunk K - 1 - i) uses slot i % kDepth
+        constexpr int kDepth = 3;
+        const int pt = tid - 4 * kWave;
+        const int rt = pt >> 4, c4 = (pt & 15) * 4; // rows rt + 16 j, columns c4 .. c4 + 3
+        const bool has_dout = prm.dout != nullptr, has_z = prm.has_z != 0;
+        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float Ah2 = prm.A[h] * kLog2e;
+        const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
+        float4 gr[kDepth][4], zr[kDepth][4], cr[kDepth][4];
+        float dtr[kDepth];
+        auto p_load = [&](int i, auto slot_c) {
+            constexpr int sl = decltype(slot_c)::value;
+            const int k = K - 1 - i, tv = tvalid(k);
+            const int64_t t0 = (int64_t)k * T;
+            const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
+            const auto rd = buf_rsrc(has_dout ? prm.dout + xo : prm.x + xo);
+            const auto rz = buf_rsrc(has_z ? prm.z + xo : prm.x + xo);
+            const auto rc = buf_rsrc(prm.C + (((int64_t)b * prm.L + t0) * G + g) * N);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = rt + 16 * j < tv;
+                gr[sl][j] = (ok && has_dout) ? buf_load4(rd, rt * rowHP4 + c4 * 4, 16 * j * rowHP4) : z4;
+                if (has_z) zr[sl][j] = ok ? buf_load4(rz, rt * rowHP4 + c4 * 4, 16 * j * rowHP4) : z4;
+                cr[sl][j] = ok ? buf_load4(rc, rt * rowGN4 + c4 * 4, 16 * j * rowGN4) : z4;
+            }
+            dtr[sl] = lane < tv ? prm.dt[((int64_t)b * prm.L + t0 + lane) * H + h] : 0.f;
+        };
+        auto put = [&](SplitTile d, int row, float4 v) {
+            half4 vh, vl;
+            split4(v, vh, vl);
+            *(half4 *)&d.hi[row * kTS + c4] = vh;
+            *(half4 *)&d.lo[row * kTS + c4] = vl;
+        };
+        auto p_stage = [&](int i, int s, auto slot_c) {
+            constexpr int sl = decltype(slot_c)::value;
+            const int tv = tvalid(K - 1 - i);
+            float a = 0.f;
+            if (lane < tv) a = Ah2 * discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
+            const float cs = wave_inclusive_scan(a); // log2 units
+            if (w == 0 && lane == 0) s_alpha[s] = exp2_f(readlane_f(cs, T - 1));
+            const float ecs = exp2_f(cs);
+            const SplitTile ge = GE(s), ct = CT(s);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = rt + 16 * j;
+                const float e = __shfl(ecs, row, kWave);
+                float4 v = gr[sl][j];
+                if (has_z) {
+                    v.x *= silu_f(zr[sl][j].x);
+                    v.y *= silu_f(zr[sl][j].y);
+                    v.z *= silu_f(zr[sl][j].z);
+                    v.w *= silu_f(zr[sl][j].w);
+                }
+                put(ge, row, make_float4(v.x * e, v.y * e, v.z * e, v.w * e));
+                put(ct, row, cr[sl][j]);
+            }
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        static_assert(kDepth == 3, "the unrolled ring below assumes three slots");
+        if (0 < K) p_load(0, S0{});
+        if (1 < K) p_load(1, S1{});
+        if (2 < K) p_load(2, S2{});
+        if (0 < K) {
+            p_stage(0, 0, S0{});
+            if (3 < K) p_load(3, S0{});
+        }
+        lds_barrier();
+        auto p_iter = [&](int i, auto slot_next) {
+            if (i + 1 < K) {
+                p_stage(i + 1, (i + 1) & 1, slot_next);
+                if (i + 1 + kDepth < K) p_load(i + 1 + kDepth, slot_next);
+            }
+            lds_barrier();
+        };
+        for (int i0 = 0; i0 < K; i0 += kDepth) {
+            p_iter(i0, S1{});
+            if (i0 + 1 < K) p_iter(i0 + 1, S2{});
+            if (i0 + 2 < K) p_iter(i0 + 2, S0{});
+        }
+        return;
+    }
+
+    // -------------------------------------------------------------- consumers
+    // g[p = 16 pb + l % 16][n = 16 w + 4 (l / 16) + i] in gs[pb][i]
+    f32x4 gs[4];
+    const int64_t bh = (int64_t)b * H + h;
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb) {
+        if (dfinal) {
+            const float4 v = *(const float4 *)(dfinal + bh * (P * N) + (16 * pb + r16) * N + 16 * w + 4 * kq);
+            gs[pb] = f32x4{v.x, v.y, v.z, v.w};
+        } else {
+            gs[pb] = zero4();
+        }
+    }
+    lds_barrier();
+    for (int i = 0; i < K; ++i) {
+        const int k = K - 1 - i, s = i & 1;
+        float *du = prm.dstates + (bh * K + k) * (int64_t)(P * N);
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+            *(float4 *)(du + (16 * pb + r16) * N + 16 * w + 4 * kq) =
+                make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
+        const SplitTile ge = GE(s), ct = CT(s);
+        f32x4 U[4];
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb) U[pb] = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const Frag a = frag_tn(ct, ks, 16 * w);
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a, frag_tn(ge, ks, 16 * pb), U[pb]);
+        }
+        const float alpha = s_alpha[s];
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) gs[pb][ii] = alpha * gs[pb][ii] + U[pb][ii];
+        lds_barrier(); // buffer s is free, buffer s ^ 1 is staged
+    }
+    if (dinit) {
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+            *(float4 *)(dinit + bh * (P * N) + (16 * pb + r16) * N + 16 * w + 4 * kq) =
+                make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
     }
 }
 

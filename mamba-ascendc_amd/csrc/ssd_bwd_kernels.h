@@ -5,7 +5,8 @@
 // inclusive cumsum of A*q, S_k the state entering chunk k, gy = dout * silu(z)
 // (or dout), decay_t = exp(cs_last - cs_t):
 //
-//   k_bwd_dstate      : dSoff_k[p][n] = sum_t gy_t[p] exp(cs_t) C_t[n]
+//   k_bwd_dstate      : dSoff_k[p][n] = sum_t gy_t[p] exp(cs_t) C_t[n] (and the
+//                       chunk log decay cs_last)
 //   k_state_pass_bwd  : reverse recurrence over chunks, in place:
 //                         dU_k = g_{k+1};  g_k = dSoff_k + exp(cs_last_k) g_{k+1}
 //                       with g_K = dfinal_state and dinitial_states = g_0
@@ -27,7 +28,7 @@ struct BwdParams {
     const float *x, *dt, *A, *B, *C, *D, *z, *dt_bias, *dout, *pre_gate;
     float *dx, *ddt, *dB, *dC, *dz;
     const float *states;    // [B, H, K, P, N] state entering each chunk
-    const float *log_decay; // [B, H, K] chunk sum of A q
+    float *log_decay;       // [B, H, K] chunk sum of A q (written by k_bwd_dstate)
     float *dstates;         // [B, H, K, P, N]: dSoff, then dU
     float *part_dA;         // [B, H, K]
     float *part_dbias;      // [B, H, K]
@@ -78,6 +79,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dstate(BwdParams prm) {
     if (w == 0) {
         const float cs = bwd_prologue(prm, b, h, t0, tv, s_q, s_cs, s_dqdu);
         s_e[lane] = __expf(cs);
+        if (lane == T - 1) prm.log_decay[((int64_t)b * prm.H + h) * prm.K + k] = cs;
     }
     __syncthreads();
 

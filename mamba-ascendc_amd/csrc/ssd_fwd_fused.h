@@ -258,6 +258,14 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             const int tv = (int)min((int64_t)T, prm.L - t0);
             const float cs_last = s_cs[s][T - 1];
             log_decay_sum += cs_last;
+            if (!kStateOnly && prm.chunk_states) {
+                // saved for the backward: the state entering chunk k
+                float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * (int64_t)(P * N);
+    #pragma unroll
+                for (int pb = 0; pb < 4; ++pb)
+                    *(float4 *)(cst + (16 * pb + r16) * N + 16 * W + 4 * kq) =
+                        make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
+            }
             const SplitTile t2 = T2(s), t3 = T3(s);
             if (!kStateOnly) {
                 Frag Cown[2];

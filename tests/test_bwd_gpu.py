@@ -80,6 +80,9 @@ CASES = [
     ([2, 192, 4, 64, 64, 64, 2], ("bias",), True, (0.0, math.inf), "out"),    # output-only
     ([2, 192, 4, 64, 64, 128, 2], ("init",), True, (0.0, math.inf), "final"), # final-only
     ([1, 320, 16, 64, 64, 64, 2], ("D",), True, (0.0, math.inf), "both"),    # 8 heads per group
+    # >= 512 (b, h) streams: the fused reverse state-gradient pass
+    ([2, 200, 256, 64, 64, 64, 64], ("D2", "z", "bias", "init"), True, (0.0, math.inf), "both"),
+    ([1, 192, 512, 64, 64, 64, 128], (), True, (0.0, math.inf), "final"),
 ]
 
 
@@ -140,3 +143,62 @@ def test_backward_baseline_config4():
         _say(f"  d{k:<3} maxabs {ma:.3e} relL2 {rl:.3e} cos {cos:.9f}")
         assert rl <= 5e-3 and ma <= 2e-2, (k, ma, rl)
         assert cos >= 0.999, (k, cos)
+
+
+def test_forward_chunk_states_are_prefix_final_states():
+    """The training forward's chunk_states[:, :, k] is the state entering chunk
+    k: the oracle's final state of the first 64 k tokens (the initial state
+    for k = 0)."""
+    _need_gpu()
+    from ascend_kernel import mamba2 as api
+
+    shape = [2, 200, 4, 64, 64, 64, 2]
+    _say(f"chunk states {shape}")
+    inp = make_inputs(shape, seed=8, features=("bias", "init"))
+    dev = {k: v.cuda() for k, v in inp.items()}
+    _, _, _, states = api._fwd_raw(dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"], None, None,
+                                   dev["dt_bias"], dev["initial_states"], 64, True, 0.0, math.inf,
+                                   want_states=True)
+    states = states.cpu()
+    assert states.shape == (2, 4, 4, 64, 64)
+    for k in range(4):
+        l = 64 * k
+        if l == 0:
+            want = inp["initial_states"].double()
+        else:
+            _, want = ssd_chunk_scan_ref(
+                inp["x"][:, :l].double(), inp["dt"][:, :l].double(), inp["A"].double(),
+                inp["B"][:, :l].double(), inp["C"][:, :l].double(), 64,
+                dt_bias=inp["dt_bias"].double(), dt_softplus=True,
+                initial_states=inp["initial_states"].double(), return_final_state=True,
+                compute_dtype=torch.float64)
+        ma, rl = parity_metrics(states[:, :, k], want)
+        _say(f"  k={k} maxabs {ma:.3e} relL2 {rl:.3e}")
+        assert rl <= 1e-5, (k, rl)
+
+
+@pytest.mark.parametrize("shape", [[2, 130, 8, 64, 64, 64, 2], [2, 130, 256, 64, 64, 64, 64]],
+                         ids=["chunk-parallel-dstate", "reverse-dstate"])
+def test_backward_saved_states_match_recompute(shape):
+    """The backward from the forward's saved chunk states and the backward that
+    recomputes them give the same gradients."""
+    _need_gpu()
+    from ascend_kernel import mamba2 as api
+
+    _say(f"saved vs recomputed states {shape}")
+    inp = make_inputs(shape, seed=9, features=("D", "bias"))
+    dev = {k: v.cuda() for k, v in inp.items()}
+    args = (dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"])
+    out, fin, _, states = api._fwd_raw(*args, dev["D"], None, dev["dt_bias"], None, 64, True, 0.0,
+                                       math.inf, want_states=True)
+    dout, dfin = torch.randn_like(out), torch.randn_like(fin)
+    common = (dout, dfin, dev["D"], None, dev["dt_bias"], None, 64, True, 0.0, math.inf)
+    a = api._bwd_raw(*args, *common, chunk_states=states)
+    b = api._bwd_raw(*args, *common, chunk_states=None)
+    torch.cuda.synchronize()
+    for name, ga, gb in zip(("dx", "ddt", "dA", "dB", "dC", "dD", "dz", "ddt_bias", "dinit"), a, b):
+        if ga is None:
+            continue
+        ma, rl = parity_metrics(ga.cpu(), gb.cpu())
+        _say(f"  {name:<8} maxabs {ma:.3e} relL2 {rl:.3e}")
+        assert rl <= 1e-5, (name, rl)

@@ -99,7 +99,13 @@ def test_workspace_size_formula():
     assert ws(fwd, seqlen=0) == 0
     bwd = lib.mamba2_ssd_bwd_m1_workspace_size
     k = 4096 // 64
-    assert ws(bwd, batch=8, seqlen=4096, nheads=256, ngroups=64) >= 2 * 8 * 256 * k * 64 * 64 * 4
+    state_buf = 8 * 256 * k * 64 * 64 * 4
+    full = ws(bwd, batch=8, seqlen=4096, nheads=256, ngroups=64)
+    assert full >= 2 * state_buf
+    # with the forward's chunk states passed in, the recompute buffer goes away
+    assert bwd(ctypes.byref(_shape(batch=8, seqlen=4096, nheads=256, ngroups=64)), rt.SAVED_STATES,
+               ctypes.byref(nbytes)) == 0
+    assert full - nbytes.value == state_buf
 
 
 def test_fwd_rejects_null_and_flag_mismatch_without_gpu():
@@ -119,6 +125,13 @@ def test_fwd_rejects_null_and_flag_mismatch_without_gpu():
     args.dt_limit_min, args.dt_limit_max = 1.0, 0.5
     assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
     args.dt_limit_min, args.dt_limit_max = 0.0, math.inf
+    args.flags = rt.SAVED_STATES  # flag without the chunk_states pointer
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
+    assert "SAVED_STATES" in rt.last_error(lib)
+    args.chunk_states = fake
+    args.shape = _shape(dstate=128)  # chunk states are saved for the M1 spec only
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -2
+    args.shape, args.flags, args.chunk_states = _shape(), 0, None
     # fast-path shape without workspace
     assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -3
     assert lib.mamba2_ssd_fwd(None, None, 0, None) == -1
