@@ -468,8 +468,12 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     nseg = nseg < K ? nseg : K;
     const int M = (int)((K + nseg - 1) / nseg);
     nseg = (K + M - 1) / M;
-    hipLaunchKernelGGL(ssd::k_bwd_ws, dim3((unsigned)(bg * nseg)), dim3(ssd::kBwsThreads), 0, st, bp,
-                       (int)nseg, M);
+    if (bp.has_z)
+        hipLaunchKernelGGL(ssd::k_bwd_ws<true>, dim3((unsigned)(bg * nseg)), dim3(ssd::kBwsThreads), 0,
+                           st, bp, (int)nseg, M);
+    else
+        hipLaunchKernelGGL(ssd::k_bwd_ws<false>, dim3((unsigned)(bg * nseg)), dim3(ssd::kBwsThreads), 0,
+                           st, bp, (int)nseg, M);
     if (int rc = launch_status("k_bwd_ws", tr, st)) return rc;
     hipLaunchKernelGGL(ssd::k_bwd_finalize_slots, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
                        bp.part_dbias, bp.part_dD, a->dA, a->ddt_bias, a->dD, B, H, K, 64,

@@ -57,6 +57,19 @@ __device__ __forceinline__ half4 tr4(const _Float16 *arr, int k0, int c0) {
     return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
 }
 
+// The LDS array base as a value the optimizer cannot see through.  Tiles
+// past the first 64 KB of LDS cannot use the 16-bit immediate offset of the
+// ds instructions, so every (array, row, k-step) address there becomes a
+// register of its own; derived from this base, those addresses are formed
+// next to their use in each phase instead of being hoisted out of the step
+// loop and held (spilled) for its whole length.
+__device__ __forceinline__ _Float16 *opaque_lds(_Float16 *p) {
+    typedef __attribute__((address_space(3))) _Float16 *lptr;
+    uint32_t a = (uint32_t)(uintptr_t)(lptr)p;
+    asm volatile("" : "+s"(a));
+    return (_Float16 *)(lptr)(uintptr_t)a;
+}
+
 __device__ __forceinline__ half8 cat8(half4 a, half4 b) {
     return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
@@ -90,16 +103,21 @@ __device__ __forceinline__ f32x4 tile_acc(SplitTile s, int row0, int c0) {
                  (float)h[3] + (float)l[3]};
 }
 
+template <bool kHasZ>
 __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg, int M) {
     constexpr int T = 64, P = 64, N = 64;
-    __shared__ __attribute__((aligned(16))) _Float16 lds[12 * kTile];
-    // per-token values of a step, double buffered by step parity
+    // x and gy tiles double buffered by step parity (the epilogue of step n
+    // still reads them while step n + 1 runs); S, dU, B, C single
+    __shared__ __attribute__((aligned(16))) _Float16 lds[16 * kTile];
+    // per-token (and per-channel D) values of a step, double buffered by step parity
     __shared__ __attribute__((aligned(16))) float s_q[2][T], s_cs[2][T], s_dqdu[2][T], s_dte[2][T],
-        s_ecs[2][T];
-    __shared__ float s_dcs[2][T], s_rd[2][T], s_sdu[2][4];
+        s_ecs[2][T], s_D[2][P];
+    __shared__ float s_dcs[2][T], s_rd[2][T], s_sdu[2][4], s_A[2];
 
-    const SplitTile Xt = tile_at(lds, 0), Gt = tile_at(lds, 1), St = tile_at(lds, 2),
-                    Ut = tile_at(lds, 3), Bt = tile_at(lds, 4), Ct = tile_at(lds, 5);
+    auto Xt = [&](int par) { return tile_at(lds, par); };
+    auto Gt = [&](int par) { return tile_at(lds, 2 + par); };
+    const SplitTile St = tile_at(lds, 4), Ut = tile_at(lds, 5), Bt = tile_at(lds, 6),
+                    Ct = tile_at(lds, 7);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int r16 = lane & 15, kq = lane >> 4;
@@ -113,43 +131,58 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     auto tvalid = [&](int k) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
 
     // ------------------------------------------------------------ producers
+    // Every step issues the same global loads, unconditionally (rows past the
+    // sequence end re-read its last row and are zeroed when staged; steps past
+    // the run re-read its last step), so the load counts the compiler tracks
+    // are exact and a stage waits only for the loads it consumes, which were
+    // issued a step earlier.  The producers also write dz, which needs no
+    // product: dz = dout pre_gate silu'(z).
     if (wave >= 4) {
         const int pt = tid - 4 * kWave, pw = wave - 4;
         const int rt = pt >> 4, c4 = (pt & 15) * 4; // rows rt + 16 j, columns c4 .. c4 + 3
-        const bool has_dout = prm.dout != nullptr, has_z = prm.has_z != 0;
+        const bool has_dout = prm.dout != nullptr;
         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        float4 xr[4], gr[4], zr[4], sr[4], ur[4], br[4], cr[4];
-        float dtr = 0.f;
+        float4 xr[4], gr[4], zr[4], pr[4], sr[4], ur[4], br[4], cr[4];
+        float dtr = 0.f, Ahr = 0.f, biasr = 0.f, Dr = 0.f;
+        const float *dtb = prm.dt_bias ? prm.dt_bias : prm.A; // read unconditionally
+        const float *Dp = prm.has_D ? prm.D : prm.A;
         auto load_xg = [&](int n) {
+            n = min(n, NS - 1);
             const int k = kbeg + n / R, h = g * R + n % R, tv = tvalid(k);
             const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
             const auto rx = buf_rsrc(prm.x + xo);
             const auto rd = buf_rsrc(has_dout ? prm.dout + xo : prm.x + xo);
-            const auto rz = buf_rsrc(has_z ? prm.z + xo : prm.x + xo);
-            const int lo = rt * rowHP4 + c4 * 4;
+            const auto rz = buf_rsrc(kHasZ ? prm.z + xo : prm.x + xo);
+            const auto rp = buf_rsrc(kHasZ ? prm.pre_gate + xo : prm.x + xo);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const bool ok = rt + 16 * j < tv;
-                xr[j] = ok ? buf_load4(rx, lo, 16 * j * rowHP4) : z4;
-                gr[j] = (ok && has_dout) ? buf_load4(rd, lo, 16 * j * rowHP4) : z4;
-                if (has_z) zr[j] = ok ? buf_load4(rz, lo, 16 * j * rowHP4) : z4;
+                const int lo = min(rt + 16 * j, tv - 1) * rowHP4 + c4 * 4;
+                xr[j] = buf_load4(rx, lo, 0);
+                gr[j] = buf_load4(rd, lo, 0);
+                if (kHasZ) {
+                    zr[j] = buf_load4(rz, lo, 0);
+                    pr[j] = buf_load4(rp, lo, 0);
+                }
             }
-            if (pw == 0)
-                dtr = lane < tv ? prm.dt[((int64_t)b * prm.L + (int64_t)k * T + lane) * H + h] : 0.f;
+            dtr = prm.dt[((int64_t)b * prm.L + (int64_t)k * T + min(lane, tv - 1)) * H + h];
+            Dr = Dp[prm.has_D && prm.d_per_channel ? h * P + lane : h];
+            Ahr = prm.A[h];
+            biasr = dtb[h];
         };
-        auto load_bc = [&](int k) {
-            const int tv = tvalid(k);
+        auto load_bc = [&](int n) {
+            n = min(n, NS - 1);
+            const int k = kbeg + n / R, tv = tvalid(k);
             const int64_t o = (((int64_t)b * prm.L + (int64_t)k * T) * G + g) * N;
             const auto rb = buf_rsrc(prm.B + o), rc = buf_rsrc(prm.C + o);
-            const int lo = rt * rowGN4 + c4 * 4;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const bool ok = rt + 16 * j < tv;
-                br[j] = ok ? buf_load4(rb, lo, 16 * j * rowGN4) : z4;
-                cr[j] = ok ? buf_load4(rc, lo, 16 * j * rowGN4) : z4;
+                const int lo = min(rt + 16 * j, tv - 1) * rowGN4 + c4 * 4;
+                br[j] = buf_load4(rb, lo, 0);
+                cr[j] = buf_load4(rc, lo, 0);
             }
         };
         auto load_su = [&](int n) {
+            n = min(n, NS - 1);
             const int k = kbeg + n / R, h = g * R + n % R;
             const int64_t so = (((int64_t)b * H + h) * K + k) * (int64_t)(P * N);
             const auto rs = buf_rsrc(prm.states + so), ru = buf_rsrc(prm.dstates + so);
@@ -168,25 +201,39 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         };
         auto stage_xg = [&](int n) {
             const int par = n & 1, k = kbeg + n / R, h = g * R + n % R, tv = tvalid(k);
+            const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
+            const SplitTile xt = Xt(par), gt = Gt(par);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                put(Xt, rt + 16 * j, xr[j]);
-                float4 v = gr[j];
-                if (has_z) {
-                    v.x *= silu_f(zr[j].x);
-                    v.y *= silu_f(zr[j].y);
-                    v.z *= silu_f(zr[j].z);
-                    v.w *= silu_f(zr[j].w);
+                const int row = rt + 16 * j;
+                const bool ok = row < tv;
+                put(xt, row, ok ? xr[j] : z4);
+                const float4 dv = (ok && has_dout) ? gr[j] : z4;
+                float4 v = dv;
+                if (kHasZ) {
+                    const float zz[4] = {zr[j].x, zr[j].y, zr[j].z, zr[j].w};
+                    const float pp[4] = {pr[j].x, pr[j].y, pr[j].z, pr[j].w};
+                    const float dd[4] = {dv.x, dv.y, dv.z, dv.w};
+                    float gv[4], dzv[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float sgm = sigmoid_f(zz[i]);
+                        gv[i] = dd[i] * zz[i] * sgm;
+                        dzv[i] = dd[i] * pp[i] * sgm * (1.f + zz[i] * (1.f - sgm));
+                    }
+                    v = make_float4(gv[0], gv[1], gv[2], gv[3]);
+                    if (ok) *(float4 *)(prm.dz + xo + (int64_t)row * H * P + c4) =
+                        make_float4(dzv[0], dzv[1], dzv[2], dzv[3]);
                 }
-                put(Gt, rt + 16 * j, v);
+                put(gt, row, v);
             }
             if (pw == 0) {
                 float q = 0.f, a = 0.f, dq = 0.f;
+                const float bias = prm.dt_bias ? biasr : 0.f;
                 if (lane < tv) {
-                    const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
                     q = discretize_dt(dtr, bias, prm.softplus != 0, prm.lo, prm.hi);
                     dq = discretize_grad(dtr, bias, prm.softplus != 0, prm.lo, prm.hi);
-                    a = prm.A[h] * kLog2e * q;
+                    a = Ahr * kLog2e * q;
                 }
                 const float cs = wave_inclusive_scan(a); // log2 units
                 const float last = readlane_f(cs, T - 1);
@@ -195,13 +242,17 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 s_dqdu[par][lane] = dq;
                 s_dte[par][lane] = exp2_f(last - cs);
                 s_ecs[par][lane] = exp2_f(cs);
+                s_D[par][lane] = prm.has_D ? Dr : 0.f;
+                if (lane == 0) s_A[par] = Ahr;
             }
         };
-        auto stage_bc = [&]() {
+        auto stage_bc = [&](int n) {
+            const int tv = tvalid(kbeg + n / R);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                put(Bt, rt + 16 * j, br[j]);
-                put(Ct, rt + 16 * j, cr[j]);
+                const bool ok = rt + 16 * j < tv;
+                put(Bt, rt + 16 * j, ok ? br[j] : z4);
+                put(Ct, rt + 16 * j, ok ? cr[j] : z4);
             }
         };
         auto stage_su = [&](int n) {
@@ -217,48 +268,44 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         };
 
         load_xg(0);
-        load_bc(kbeg);
+        load_bc(0);
         load_su(0);
         stage_xg(0);
-        stage_bc();
-        if (NS > 1) {
-            load_xg(1);
-            if (1 % R == 0) load_bc(kbeg + 1);
-        }
+        stage_bc(0);
+        load_xg(1);
+        load_bc(1);
         lds_barrier();
-        // every step: two barriers, as in the consumer loop
+        // every step: two barriers, as in the consumer loop; the B, C loads
+        // of a step fetch the chunk of step n + 2 (L2 hits within a chunk)
         for (int n = 0; n < NS; ++n) {
             stage_su(n);
-            if (n + 1 < NS) load_su(n + 1);
+            load_su(n + 1);
             lds_barrier();
             if (n + 1 < NS) {
                 stage_xg(n + 1);
-                if ((n + 1) % R == 0) stage_bc();
+                if ((n + 1) % R == 0) stage_bc(n + 1);
             }
-            if (n + 2 < NS) {
-                load_xg(n + 2);
-                if ((n + 2) % R == 0) load_bc(kbeg + (n + 2) / R);
-            }
+            load_xg(n + 2);
+            load_bc(n + 2);
             lds_barrier();
         }
         return;
     }
 
     // ------------------------------------------------------------ consumers
+    // No global loads: every operand comes from LDS, every output is a store.
     auto consumer = [&](auto wave_c) {
         constexpr int W = decltype(wave_c)::value;
-        const int own = 16 * W + r16;   // operand row of this lane
+        const int own = 16 * W + r16;     // operand row of this lane
         const int trow = 16 * W + 4 * kq; // first of the 4 accumulator rows of this lane
-        f32x4 dBa[4], dCa[4];
-        // carried from phase B of a step to its epilogue
-        f32x4 dxa[4], xa[4], ga[4];
-        float dqp[4];
+        f32x4 dBa[4], dCa[4], dxa[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             dBa[i] = zero4();
             dCa[i] = zero4();
         }
 
+        // epilogue of step n (dxa holds its dxdt)
         auto epilogue = [&](int n) {
             const int k = kbeg + n / R, h = g * R + n % R, par = n & 1;
             const int64_t t0 = (int64_t)k * T;
@@ -273,8 +320,17 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 const float dA_p = wave_sum(da * s_q[par][lane]);
                 if (lane == 0) prm.part_dA[bhk] = dA_p;
             }
-            const float Ah = prm.A[h];
+            const float Ah = s_A[par];
             const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
+            f32x4 xa[4], ga[4];
+            float Dv[4];
+            _Float16 *le = opaque_lds(lds);
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) {
+                xa[pb] = tile_acc(tile_at(le, par), 16 * W, 16 * pb);
+                ga[pb] = tile_acc(tile_at(le, 2 + par), 16 * W, 16 * pb);
+                Dv[pb] = s_D[par][prm.d_per_channel ? 16 * pb + r16 : 0];
+            }
             float dbias = 0.f, dDp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
@@ -282,30 +338,18 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 const bool valid = t < tv;
                 const float da_t = __shfl(da, t, kWave);
                 const float q_t = s_q[par][t];
-                const float ddt = valid ? (Ah * da_t + dqp[rr]) * s_dqdu[par][t] : 0.f;
+                const float dqp = sum16(xa[0][rr] * dxa[0][rr] + xa[1][rr] * dxa[1][rr] +
+                                        xa[2][rr] * dxa[2][rr] + xa[3][rr] * dxa[3][rr]);
+                const float ddt = valid ? (Ah * da_t + dqp) * s_dqdu[par][t] : 0.f;
                 if (r16 == 0) {
                     if (valid) prm.ddt[((int64_t)b * prm.L + t0 + t) * H + h] = ddt;
                     dbias += ddt;
                 }
 #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) {
-                    const int c = 16 * pb + r16;
-                    const float gyv = ga[pb][rr], xv = xa[pb][rr];
-                    float dxv = q_t * dxa[pb][rr];
-                    if (prm.has_D) {
-                        const float Dv = prm.d_per_channel ? prm.D[h * P + c] : prm.D[h];
-                        dxv += Dv * gyv;
-                        dDp[pb] += gyv * xv;
-                    }
-                    if (valid) {
-                        const int64_t o = xo + (int64_t)t * H * P + c;
-                        prm.dx[o] = dxv;
-                        if (prm.has_z) {
-                            const float zv = prm.z[o], sgm = sigmoid_f(zv);
-                            const float dov = prm.dout ? prm.dout[o] : 0.f;
-                            prm.dz[o] = dov * prm.pre_gate[o] * sgm * (1.f + zv * (1.f - sgm));
-                        }
-                    }
+                    const float gyv = ga[pb][rr];
+                    dDp[pb] += gyv * xa[pb][rr];
+                    if (valid) prm.dx[xo + (int64_t)t * H * P + 16 * pb + r16] = q_t * dxa[pb][rr] + Dv[pb] * gyv;
                 }
             }
             dbias = wave_sum(dbias);
@@ -328,119 +372,124 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         for (int n = 0; n < NS; ++n) {
             const int k = kbeg + n / R, r = n % R, par = n & 1;
             if (n > 0) epilogue(n - 1);
+            _Float16 *la = opaque_lds(lds);
+            const SplitTile xt = tile_at(la, par), gt = tile_at(la, 2 + par);
+            const SplitTile Bt = tile_at(la, 6), Ct = tile_at(la, 7);
 
             // ---------------- phase A: x, gy, B, C
             const float *q_ = s_q[par], *cs_ = s_cs[par];
-            Frag Bo[2], Co[2], Go[2], Xo[2];
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                Bo[ks] = frag(Bt, own, ks);
-                Co[ks] = frag(Ct, own, ks);
-                Go[ks] = frag(Gt, own, ks);
-                Xo[ks] = frag(Xt, own, ks);
-            }
-            const float cs_own = cs_[own], q_own = q_[own];
-            Frag DCT[2], DCS[2], WS[2];
-            float rows = 0.f, cols = 0.f;
-            {
-                // T orientation: t = own, s = 16 j + 4 kq + i, s-blocks j <= W
-                float dct[2][8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (j <= W) {
-                        f32x4 cb = zero4(), dw = zero4();
-#pragma unroll
-                        for (int ks = 0; ks < 2; ++ks) {
-                            cb = mma3f(frag(Bt, 16 * j + r16, ks), Co[ks], cb);
-                            dw = mma3f(frag(Xt, 16 * j + r16, ks), Go[ks], dw);
-                        }
-                        const float4 qv = *(const float4 *)&q_[16 * j + 4 * kq];
-                        const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
-                        const float qa[4] = {qv.x, qv.y, qv.z, qv.w}, ca[4] = {cv.x, cv.y, cv.z, cv.w};
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const bool in = j < W || 4 * kq + i <= r16;
-                            const float e = in ? exp2_f(cs_own - ca[i]) : 0.f;
-                            const float dwv = dw[i] * qa[i];
-                            rows += dwv * cb[i] * e;
-                            dct[j >> 1][(j & 1) * 4 + i] = dwv * e;
-                        }
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) dct[j >> 1][(j & 1) * 4 + i] = 0.f;
-                    }
-                }
-                DCT[0] = pack_frag(dct[0]);
-                DCT[1] = pack_frag(dct[1]);
-            }
-            {
-                // S orientation: s = own, t = 16 j + 4 kq + i, t-blocks j >= W
-                float ws[2][8], dcs[2][8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (j >= W) {
-                        f32x4 cb = zero4(), dw = zero4();
-#pragma unroll
-                        for (int ks = 0; ks < 2; ++ks) {
-                            cb = mma3f(frag(Ct, 16 * j + r16, ks), Bo[ks], cb);
-                            dw = mma3f(frag(Gt, 16 * j + r16, ks), Xo[ks], dw);
-                        }
-                        const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
-                        const float ca[4] = {cv.x, cv.y, cv.z, cv.w};
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const bool in = j > W || r16 <= 4 * kq + i;
-                            const float e = in ? exp2_f(ca[i] - cs_own) : 0.f;
-                            const float dwv = dw[i] * q_own, wsv = cb[i] * e;
-                            cols += dwv * wsv;
-                            ws[j >> 1][(j & 1) * 4 + i] = wsv;
-                            dcs[j >> 1][(j & 1) * 4 + i] = dwv * e;
-                        }
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            ws[j >> 1][(j & 1) * 4 + i] = 0.f;
-                            dcs[j >> 1][(j & 1) * 4 + i] = 0.f;
-                        }
-                    }
-                }
-                WS[0] = pack_frag(ws[0]);
-                WS[1] = pack_frag(ws[1]);
-                DCS[0] = pack_frag(dcs[0]);
-                DCS[1] = pack_frag(dcs[1]);
-            }
-            rows = sum_kq(rows);
-            cols = sum_kq(cols);
-            if (kq == 0) s_dcs[par][own] = rows - cols;
-
-            // dxdt = W^T gy (rows s of this wave)
-#pragma unroll
-            for (int pb = 0; pb < 4; ++pb) dxa[pb] = zero4();
-#pragma unroll
-            for (int m = 0; m < 2; ++m)
-                if (2 * m + 1 >= W)
-#pragma unroll
-                    for (int pb = 0; pb < 4; ++pb) dxa[pb] = mma3f(WS[m], frag_tp(Gt, m, 16 * pb), dxa[pb]);
-            // dC += dCB B (rows t), dB += dCB^T C (rows s)
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                if (2 * m <= W)
-#pragma unroll
-                    for (int nb = 0; nb < 4; ++nb) dCa[nb] = mma3f(DCT[m], frag_tp(Bt, m, 16 * nb), dCa[nb]);
-                if (2 * m + 1 >= W)
-#pragma unroll
-                    for (int nb = 0; nb < 4; ++nb) dBa[nb] = mma3f(DCS[m], frag_tp(Ct, m, 16 * nb), dBa[nb]);
-            }
+            Frag Bo[2];
             f32x4 ca[4];
+            {
+                Frag Co[2], Go[2], Xo[2];
 #pragma unroll
-            for (int pb = 0; pb < 4; ++pb) {
-                xa[pb] = tile_acc(Xt, 16 * W, 16 * pb);
-                ga[pb] = tile_acc(Gt, 16 * W, 16 * pb);
-                ca[pb] = tile_acc(Ct, 16 * W, 16 * pb);
-            }
-            lds_barrier(); // phase-A tiles free; S, dU staged
+                for (int ks = 0; ks < 2; ++ks) {
+                    Bo[ks] = frag(Bt, own, ks);
+                    Co[ks] = frag(Ct, own, ks);
+                    Go[ks] = frag(gt, own, ks);
+                    Xo[ks] = frag(xt, own, ks);
+                }
+                const float cs_own = cs_[own], q_own = q_[own];
+                Frag DCT[2], DCS[2], WS[2];
+                float rows = 0.f, cols = 0.f;
+                {
+                    // T orientation: t = own, s = 16 j + 4 kq + i, s-blocks j <= W
+                    float dct[2][8];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (j <= W) {
+                            f32x4 cb = zero4(), dw = zero4();
+#pragma unroll
+                            for (int ks = 0; ks < 2; ++ks) {
+                                cb = mma3f(frag(Bt, 16 * j + r16, ks), Co[ks], cb);
+                                dw = mma3f(frag(xt, 16 * j + r16, ks), Go[ks], dw);
+                            }
+                            const float4 qv = *(const float4 *)&q_[16 * j + 4 * kq];
+                            const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
+                            const float qa[4] = {qv.x, qv.y, qv.z, qv.w}, cva[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const bool in = j < W || 4 * kq + i <= r16;
+                                const float e = in ? exp2_f(cs_own - cva[i]) : 0.f;
+                                const float dwv = dw[i] * qa[i];
+                                rows += dwv * cb[i] * e;
+                                dct[j >> 1][(j & 1) * 4 + i] = dwv * e;
+                            }
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) dct[j >> 1][(j & 1) * 4 + i] = 0.f;
+                        }
+                    }
+                    DCT[0] = pack_frag(dct[0]);
+                    DCT[1] = pack_frag(dct[1]);
+                }
+                {
+                    // S orientation: s = own, t = 16 j + 4 kq + i, t-blocks j >= W
+                    float ws[2][8], dcs[2][8];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (j >= W) {
+                            f32x4 cb = zero4(), dw = zero4();
+#pragma unroll
+                            for (int ks = 0; ks < 2; ++ks) {
+                                cb = mma3f(frag(Ct, 16 * j + r16, ks), Bo[ks], cb);
+                                dw = mma3f(frag(gt, 16 * j + r16, ks), Xo[ks], dw);
+                            }
+                            const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
+                            const float cva[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const bool in = j > W || r16 <= 4 * kq + i;
+                                const float e = in ? exp2_f(cva[i] - cs_own) : 0.f;
+                                const float dwv = dw[i] * q_own, wsv = cb[i] * e;
+                                cols += dwv * wsv;
+                                ws[j >> 1][(j & 1) * 4 + i] = wsv;
+                                dcs[j >> 1][(j & 1) * 4 + i] = dwv * e;
+                            }
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                ws[j >> 1][(j & 1) * 4 + i] = 0.f;
+                                dcs[j >> 1][(j & 1) * 4 + i] = 0.f;
+                            }
+                        }
+                    }
+                    WS[0] = pack_frag(ws[0]);
+                    WS[1] = pack_frag(ws[1]);
+                    DCS[0] = pack_frag(dcs[0]);
+                    DCS[1] = pack_frag(dcs[1]);
+                }
+                rows = sum_kq(rows);
+                cols = sum_kq(cols);
+                if (kq == 0) s_dcs[par][own] = rows - cols;
 
-            // ---------------- phase B: S, dU
+                // dxdt = W^T gy (rows s of this wave)
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) dxa[pb] = zero4();
+#pragma unroll
+                for (int m = 0; m < 2; ++m)
+                    if (2 * m + 1 >= W)
+#pragma unroll
+                        for (int pb = 0; pb < 4; ++pb) dxa[pb] = mma3f(WS[m], frag_tp(gt, m, 16 * pb), dxa[pb]);
+                // dC += dCB B (rows t), dB += dCB^T C (rows s)
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    if (2 * m <= W)
+#pragma unroll
+                        for (int nb = 0; nb < 4; ++nb) dCa[nb] = mma3f(DCT[m], frag_tp(Bt, m, 16 * nb), dCa[nb]);
+                    if (2 * m + 1 >= W)
+#pragma unroll
+                        for (int nb = 0; nb < 4; ++nb) dBa[nb] = mma3f(DCS[m], frag_tp(Ct, m, 16 * nb), dBa[nb]);
+                }
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) ca[nb] = tile_acc(Ct, 16 * W, 16 * nb);
+            }
+            lds_barrier(); // S, dU staged; B, C of the next chunk may now be staged
+
+            // ---------------- phase B: S, dU (x, gy of this step are still in LDS)
+            _Float16 *lb = opaque_lds(lds);
+            const SplitTile xb = tile_at(lb, par), gb = tile_at(lb, 2 + par);
+            const SplitTile St = tile_at(lb, 4), Ut = tile_at(lb, 5);
             float tq[4], tdte[4], tecs[4];
             {
                 const float4 a = *(const float4 *)&s_q[par][trow];
@@ -458,15 +507,19 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                     f32x4 rm = zero4();
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) rm = mma3f(Bo[ks], frag(Ut, 16 * pb + r16, ks), rm);
+                    const f32x4 xv = tile_acc(xb, 16 * W, 16 * pb);
 #pragma unroll
                     for (int rr = 0; rr < 4; ++rr) {
                         dxa[pb][rr] += tdte[rr] * rm[rr];
-                        rpart[rr] += xa[pb][rr] * rm[rr];
+                        rpart[rr] += xv[rr] * rm[rr];
                     }
                 }
             }
             {
                 // gy S: [t][n]
+                Frag Go[2];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) Go[ks] = frag(gb, own, ks);
 #pragma unroll
                 for (int nb = 0; nb < 4; ++nb) {
                     f32x4 co = zero4();
@@ -482,6 +535,9 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             }
             {
                 // x dU: [t][n]
+                Frag Xo[2];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) Xo[ks] = frag(xb, own, ks);
 #pragma unroll
                 for (int nb = 0; nb < 4; ++nb) {
                     f32x4 bs = zero4();
@@ -495,8 +551,6 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             for (int rr = 0; rr < 4; ++rr) {
                 const float rd = sum16(rpart[rr]) * tq[rr] * tdte[rr];
                 const float gp = sum16(gpart[rr]);
-                dqp[rr] = sum16(xa[0][rr] * dxa[0][rr] + xa[1][rr] * dxa[1][rr] +
-                                xa[2][rr] * dxa[2][rr] + xa[3][rr] * dxa[3][rr]);
                 if (r16 == 0) {
                     s_dcs[par][trow + rr] += gp - rd;
                     s_rd[par][trow + rr] = rd;
@@ -523,7 +577,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                     dCa[i] = zero4();
                 }
             }
-            lds_barrier(); // phase-B tiles free; next x, gy (B, C) staged
+            lds_barrier(); // S, dU free; x, gy of step n + 1 staged
         }
         epilogue(NS - 1);
     };
