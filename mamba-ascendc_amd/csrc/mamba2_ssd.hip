@@ -269,7 +269,12 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         } else {
             sp.write_final = 1;
         }
-        hipLaunchKernelGGL(ssd::k_fwd_seg<false>, dim3(units), dim3(ssd::kWsThreads), 0, st, prm, sp);
+        if (prm.chunk_states)
+            hipLaunchKernelGGL((ssd::k_fwd_seg<false, true>), dim3(units), dim3(ssd::kWsThreads), 0, st,
+                               prm, sp);
+        else
+            hipLaunchKernelGGL((ssd::k_fwd_seg<false, false>), dim3(units), dim3(ssd::kWsThreads), 0, st,
+                               prm, sp);
         if (int rc = launch_status("k_fwd_seg", tr, st)) return rc;
         return ok();
     }
@@ -452,8 +457,12 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     }
     // state gradients dU_k (and dinitial_states)
     if ((int64_t)B * H >= kMinRevStreams) {
-        hipLaunchKernelGGL(ssd::k_bwd_dstate_rev, dim3((unsigned)(B * H)), dim3(ssd::kWsThreads), 0,
-                           st, bp, a->dfinal_state, a->dinitial_states);
+        if (bp.has_z)
+            hipLaunchKernelGGL(ssd::k_bwd_dstate_rev<true>, dim3((unsigned)(B * H)), dim3(ssd::kWsThreads),
+                               0, st, bp, a->dfinal_state, a->dinitial_states);
+        else
+            hipLaunchKernelGGL(ssd::k_bwd_dstate_rev<false>, dim3((unsigned)(B * H)), dim3(ssd::kWsThreads),
+                               0, st, bp, a->dfinal_state, a->dinitial_states);
         if (int rc = launch_status("k_bwd_dstate_rev", tr, st)) return rc;
     } else {
         hipLaunchKernelGGL(ssd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);

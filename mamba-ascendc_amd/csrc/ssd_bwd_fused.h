@@ -599,6 +599,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 // dSoff^T[n][p] = sum_t C[t][n] (gy exp(cs))[t][p], read transposed from LDS.
 // The recurrence is that of mamba_ascendc/csrc/ops/mamba2_ssd_state_passing_bwd
 // (state_passing_bwd/design.md:44-61) with the dS_off product fused in.
+template <bool kHasZ>
 __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, const float *dfinal,
                                                                 float *dinit) {
     constexpr int T = 64, P = 64, N = 64;
@@ -622,28 +623,33 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         constexpr int kDepth = 3;
         const int pt = tid - 4 * kWave;
         const int rt = pt >> 4, c4 = (pt & 15) * 4; // rows rt + 16 j, columns c4 .. c4 + 3
-        const bool has_dout = prm.dout != nullptr, has_z = prm.has_z != 0;
+        const bool has_dout = prm.dout != nullptr;
         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
         const float Ah2 = prm.A[h] * kLog2e;
         const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
         float4 gr[kDepth][4], zr[kDepth][4], cr[kDepth][4];
         float dtr[kDepth];
+        // unconditional loads (exact wait counts): rows past the sequence end
+        // re-read its last row (zeroed when staged), steps past the first
+        // chunk read through an empty-range resource (zeros, no traffic)
         auto p_load = [&](int i, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
-            const int k = K - 1 - i, tv = tvalid(k);
+            const bool real = i < K;
+            const int k = real ? K - 1 - i : 0, tv = tvalid(k);
+            const int range = real ? 0x7fffffff : 0;
             const int64_t t0 = (int64_t)k * T;
             const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
-            const auto rd = buf_rsrc(has_dout ? prm.dout + xo : prm.x + xo);
-            const auto rz = buf_rsrc(has_z ? prm.z + xo : prm.x + xo);
-            const auto rc = buf_rsrc(prm.C + (((int64_t)b * prm.L + t0) * G + g) * N);
+            const auto rd = buf_rsrc_n(has_dout ? prm.dout + xo : prm.x + xo, range);
+            const auto rz = buf_rsrc_n(kHasZ ? prm.z + xo : prm.x + xo, range);
+            const auto rc = buf_rsrc_n(prm.C + (((int64_t)b * prm.L + t0) * G + g) * N, range);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const bool ok = rt + 16 * j < tv;
-                gr[sl][j] = (ok && has_dout) ? buf_load4(rd, rt * rowHP4 + c4 * 4, 16 * j * rowHP4) : z4;
-                if (has_z) zr[sl][j] = ok ? buf_load4(rz, rt * rowHP4 + c4 * 4, 16 * j * rowHP4) : z4;
-                cr[sl][j] = ok ? buf_load4(rc, rt * rowGN4 + c4 * 4, 16 * j * rowGN4) : z4;
+                const int row = min(rt + 16 * j, tv - 1);
+                gr[sl][j] = buf_load4(rd, row * rowHP4 + c4 * 4, 0);
+                if (kHasZ) zr[sl][j] = buf_load4(rz, row * rowHP4 + c4 * 4, 0);
+                cr[sl][j] = buf_load4(rc, row * rowGN4 + c4 * 4, 0);
             }
-            dtr[sl] = lane < tv ? prm.dt[((int64_t)b * prm.L + t0 + lane) * H + h] : 0.f;
+            dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * H + h];
         };
         auto put = [&](SplitTile d, int row, float4 v) {
             half4 vh, vl;
@@ -653,7 +659,7 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         };
         auto p_stage = [&](int i, int s, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
-            const int tv = tvalid(K - 1 - i);
+            const int tv = i < K ? tvalid(K - 1 - i) : 0; // nothing valid past the first chunk
             float a = 0.f;
             if (lane < tv) a = Ah2 * discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
             const float cs = wave_inclusive_scan(a); // log2 units
@@ -663,42 +669,44 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = rt + 16 * j;
+                const bool ok = row < tv;
                 const float e = __shfl(ecs, row, kWave);
-                float4 v = gr[sl][j];
-                if (has_z) {
+                float4 v = (ok && has_dout) ? gr[sl][j] : z4;
+                if (kHasZ) {
                     v.x *= silu_f(zr[sl][j].x);
                     v.y *= silu_f(zr[sl][j].y);
                     v.z *= silu_f(zr[sl][j].z);
                     v.w *= silu_f(zr[sl][j].w);
                 }
                 put(ge, row, make_float4(v.x * e, v.y * e, v.z * e, v.w * e));
-                put(ct, row, cr[sl][j]);
+                put(ct, row, ok ? cr[sl][j] : z4);
             }
         };
         using S0 = std::integral_constant<int, 0>;
         using S1 = std::integral_constant<int, 1>;
         using S2 = std::integral_constant<int, 2>;
         static_assert(kDepth == 3, "the unrolled ring below assumes three slots");
-        if (0 < K) p_load(0, S0{});
-        if (1 < K) p_load(1, S1{});
-        if (2 < K) p_load(2, S2{});
-        if (0 < K) {
-            p_stage(0, 0, S0{});
-            if (3 < K) p_load(3, S0{});
-        }
+        p_load(0, S0{});
+        p_load(1, S1{});
+        p_load(2, S2{});
+        p_stage(0, 0, S0{});
+        p_load(3, S0{});
         lds_barrier();
+        // past the last step this stages zeros that no consumer reads
         auto p_iter = [&](int i, auto slot_next) {
-            if (i + 1 < K) {
-                p_stage(i + 1, (i + 1) & 1, slot_next);
-                if (i + 1 + kDepth < K) p_load(i + 1 + kDepth, slot_next);
-            }
+            p_stage(i + 1, (i + 1) & 1, slot_next);
+            p_load(i + 1 + kDepth, slot_next);
             lds_barrier();
         };
-        for (int i0 = 0; i0 < K; i0 += kDepth) {
+        // whole rounds of the ring, then the 0..2 remaining steps
+        int i0 = 0;
+        for (; i0 + kDepth <= K; i0 += kDepth) {
             p_iter(i0, S1{});
-            if (i0 + 1 < K) p_iter(i0 + 1, S2{});
-            if (i0 + 2 < K) p_iter(i0 + 2, S0{});
+            p_iter(i0 + 1, S2{});
+            p_iter(i0 + 2, S0{});
         }
+        if (i0 < K) p_iter(i0, S1{});
+        if (i0 + 1 < K) p_iter(i0 + 1, S2{});
         return;
     }
 

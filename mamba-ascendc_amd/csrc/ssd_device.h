@@ -246,6 +246,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p) {
                                              0x00020000);
 }
 
+// The same with a byte range: a load whose offset lies outside [0, nbytes)
+// returns 0 without touching memory.  nbytes = 0 gives a resource every load
+// of which returns 0, used to issue a fixed number of loads per pipeline step
+// past the end of a run (the wait counts then stay exact).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_n(const void *p, int nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, nbytes, 0x00020000);
+}
+
 // The builtin returns the raw 32 bits (unsigned); reinterpret, do not convert.
 __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int lane_bytes, int uniform_bytes) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane_bytes, uniform_bytes, 0));

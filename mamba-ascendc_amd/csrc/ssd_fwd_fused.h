@@ -66,7 +66,8 @@ __device__ __forceinline__ int xcd_unit(int id, int total, int R) {
 
 constexpr int kWsThreads = 512; // 4 producer + 4 consumer waves
 
-template <bool kStateOnly>
+// kSave: also write the state entering every chunk to prm.chunk_states.
+template <bool kStateOnly, bool kSave = false>
 __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams sp) {
     constexpr int T = 64, P = 64, N = 64;
     // stage tiles, double buffered by chunk parity s: full pass T1(s), T2(s),
@@ -108,26 +109,32 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     const int rowHP4 = (int)(rowHP * 4), rowGN4 = (int)(rowGN * 4); // token strides, bytes
     const float Ah2 = prm.A[h] * kLog2e;                                 // A in log2 units
     const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
+    // Loads are issued unconditionally, so the wait counts the compiler
+    // derives are exact: tokens past the sequence end re-read its last token
+    // (their q is 0, so they add nothing), and chunks past the segment read
+    // through an empty-range resource (all zeros, no memory traffic).
     auto p_load = [&](int k, auto slot_c) {
         constexpr int sl = decltype(slot_c)::value;
-        const int64_t t0 = (int64_t)k * T;
+        const bool real = k < kend;
+        const int64_t t0 = (int64_t)(real ? k : kbeg) * T;
         const int tv = (int)min((int64_t)T, prm.L - t0);
-        const auto rx = buf_rsrc(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P);
-        const auto rb = buf_rsrc(prm.B + (((int64_t)b * prm.L + t0) * G + g) * N);
+        const int range = real ? 0x7fffffff : 0;
+        const auto rx = buf_rsrc_n(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P, range);
+        const auto rb = buf_rsrc_n(prm.B + (((int64_t)b * prm.L + t0) * G + g) * N, range);
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const int t = perm_token((w + 4 * rr) * 8 + i); // wave-uniform
-                xr[sl][rr * 8 + i] = t < tv ? buf_load(rx, 4 * c, t * rowHP4) : 0.f;
-                br[sl][rr * 8 + i] = t < tv ? buf_load(rb, 4 * c, t * rowGN4) : 0.f;
+                const int t = min(perm_token((w + 4 * rr) * 8 + i), tv - 1); // wave-uniform
+                xr[sl][rr * 8 + i] = buf_load(rx, 4 * c, t * rowHP4);
+                br[sl][rr * 8 + i] = buf_load(rb, 4 * c, t * rowGN4);
             }
-        dtr[sl] = lane < tv ? prm.dt[((int64_t)b * prm.L + t0 + lane) * H + h] : 0.f;
+        dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * H + h];
     };
     // discretise (lane = token), cumsum in log2 units, fill the stage tiles
     auto p_stage = [&](int k, int s, auto slot_c) {
         constexpr int sl = decltype(slot_c)::value;
-        const int tv = (int)min((int64_t)T, prm.L - (int64_t)k * T);
+        const int tv = (int)min((int64_t)T, prm.L - (int64_t)k * T); // <= 0 past the end
         float q = 0.f, a = 0.f;
         if (lane < tv) {
             q = discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
@@ -171,29 +178,31 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     // after the prologue, one per chunk), so the compiler can give the
     // producer's load ring and the consumer's state the same registers.
     if (producer) {
-        if (kbeg < kend) p_load(kbeg, S0{});
-        if (kbeg + 1 < kend) p_load(kbeg + 1, S1{});
-        if (kbeg + 2 < kend) p_load(kbeg + 2, S2{});
-        if (kbeg < kend) {
-            p_stage(kbeg, 0, S0{});
-            if (kbeg + 3 < kend) p_load(kbeg + 3, S0{});
-        }
+        p_load(kbeg, S0{});
+        p_load(kbeg + 1, S1{});
+        p_load(kbeg + 2, S2{});
+        p_stage(kbeg, 0, S0{});
+        p_load(kbeg + 3, S0{});
         lds_barrier();
         // stage chunk k + 1 into the other buffer while the consumers work
-        // on chunk k; chunk k + 1 sits in slot (k + 1 - kbeg) % 3
+        // on chunk k; chunk k + 1 sits in slot (k + 1 - kbeg) % 3.  Past the
+        // segment end this stages zeros that no consumer reads.
         auto p_iter = [&](int k, auto slot_next) {
             const int s = (k - kbeg) & 1;
-            if (k + 1 < kend) {
-                p_stage(k + 1, s ^ 1, slot_next);
-                if (k + 1 + kDepth < kend) p_load(k + 1 + kDepth, slot_next);
-            }
+            p_stage(k + 1, s ^ 1, slot_next);
+            p_load(k + 1 + kDepth, slot_next);
             lds_barrier();
         };
-        for (int k0 = kbeg; k0 < kend; k0 += kDepth) {
+        // whole rounds of the ring, then the 0..2 remaining chunks: every
+        // path into the loop's back edge has issued the same loads
+        int k0 = kbeg;
+        for (; k0 + kDepth <= kend; k0 += kDepth) {
             p_iter(k0, S1{});
-            if (k0 + 1 < kend) p_iter(k0 + 1, S2{});
-            if (k0 + 2 < kend) p_iter(k0 + 2, S0{});
+            p_iter(k0 + 1, S2{});
+            p_iter(k0 + 2, S0{});
         }
+        if (k0 < kend) p_iter(k0, S1{});
+        if (k0 + 1 < kend) p_iter(k0 + 1, S2{});
         return;
     }
 
@@ -206,16 +215,25 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         const int own = 16 * W + r16; // token row of this lane
         // state: Sr[pb][i] = S[p = 16 pb + l % 16][n = 16 W + 4 (l / 16) + i]
         f32x4 Sr[4];
-        float4 cr[4]; // C row `own` of the next chunk
-        auto c_load = [&](int k) {
-            const int64_t t0 = (int64_t)k * T;
+        // C row `own` of the next two chunks: chunk k in cr[(k - kbeg) & 1],
+        // loaded two chunks ahead
+        float4 cr[2][4];
+        // C row `own` of chunk k (rows past the sequence end re-read its last
+        // row: they only feed outputs that are not stored); past the segment
+        // end an empty-range read, so the load count per chunk is fixed
+        auto c_load = [&](int k, auto slot_c) {
+            constexpr int sl = decltype(slot_c)::value;
+            const bool real = k < kend;
+            const int64_t t0 = (int64_t)(real ? k : kbeg) * T;
             const int tv = (int)min((int64_t)T, prm.L - t0);
-            const float *cb = prm.C + (((int64_t)b * prm.L + t0 + own) * G + g) * N;
+            const auto rc = buf_rsrc_n(prm.C + (((int64_t)b * prm.L + t0) * G + g) * N,
+                                       real ? 0x7fffffff : 0);
+            const int vo = (min(own, tv - 1) * G * N + 8 * kq) * 4;
     #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                cr[j] = own < tv ? *(const float4 *)(cb + 32 * (j >> 1) + 8 * kq + 4 * (j & 1))
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int j = 0; j < 4; ++j) cr[sl][j] = buf_load4(rc, vo + (32 * (j >> 1) + 4 * (j & 1)) * 4, 0);
         };
+        using C0 = std::integral_constant<int, 0>;
+        using C1 = std::integral_constant<int, 1>;
         auto write_T4 = [&](int s) {
             const SplitTile t4 = T4(s);
     #pragma unroll
@@ -246,19 +264,25 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             }
             if (!kStateOnly) {
                 write_T4(0);
-                if (kbeg < kend) c_load(kbeg);
+                c_load(kbeg, C0{});
+                c_load(kbeg + 1, C1{});
             }
         }
         lds_barrier();
 
         float log_decay_sum = 0.f;
-        for (int k = kbeg; k < kend; ++k) {
+        // full chunks store unconditionally (a fixed number of stores per
+        // chunk keeps the C-row prefetch wait exact); only the last chunk of
+        // the sequence can be partial
+        auto iter = [&](int k, auto full_c, auto slot_c) {
+            constexpr bool kFull = decltype(full_c)::value;
+            constexpr int sl = decltype(slot_c)::value;
             const int s = (k - kbeg) & 1;
             const int64_t t0 = (int64_t)k * T;
             const int tv = (int)min((int64_t)T, prm.L - t0);
             const float cs_last = s_cs[s][T - 1];
             log_decay_sum += cs_last;
-            if (!kStateOnly && prm.chunk_states) {
+            if (kSave) {
                 // saved for the backward: the state entering chunk k
                 float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * (int64_t)(P * N);
     #pragma unroll
@@ -271,11 +295,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 Frag Cown[2];
     #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    const float4 v0 = cr[2 * ks], v1 = cr[2 * ks + 1];
+                    const float4 v0 = cr[sl][2 * ks], v1 = cr[sl][2 * ks + 1];
                     const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
                     Cown[ks] = pack_frag(vv);
                 }
-                if (k + 1 < kend) c_load(k + 1);
+                c_load(k + 2, slot_c);
                 const SplitTile t1 = T1(s), t4 = T4(s);
                 const float cs_own = s_cs[s][own];
                 // W^T tiles: C_t . B_s exp2(cs_t - cs_s), s <= t, t = own
@@ -319,7 +343,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     #pragma unroll
                         for (int pb = 0; pb < 4; ++pb)
                             acc[pb] = mma3f(frag(t2, 16 * pb + r16, m), WT[m], acc[pb]);
-                if (own < tv) {
+                if (kFull || own < tv) {
                     const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P;
     #pragma unroll
                     for (int pb = 0; pb < 4; ++pb) {
@@ -368,6 +392,18 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             }
             if (!kStateOnly) write_T4(s ^ 1);
             lds_barrier(); // buffer s is free, buffer s ^ 1 and T4(s ^ 1) are complete
+        };
+        const int kfull = (int)min((int64_t)kend, prm.L / T);
+        int k = kbeg;
+        for (; k + 2 <= kfull; k += 2) {
+            iter(k, std::true_type{}, C0{});
+            iter(k + 1, std::true_type{}, C1{});
+        }
+        if (k < kfull) {
+            iter(k, std::true_type{}, C0{});
+            if (k + 1 < kend) iter(k + 1, std::false_type{}, C1{});
+        } else if (k < kend) {
+            iter(k, std::false_type{}, C0{});
         }
 
         float *dst = nullptr;
