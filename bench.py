@@ -130,9 +130,23 @@ def fwd_kernel_model(name: str, shape) -> dict:
         # entry/exit states are a few per stream and not counted)
         per = f4 * (2 * T * p + T + 2 * T * n / r)
         fl = 2 * (T * T * n / r + T * T * p + 2 * T * n * p)
+    elif name == "k_fwd_seg_save":
+        # training forward: as k_fwd_seg plus the state entering every chunk
+        per = f4 * (2 * T * p + T + 2 * T * n / r + p * n)
+        fl = 2 * (T * T * n / r + T * T * p + 2 * T * n * p)
     elif name == "k_fwd_seg_state":
         per = f4 * (T * p + T + T * n / r)
         fl = 2 * T * p * n
+    elif name == "k_bwd_dstate_rev":
+        # dout, dt, C in; dU (state gradient leaving each chunk) out
+        per = f4 * (T * p + T + T * n / r + p * n)
+        fl = 2 * T * p * n
+    elif name == "k_bwd_ws":
+        # x, dout, dt, S, dU, B, C in; dx, ddt, dB, dC out.  Products per unit
+        # (dense tiles): C.B^T per group, dW twice, W^T gy, dCB.B, dCB^T.C,
+        # B.dU^T, gy.S, x.dU
+        per = f4 * (3 * T * p + 2 * T + 2 * p * n + 4 * T * n / r)
+        fl = 2 * (2 * T * T * n / r + 2 * T * T * p + 2 * T * T * n + 3 * T * n * p)
     else:
         per, fl = float("nan"), float("nan")
     return {"bytes": units * per, "flops": units * fl, "units": units, "bytes_per_unit": per}
@@ -268,10 +282,10 @@ def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup):
                                               ev, nev, names, ctypes.byref(nk)), "bwd", lib)
 
     run_traced(torch, lib, rt, hip, call_b, warmup)
-    fres, _, _ = run_traced(torch, lib, rt, hip, call_f, steps)
+    fres, fnames, _ = run_traced(torch, lib, rt, hip, call_f, steps)
     bres, bnames, _ = run_traced(torch, lib, rt, hip, call_b, steps)
     ok = all(bool(torch.isfinite(v).all()) for v in grads.values())
-    return fres, bres, bnames, ok, ws.numel()
+    return fres, bres, bnames, ok, ws.numel(), fnames
 
 
 def copy_calibration(torch, nbytes):
@@ -397,7 +411,54 @@ def _short(name: str) -> str:
     return base.replace("ssd::", "")
 
 
-def summarize_profiles(trace_dir, fetch_dir, write_dir, shape, copy_bytes=1 << 30):
+def model_key(short: str) -> str:
+    """Kernel-model / trace name of a (templated) kernel: the C ABI traces
+    k_fwd_seg<false, true> as k_fwd_seg_save, k_fwd_seg<true, ...> as
+    k_fwd_seg_state, and drops the feature template of the others."""
+    if short.startswith("k_fwd_seg<"):
+        args = [a.strip() for a in short[len("k_fwd_seg<"):-1].split(",")]
+        if args[0] == "true":
+            return "k_fwd_seg_state"
+        return "k_fwd_seg_save" if len(args) > 1 and args[1] == "true" else "k_fwd_seg"
+    base = short.split("<")[0]
+    return base if base in ("k_bwd_ws", "k_bwd_dstate_rev") else short
+
+
+SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs
+PEAK_CLOCK_GHZ = 2.4  # MI355X peak engine clock
+
+
+def summarize_sq(sq_dir, durations_ms):
+    """Markdown table of per-kernel SQ counters (one rocprofv3 --pmc pass):
+    MFMA pipe busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x duration x peak clock),
+    wait = SQ_WAIT_ANY / SQ_WAVE_CYCLES, VALU = SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES
+    (both wave-time fractions), LDS bank-conflict cycles per LDS-busy SIMD."""
+    import csv
+    import glob
+
+    f = [x for x in glob.glob(os.path.join(sq_dir, "**", "*counter_collection.csv"), recursive=True)][0]
+    per = {}
+    for r in csv.DictReader(open(f)):
+        if "ssd::" not in r["Kernel_Name"]:
+            continue
+        per.setdefault(_short(r["Kernel_Name"]), {}).setdefault(r["Counter_Name"], []).append(
+            float(r["Counter_Value"]))
+    lines = ["| kernel | MFMA instr | MFMA pipe busy | VALU instr | VALU active / wave time | "
+             "waiting / wave time | LDS bank-conflict cycles |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for k, cs in per.items():
+        m = {c: statistics.fmean(v) for c, v in cs.items()}
+        dur = durations_ms.get(k)
+        busy = (m.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (SIMDS * dur * 1e-3 * PEAK_CLOCK_GHZ * 1e9)
+                if dur else float("nan"))
+        wc = m.get("SQ_WAVE_CYCLES", float("nan"))
+        lines.append(f"| `{k}` | {m.get('SQ_INSTS_MFMA', 0):.3e} | {100 * busy:.1f} % | "
+                     f"{m.get('SQ_INSTS_VALU', 0):.3e} | {100 * m.get('SQ_ACTIVE_INST_VALU', 0) / wc:.1f} % | "
+                     f"{100 * m.get('SQ_WAIT_ANY', 0) / wc:.1f} % | {m.get('SQ_LDS_BANK_CONFLICT', 0):.3e} |")
+    return "\n".join(["### SQ counters (rocprofv3 --pmc, one pass)", "", *lines, ""])
+
+
+def summarize_profiles(trace_dir, fetch_dir, write_dir, shape, copy_bytes=1 << 30, sq_dir=None):
     """Markdown summary of a rocprofv3 kernel-trace (--stats, csv) run and two
     --pmc runs (FETCH_SIZE, WRITE_SIZE; csv) of `bench.py --copy-calib`.
 
@@ -420,6 +481,7 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir, shape, copy_bytes=1 << 3
                      f"{float(r['MinNs']) / 1e6:.4f} | {float(r['MaxNs']) / 1e6:.4f} | "
                      f"{float(r['Percentage']):.2f} % |")
     md = ["### Kernel durations (rocprofv3 --kernel-trace --stats)", "", *lines, ""]
+    durations = {_short(r["Name"]): float(r["AverageNs"]) / 1e6 for r in rows}
 
     def counters(d):
         f = [x for x in one(d) if x.endswith("counter_collection.csv")][0]
@@ -443,15 +505,17 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir, shape, copy_bytes=1 << 3
            f"Calibration: a plain {copy_bytes >> 20} MiB device copy reads FETCH_SIZE = {fcal:.0f} KiB "
            f"and WRITE_SIZE = {wcal:.0f} KiB per dispatch, so the counters are scaled by "
            f"{fscale:.3f} (fetch) and {wscale:.3f} (write).", "",
-           "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled traffic GB | algorithmic GB (fwd model) |",
+           "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled traffic GB | algorithmic GB (kernel model) |",
            "|---|---:|---:|---:|---:|"]
     for k in fetch:
         t = (fetch[k] * fscale + write.get(k, 0.0) * wscale) * 1024
-        traffic[k.split("<")[0]] = t
-        alg = fwd_kernel_model(k.split("<")[0], shape)["bytes"]
+        traffic[model_key(k)] = t
+        alg = fwd_kernel_model(model_key(k), shape)["bytes"]
         alg_s = "" if alg != alg else f"{alg / 1e9:.3f}"
         md.append(f"| `{k}` | {fetch[k]:.0f} | {write.get(k, 0.0):.0f} | {t / 1e9:.3f} | {alg_s} |")
     md.append("")
+    if sq_dir:
+        md.append(summarize_sq(sq_dir, durations))
     return "\n".join(md), traffic
 
 
@@ -472,10 +536,12 @@ def main(argv=None):
     ap.add_argument("--summarize-profile", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
                     help="print a markdown summary of rocprofv3 csv output and exit (no GPU)")
     ap.add_argument("--traffic-json", help="with --summarize-profile: also write per-kernel traffic")
+    ap.add_argument("--sq-dir", help="with --summarize-profile: also summarize an SQ counter pass")
     args = ap.parse_args(argv)
 
     if args.summarize_profile:
-        md, traffic = summarize_profiles(*args.summarize_profile, CONFIGS[args.config])
+        md, traffic = summarize_profiles(*args.summarize_profile, CONFIGS[args.config],
+                                         sq_dir=args.sq_dir)
         print(md)
         if args.traffic_json:
             with open(args.traffic_json, "w") as fh:
@@ -540,7 +606,7 @@ def main(argv=None):
         if tr is None:
             bwd_note = "M1 backward needs headdim == dstate == 64"
         else:
-            fres, bres, bnames, bfinite, _ = tr
+            fres, bres, bnames, bfinite = tr[:4]
             bwd_ms = statistics.median(r[0] for r in bres)
             fwd_train_ms = statistics.median(r[0] for r in fres)
             fwd_bwd_ms = statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres))
@@ -549,9 +615,23 @@ def main(argv=None):
             log(f"training forward (saving chunk states) median {fwd_train_ms:.4f} ms")
             for i, name in enumerate(bnames):
                 durs = [r[1][i] for r in bres]
-                bwd_kern[name] = {"avg_ms": round(statistics.fmean(durs), 6),
+                avg = statistics.fmean(durs)
+                model = fwd_kernel_model(name, shape)
+                bwd_kern[name] = {"avg_ms": round(avg, 6),
                                   "median_ms": round(statistics.median(durs), 6)}
-                log(f"  bwd {name:<18} avg {bwd_kern[name]['avg_ms']:8.4f} ms")
+                if model["bytes"] == model["bytes"]:
+                    bwd_kern[name]["GB_s"] = round(model["bytes"] / (avg * 1e-3) / 1e9, 1)
+                    bwd_kern[name]["TFLOP_s"] = round(model["flops"] / (avg * 1e-3) / 1e12, 2)
+                    bwd_kern[name]["traffic"] = measured_traffic(name, shape)
+                log(f"  bwd {name:<18} avg {avg:8.4f} ms"
+                    + (f"  {bwd_kern[name]['GB_s']:8.1f} GB/s  {bwd_kern[name]['TFLOP_s']:7.2f} TFLOP/s"
+                       if "GB_s" in bwd_kern[name] else ""))
+            fnames = tr[5]
+            for i, name in enumerate(fnames):
+                durs = [r[1][i] for r in fres]
+                avg = statistics.fmean(durs)
+                model = fwd_kernel_model(name, shape)
+                log(f"  train {name:<16} avg {avg:8.4f} ms  {model['bytes'] / (avg * 1e-3) / 1e9:8.1f} GB/s")
             log(f"bwd median {bwd_ms:.4f} ms; fwd+bwd median {fwd_bwd_ms:.4f} ms")
             api_fwd_bwd_ms, _ = bench_fwd_bwd(torch, api, inp, chunk, max(5, args.steps // 3), 3)
             log(f"public API (autograd) fwd+bwd median {api_fwd_bwd_ms:.4f} ms")

@@ -269,13 +269,15 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         } else {
             sp.write_final = 1;
         }
-        if (prm.chunk_states)
+        if (prm.chunk_states) {
             hipLaunchKernelGGL((ssd::k_fwd_seg<false, true>), dim3(units), dim3(ssd::kWsThreads), 0, st,
                                prm, sp);
-        else
+            if (int rc = launch_status("k_fwd_seg_save", tr, st)) return rc;
+        } else {
             hipLaunchKernelGGL((ssd::k_fwd_seg<false, false>), dim3(units), dim3(ssd::kWsThreads), 0, st,
                                prm, sp);
-        if (int rc = launch_status("k_fwd_seg", tr, st)) return rc;
+            if (int rc = launch_status("k_fwd_seg", tr, st)) return rc;
+        }
         return ok();
     }
     if (pl.chunked) {

@@ -169,11 +169,15 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             Ahr = prm.A[h];
             biasr = dtb[h];
         };
+        // B, C of the chunk of step n, read for real only when step n starts
+        // a chunk (the only steps whose B, C get staged); the other steps
+        // issue the same loads through an empty-range resource
         auto load_bc = [&](int n) {
+            const int range = (n < NS && n % R == 0) ? 0x7fffffff : 0;
             n = min(n, NS - 1);
             const int k = kbeg + n / R, tv = tvalid(k);
             const int64_t o = (((int64_t)b * prm.L + (int64_t)k * T) * G + g) * N;
-            const auto rb = buf_rsrc(prm.B + o), rc = buf_rsrc(prm.C + o);
+            const auto rb = buf_rsrc_n(prm.B + o, range), rc = buf_rsrc_n(prm.C + o, range);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int lo = min(rt + 16 * j, tv - 1) * rowGN4 + c4 * 4;
@@ -275,8 +279,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         load_xg(1);
         load_bc(1);
         lds_barrier();
-        // every step: two barriers, as in the consumer loop; the B, C loads
-        // of a step fetch the chunk of step n + 2 (L2 hits within a chunk)
+        // every step: two barriers, as in the consumer loop
         for (int n = 0; n < NS; ++n) {
             stage_su(n);
             load_su(n + 1);
