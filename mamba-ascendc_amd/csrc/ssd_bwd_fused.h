@@ -47,62 +47,6 @@ namespace ssd {
 constexpr int kBwsThreads = 512;  // 4 consumer + 4 producer waves
 constexpr int kBwsSlots = 4;      // partial sums per (b, h, k): one per consumer wave
 
-// ds_read_b64_tr_b16 on a split-tile array stored with the contraction index
-// along rows (tile[k][c]).  Each 16-lane group names rows k0..k0+3 (k0 may
-// differ between groups); lane l receives tile[k0 + e][c0 + l % 16], e = 0..3.
-__device__ __forceinline__ half4 tr4(const _Float16 *arr, int k0, int c0) {
-    const int m = threadIdx.x & 15;
-    typedef short v4s __attribute__((ext_vector_type(4)));
-    auto p = (__attribute__((address_space(3))) v4s *)(arr + (k0 + (m >> 2)) * kTS + c0 + 4 * (m & 3));
-    return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
-}
-
-// The LDS array base as a value the optimizer cannot see through.  Tiles
-// past the first 64 KB of LDS cannot use the 16-bit immediate offset of the
-// ds instructions, so every (array, row, k-step) address there becomes a
-// register of its own; derived from this base, those addresses are formed
-// next to their use in each phase instead of being hoisted out of the step
-// loop and held (spilled) for its whole length.
-__device__ __forceinline__ _Float16 *opaque_lds(_Float16 *p) {
-    typedef __attribute__((address_space(3))) _Float16 *lptr;
-    uint32_t a = (uint32_t)(uintptr_t)(lptr)p;
-    asm volatile("" : "+s"(a));
-    return (_Float16 *)(lptr)(uintptr_t)a;
-}
-
-__device__ __forceinline__ half8 cat8(half4 a, half4 b) {
-    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-// Operand of columns c0 .. c0 + 15 contracting over the tile's rows in
-// natural order (k = 32 ks + 8 (l / 16) + 0..7).
-__device__ __forceinline__ Frag frag_tn(SplitTile s, int ks, int c0) {
-    const int k0 = 32 * ks + 8 * ((threadIdx.x & 63) >> 4);
-    Frag f;
-    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 4, c0));
-    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 4, c0));
-    return f;
-}
-
-// The same in the k order of operands taken from MFMA outputs (perm32):
-// slots 0..3 are rows 32 m + 4 (l / 16) + 0..3, slots 4..7 rows 32 m + 16 + ...
-__device__ __forceinline__ Frag frag_tp(SplitTile s, int m, int c0) {
-    const int k0 = 32 * m + 4 * ((threadIdx.x & 63) >> 4);
-    Frag f;
-    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 16, c0));
-    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 16, c0));
-    return f;
-}
-
-// fp32 values of rows row0 + 4 (l / 16) + r, column c0 + l % 16 (r = 0..3):
-// the MFMA accumulator layout of a 16-row block.
-__device__ __forceinline__ f32x4 tile_acc(SplitTile s, int row0, int c0) {
-    const int k0 = row0 + 4 * ((threadIdx.x & 63) >> 4);
-    const half4 h = tr4(s.hi, k0, c0), l = tr4(s.lo, k0, c0);
-    return f32x4{(float)h[0] + (float)l[0], (float)h[1] + (float)l[1], (float)h[2] + (float)l[2],
-                 (float)h[3] + (float)l[3]};
-}
-
 template <bool kHasZ>
 __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg, int M) {
     constexpr int T = 64, P = 64, N = 64;

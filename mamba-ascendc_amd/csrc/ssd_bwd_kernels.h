@@ -58,7 +58,6 @@ __device__ __forceinline__ float bwd_prologue(const BwdParams &p, int b, int h, 
     return cs;
 }
 
-__device__ __forceinline__ float sigmoid_f(float v) { return 1.f / (1.f + __expf(-v)); }
 
 // --------------------------------------------------------------------------
 // dSoff_k = (gy * exp(cs))^T C, one workgroup per (k, h, b)

@@ -47,10 +47,24 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 // hi, a scalar v_cvt_f16_f32 for the subtraction); on a rounding tie the two
 // disagree and hi + lo is off by one fp16 ulp.  With hi truncated, |lo| <
 // ulp16(v) and the pair keeps about 21 significant bits.
+// lo = fp16(v - hi) is one mixed-precision FMA per value (fp16 hi and fp32 v
+// in, fp16 out, round to nearest even): v - hi is exact in fp32, so the
+// result equals converting that difference, in half the instructions of
+// convert-back, subtract and convert.  The compiler does not form these
+// itself, and it cannot see the register writes inside an asm block when it
+// spaces dependent instructions, so the block ends with the two wait states
+// an MFMA reading a VALU result needs (the s_nop 1 the compiler puts between
+// its own conversions and such an MFMA).
 __device__ __forceinline__ void split2(float a, float b, half2v &hi, half2v &lo) {
-    hi = __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
-    const float ra = a - (float)hi[0], rb = b - (float)hi[1];
-    lo = half2v{(_Float16)ra, (_Float16)rb};
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+    uint32_t l;
+    asm("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, -%1, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "s_nop 1"
+        : "=&v"(l)
+        : "v"(h), "v"(a), "v"(b));
+    hi = __builtin_bit_cast(half2v, h);
+    lo = __builtin_bit_cast(half2v, l);
 }
 
 __device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo) {
@@ -68,10 +82,26 @@ __device__ __forceinline__ void split4(float4 v, half4 &hi, half4 &lo) {
     lo = half4{l0[0], l0[1], l1[0], l1[1]};
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// 2^v on the transcendental unit (one v_exp_f32, about 1 ulp).
+__device__ __forceinline__ float exp2_f(float v) { return __builtin_amdgcn_exp2f(v); }
+
+// 1 / v on the transcendental unit (v_rcp_f32, about 1 ulp).
+__device__ __forceinline__ float rcp_f(float v) { return __builtin_amdgcn_rcpf(v); }
+
+// torch.nn.functional.softplus with beta = 1, threshold = 20, as
+// max(u, 0) + ln(1 + e^-|u|) with hardware exp2/log2: a handful of
+// instructions instead of the libm expf/log1pf chains.  Where e^-|u| < 2^-24
+// the log term rounds to 0 (absolute error below 6e-8).
 __device__ __forceinline__ float softplus_f(float u) {
-    // torch.nn.functional.softplus with beta = 1, threshold = 20
-    return u > 20.f ? u : log1pf(expf(u));
+    if (u > 20.f) return u;
+    const float e = exp2_f(-fabsf(u) * kLog2e);
+    return fmaxf(u, 0.f) + kLn2 * __builtin_amdgcn_logf(1.f + e);
 }
+
+__device__ __forceinline__ float sigmoid_f(float v) { return rcp_f(1.f + exp2_f(-v * kLog2e)); }
 
 // q = clamp(softplus(dt + bias) or dt + bias, lo, hi)
 __device__ __forceinline__ float discretize_dt(float dt, float bias, bool softplus, float lo,
@@ -88,20 +118,30 @@ __device__ __forceinline__ float discretize_grad(float dt, float bias, bool soft
     float u = dt + bias;
     float pre = softplus ? softplus_f(u) : u;
     float g = (pre >= lo && pre <= hi) ? 1.f : 0.f;
-    if (softplus) g *= 1.f / (1.f + expf(-u));
+    if (softplus) g *= sigmoid_f(u);
     return g;
 }
 
-__device__ __forceinline__ float silu_f(float z) { return z / (1.f + expf(-z)); }
+__device__ __forceinline__ float silu_f(float z) { return z * sigmoid_f(z); }
 
-// Inclusive prefix sum across the 64 lanes of a wave.
+// Lane shift / broadcast of a wave through DPP (register crossbar, no LDS
+// round trip); lanes without a source, or outside row_mask, read 0.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl,
+                                                                 kRowMask, 0xf, false));
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave: Hillis-Steele within
+// each row of 16 lanes (row_shr 1, 2, 4, 8), then the row totals are carried
+// with row_bcast:15 (rows 1, 3) and row_bcast:31 (rows 2, 3).
 __device__ __forceinline__ float wave_inclusive_scan(float v) {
-    const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        float o = __shfl_up(v, off, kWave);
-        if (lane >= off) v += o;
-    }
+    v += dpp_f<0x111>(v);
+    v += dpp_f<0x112>(v);
+    v += dpp_f<0x114>(v);
+    v += dpp_f<0x118>(v);
+    v += dpp_f<0x142, 0xa>(v);
+    v += dpp_f<0x143, 0xc>(v);
     return v;
 }
 
@@ -221,6 +261,62 @@ __device__ __forceinline__ Frag pack_frag(const float (&v)[8]) {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// ds_read_b64_tr_b16 on a split-tile array stored with the contraction index
+// along rows (tile[k][c]).  Each 16-lane group names rows k0..k0+3 (k0 may
+// differ between groups); lane l receives tile[k0 + e][c0 + l % 16], e = 0..3.
+__device__ __forceinline__ half4 tr4(const _Float16 *arr, int k0, int c0) {
+    const int m = threadIdx.x & 15;
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    auto p = (__attribute__((address_space(3))) v4s *)(arr + (k0 + (m >> 2)) * kTS + c0 + 4 * (m & 3));
+    return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
+}
+
+// The LDS array base as a value the optimizer cannot see through.  Tiles
+// past the first 64 KB of LDS cannot use the 16-bit immediate offset of the
+// ds instructions, so every (array, row, k-step) address there becomes a
+// register of its own; derived from this base, those addresses are formed
+// next to their use in each phase instead of being hoisted out of the step
+// loop and held (spilled) for its whole length.
+__device__ __forceinline__ _Float16 *opaque_lds(_Float16 *p) {
+    typedef __attribute__((address_space(3))) _Float16 *lptr;
+    uint32_t a = (uint32_t)(uintptr_t)(lptr)p;
+    asm volatile("" : "+s"(a));
+    return (_Float16 *)(lptr)(uintptr_t)a;
+}
+
+__device__ __forceinline__ half8 cat8(half4 a, half4 b) {
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Operand of columns c0 .. c0 + 15 contracting over the tile's rows in
+// natural order (k = 32 ks + 8 (l / 16) + 0..7).
+__device__ __forceinline__ Frag frag_tn(SplitTile s, int ks, int c0) {
+    const int k0 = 32 * ks + 8 * ((threadIdx.x & 63) >> 4);
+    Frag f;
+    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 4, c0));
+    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 4, c0));
+    return f;
+}
+
+// The same in the k order of operands taken from MFMA outputs (perm32):
+// slots 0..3 are rows 32 m + 4 (l / 16) + 0..3, slots 4..7 rows 32 m + 16 + ...
+__device__ __forceinline__ Frag frag_tp(SplitTile s, int m, int c0) {
+    const int k0 = 32 * m + 4 * ((threadIdx.x & 63) >> 4);
+    Frag f;
+    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 16, c0));
+    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 16, c0));
+    return f;
+}
+
+// fp32 values of rows row0 + 4 (l / 16) + r, column c0 + l % 16 (r = 0..3):
+// the MFMA accumulator layout of a 16-row block.
+__device__ __forceinline__ f32x4 tile_acc(SplitTile s, int row0, int c0) {
+    const int k0 = row0 + 4 * ((threadIdx.x & 63) >> 4);
+    const half4 h = tr4(s.hi, k0, c0), l = tr4(s.lo, k0, c0);
+    return f32x4{(float)h[0] + (float)l[0], (float)h[1] + (float)l[1], (float)h[2] + (float)l[2],
+                 (float)h[3] + (float)l[3]};
+}
+
 // Value of v in lane `lane` (which must be the same for the whole wave).
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -262,12 +358,6 @@ __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int lane_byt
 __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int lane_bytes, int uniform_bytes) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, uniform_bytes, 0));
 }
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-
-// 2^v on the transcendental unit (one v_exp_f32, about 1 ulp).
-__device__ __forceinline__ float exp2_f(float v) { return __builtin_amdgcn_exp2f(v); }
 
 // The wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }

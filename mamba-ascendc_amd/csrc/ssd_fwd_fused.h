@@ -20,15 +20,20 @@
 // Exponentials are taken in the log2 domain: the chunk cumsum is formed over
 // A q log2(e), so every decay factor is a single exp2 of a difference.
 //
-// Tiles (split fp16, LDS), for the chunk being processed:
-//   T1 = B [t][n]              (A operand of C.B^T, rows s)
-//   T2 = (q x)^T [p][slot]     (A operand of y^T, B operand of U^T; perm order)
-//   T3 = (decay B)^T [n][slot] (A operand of U^T; perm order)
-//   T4 = S [p][n]              (A operand of the C.S term)
+// Tiles (split fp16, LDS, all stored row-major in their first index), for
+// the chunk being processed:
+//   T1 = B [t][n]          (A operand of C.B^T, rows s)
+//   T2 = q x [t][p]        (A operand of y^T and B operand of U^T, both
+//                           contracting over t: transposed reads)
+//   T3 = decay B [t][n]    (A operand of U^T, transposed reads)
+//   T4 = S [p][n]          (A operand of the C.S term)
 // and, in registers, C_t for the lane's own token row t = 16 w + l % 16.
 // Outputs are produced transposed (y^T[p][t], U^T[n][p]) so that the C.B^T
-// tiles feed the next product straight from registers (see perm32) and S
-// stays in the accumulator layout of U^T.
+// tiles feed the next product straight from registers (see perm32; the
+// transposed reads of T2 use the same k order) and S stays in the
+// accumulator layout of U^T.  Producers fill the tiles from 16-byte row loads
+// (nine loads per chunk and lane, so three chunks of loads stay within the
+// 63 outstanding vector-memory operations a wave can track).
 //
 // The math is that of mamba_ascendc/csrc/ops/mamba2_ssd_fwd/design.md:10-20 and
 // the chunked decomposition of mamba_torch/ssd_reference.py:113-189; the
@@ -81,7 +86,6 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     const bool producer = wave >= 4;
     const int w = wave & 3; // index of the wave within its role
     const int r16 = lane & 15, kq = lane >> 4;
-    const int c = lane;           // producer: tile column staged by this lane
 
     auto T1 = [&](int s) { return tile_at(lds, 3 * s); };
     auto T2 = [&](int s) { return tile_at(lds, kStateOnly ? 2 * s : 3 * s + 1); };
@@ -100,17 +104,20 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     const int kbeg = sg * sp.M, kend = min(kbeg + sp.M, prm.K);
 
     // ------------------------------------------------------------ producer
-    // A ring of kDepth register slots holds 16 tokens of column c of x and B
-    // (perm order of the runs w, w + 4) and dt of token `lane` for the next
-    // kDepth chunks, so each chunk's loads are issued kDepth iterations
-    // before it is staged.  Slot of chunk k: (k - kbeg) % kDepth.
+    // A ring of kDepth register slots holds, for the next kDepth chunks, rows
+    // rt + 16 j (columns c4 .. c4 + 3) of x and B and dt of token `lane`, so
+    // each chunk's loads are issued kDepth iterations before it is staged.
+    // Slot of chunk k: (k - kbeg) % kDepth.
     constexpr int kDepth = 3;
-    float xr[kDepth][16], br[kDepth][16], dtr[kDepth];
+    const int pt = tid - 4 * kWave;
+    const int rt = pt >> 4, c4 = (pt & 15) * 4;
+    float4 xr[kDepth][4], br[kDepth][4];
+    float dtr[kDepth];
     const int rowHP4 = (int)(rowHP * 4), rowGN4 = (int)(rowGN * 4); // token strides, bytes
     const float Ah2 = prm.A[h] * kLog2e;                                 // A in log2 units
     const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
     // Loads are issued unconditionally, so the wait counts the compiler
-    // derives are exact: tokens past the sequence end re-read its last token
+    // derives are exact: rows past the sequence end re-read its last row
     // (their q is 0, so they add nothing), and chunks past the segment read
     // through an empty-range resource (all zeros, no memory traffic).
     auto p_load = [&](int k, auto slot_c) {
@@ -122,14 +129,18 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         const auto rx = buf_rsrc_n(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P, range);
         const auto rb = buf_rsrc_n(prm.B + (((int64_t)b * prm.L + t0) * G + g) * N, range);
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int t = min(perm_token((w + 4 * rr) * 8 + i), tv - 1); // wave-uniform
-                xr[sl][rr * 8 + i] = buf_load(rx, 4 * c, t * rowHP4);
-                br[sl][rr * 8 + i] = buf_load(rb, 4 * c, t * rowGN4);
-            }
+        for (int j = 0; j < 4; ++j) {
+            const int row = min(rt + 16 * j, tv - 1);
+            xr[sl][j] = buf_load4(rx, row * rowHP4 + c4 * 4, 0);
+            br[sl][j] = buf_load4(rb, row * rowGN4 + c4 * 4, 0);
+        }
         dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * H + h];
+    };
+    auto put = [&](SplitTile d, int row, float4 v) {
+        half4 vh, vl;
+        split4(v, vh, vl);
+        *(half4 *)&d.hi[row * kTS + c4] = vh;
+        *(half4 *)&d.lo[row * kTS + c4] = vl;
     };
     // discretise (lane = token), cumsum in log2 units, fill the stage tiles
     auto p_stage = [&](int k, int s, auto slot_c) {
@@ -143,29 +154,16 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         const float cs = wave_inclusive_scan(a);
         const float cs_last = readlane_f(cs, T - 1);
         if (w == 0) s_cs[s][lane] = cs;
+        const float dec = exp2_f(cs_last - cs);
         const SplitTile t1 = T1(s), t2 = T2(s), t3 = T3(s);
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-            const int run = w + 4 * rr;
-            float xv[8], dv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int t = perm_token(run * 8 + i);
-                const float bv = br[sl][rr * 8 + i];
-                xv[i] = xr[sl][rr * 8 + i] * readlane_f(q, t);
-                dv[i] = bv * exp2_f(cs_last - readlane_f(cs, t));
-                if (!kStateOnly) {
-                    _Float16 hh, ll;
-                    split_f16(bv, hh, ll);
-                    t1.hi[t * kTS + c] = hh;
-                    t1.lo[t * kTS + c] = ll;
-                }
-            }
-            const Frag fx = pack_frag(xv), fd = pack_frag(dv);
-            *(half8 *)&t2.hi[c * kTS + run * 8] = fx.h;
-            *(half8 *)&t2.lo[c * kTS + run * 8] = fx.l;
-            *(half8 *)&t3.hi[c * kTS + run * 8] = fd.h;
-            *(half8 *)&t3.lo[c * kTS + run * 8] = fd.l;
+        for (int j = 0; j < 4; ++j) {
+            const int row = rt + 16 * j;
+            const float qr = __shfl(q, row, kWave), dr = __shfl(dec, row, kWave);
+            const float4 xv = xr[sl][j], bv = br[sl][j];
+            put(t2, row, make_float4(xv.x * qr, xv.y * qr, xv.z * qr, xv.w * qr));
+            put(t3, row, make_float4(bv.x * dr, bv.y * dr, bv.z * dr, bv.w * dr));
+            if (!kStateOnly) put(t1, row, bv);
         }
     };
 
@@ -342,7 +340,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     if (2 * m <= W)
     #pragma unroll
                         for (int pb = 0; pb < 4; ++pb)
-                            acc[pb] = mma3f(frag(t2, 16 * pb + r16, m), WT[m], acc[pb]);
+                            acc[pb] = mma3f(frag_tp(t2, m, 16 * pb), WT[m], acc[pb]);
                 if (kFull || own < tv) {
                     const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P;
     #pragma unroll
@@ -380,9 +378,9 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 for (int pb = 0; pb < 4; ++pb) U[pb] = zero4();
     #pragma unroll
                 for (int m = 0; m < 2; ++m) {
-                    const Frag a3 = frag(t3, 16 * W + r16, m);
+                    const Frag a3 = frag_tp(t3, m, 16 * W);
     #pragma unroll
-                    for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag(t2, 16 * pb + r16, m), U[pb]);
+                    for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag_tp(t2, m, 16 * pb), U[pb]);
                 }
                 const float alpha = exp2_f(cs_last);
     #pragma unroll
