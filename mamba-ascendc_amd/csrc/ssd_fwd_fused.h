@@ -289,6 +289,9 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
             }
             const SplitTile t2 = T2(s), t3 = T3(s);
+            f32x4 U[4];
+    #pragma unroll
+            for (int pb = 0; pb < 4; ++pb) U[pb] = zero4();
             if (!kStateOnly) {
                 Frag Cown[2];
     #pragma unroll
@@ -335,12 +338,17 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 for (int pb = 0; pb < 4; ++pb)
     #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[pb][i] *= ecs;
+                // each (q x) fragment feeds both y^T (W part) and U^T
     #pragma unroll
-                for (int m = 0; m < 2; ++m)
-                    if (2 * m <= W)
+                for (int m = 0; m < 2; ++m) {
+                    const Frag a3 = frag_tp(t3, m, 16 * W);
     #pragma unroll
-                        for (int pb = 0; pb < 4; ++pb)
-                            acc[pb] = mma3f(frag_tp(t2, m, 16 * pb), WT[m], acc[pb]);
+                    for (int pb = 0; pb < 4; ++pb) {
+                        const Frag f2 = frag_tp(t2, m, 16 * pb);
+                        if (2 * m <= W) acc[pb] = mma3f(f2, WT[m], acc[pb]);
+                        U[pb] = mma3f(a3, f2, U[pb]);
+                    }
+                }
                 if (kFull || own < tv) {
                     const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P;
     #pragma unroll
@@ -371,16 +379,16 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     }
                 }
             }
-            // S <- exp2(cs_last) S + U, U^T[n][p] = T3 x T2
+            // S <- exp2(cs_last) S + U, U^T[n][p] = T3 x T2 (the full pass forms
+            // U together with y)
             {
-                f32x4 U[4];
+                if (kStateOnly) {
     #pragma unroll
-                for (int pb = 0; pb < 4; ++pb) U[pb] = zero4();
+                    for (int m = 0; m < 2; ++m) {
+                        const Frag a3 = frag_tp(t3, m, 16 * W);
     #pragma unroll
-                for (int m = 0; m < 2; ++m) {
-                    const Frag a3 = frag_tp(t3, m, 16 * W);
-    #pragma unroll
-                    for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag_tp(t2, m, 16 * pb), U[pb]);
+                        for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag_tp(t2, m, 16 * pb), U[pb]);
+                    }
                 }
                 const float alpha = exp2_f(cs_last);
     #pragma unroll
