@@ -57,6 +57,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     __shared__ __attribute__((aligned(16))) float s_q[2][T], s_cs[2][T], s_dqdu[2][T], s_dte[2][T],
         s_ecs[2][T], s_D[2][P];
     __shared__ float s_dcs[2][T], s_rd[2][T], s_sdu[2][4], s_A[2];
+    __shared__ __attribute__((aligned(16))) float s_da[4][T]; // epilogue: da of a step, per consumer wave
 
     auto Xt = [&](int par) { return tile_at(lds, par); };
     auto Gt = [&](int par) { return tile_at(lds, 2 + par); };
@@ -278,16 +279,24 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 ga[pb] = tile_acc(tile_at(le, 2 + par), 16 * W, 16 * pb);
                 Dv[pb] = s_D[par][prm.d_per_channel ? 16 * pb + r16 : 0];
             }
+            // da of this lane's 4 accumulator rows: through this wave's LDS row
+            // (written and read back by the same wave, so no barrier)
+            s_da[W][lane] = da;
+            const float4 da4 = *(const float4 *)&s_da[W][trow];
+            const float4 q4 = *(const float4 *)&s_q[par][trow];
+            const float4 u4 = *(const float4 *)&s_dqdu[par][trow];
+            const float dav[4] = {da4.x, da4.y, da4.z, da4.w}, qv4[4] = {q4.x, q4.y, q4.z, q4.w},
+                        uv4[4] = {u4.x, u4.y, u4.z, u4.w};
             float dbias = 0.f, dDp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int t = trow + rr;
                 const bool valid = t < tv;
-                const float da_t = __shfl(da, t, kWave);
-                const float q_t = s_q[par][t];
+                const float da_t = dav[rr];
+                const float q_t = qv4[rr];
                 const float dqp = sum16(xa[0][rr] * dxa[0][rr] + xa[1][rr] * dxa[1][rr] +
                                         xa[2][rr] * dxa[2][rr] + xa[3][rr] * dxa[3][rr]);
-                const float ddt = valid ? (Ah * da_t + dqp) * s_dqdu[par][t] : 0.f;
+                const float ddt = valid ? (Ah * da_t + dqp) * uv4[rr] : 0.f;
                 if (r16 == 0) {
                     if (valid) prm.ddt[((int64_t)b * prm.L + t0 + t) * H + h] = ddt;
                     dbias += ddt;

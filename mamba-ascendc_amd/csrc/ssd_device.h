@@ -145,21 +145,54 @@ __device__ __forceinline__ float wave_inclusive_scan(float v) {
     return v;
 }
 
-// Suffix (reverse inclusive) sum across the 64 lanes of a wave.
-__device__ __forceinline__ float wave_suffix_scan(float v) {
-    const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        float o = __shfl_down(v, off, kWave);
-        if (lane + off < kWave) v += o;
-    }
+// v of lane l ^ 16 and of lane l ^ 32, through the gfx950 lane-swap
+// instructions (v_permlane16_swap / v_permlane32_swap exchange odd and even
+// 16-lane rows / the two 32-lane halves of two registers).  Swapping a
+// register with itself leaves, in every lane, its own value in one result
+// and its partner's in the other; the partner's is the one whose bits differ
+// (if they are equal, either is right), which does not depend on which
+// result receives which rows.
+__device__ __forceinline__ float xor16_f(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, r[0] == u ? r[1] : r[0]);
+}
+__device__ __forceinline__ float xor32_f(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, r[0] == u ? r[1] : r[0]);
+}
+// v[l] + v[l ^ 16] (resp. ^ 32): addition commutes, so both lanes of a pair
+// form the same sum.  (The two results of the swap are not used directly:
+// when both operands are one value the compiler may give the instruction a
+// single register, which then holds the partner's value in both results.)
+__device__ __forceinline__ float add_xor16(float v) { return v + xor16_f(v); }
+__device__ __forceinline__ float add_xor32(float v) { return v + xor32_f(v); }
+
+// Sum over the 16 lanes of each row (DPP quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror, row_mirror); every lane of the row gets the sum.
+__device__ __forceinline__ float sum16(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
     return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+// Sum over the 4 lanes that share l % 16.
+__device__ __forceinline__ float sum_kq(float v) { return add_xor32(add_xor16(v)); }
+
+// Sum over the 64 lanes, in every lane.
+__device__ __forceinline__ float wave_sum(float v) { return sum_kq(sum16(v)); }
+
+// v of lane 63 - l (row_mirror within the row, then the row order reversed).
+__device__ __forceinline__ float reverse_lanes(float v) {
+    return xor32_f(xor16_f(dpp_f<0x140>(v)));
+}
+
+// Suffix (reverse inclusive) sum across the 64 lanes of a wave.
+__device__ __forceinline__ float wave_suffix_scan(float v) {
+    return reverse_lanes(wave_inclusive_scan(reverse_lanes(v)));
 }
 
 // Position of token s (0..31 inside a 32-token slab) in the k-permuted operand
@@ -361,21 +394,5 @@ __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int lane_b
 
 // The wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
-
-// Sum over the 16 lanes that share a lane group (same l / 16).
-__device__ __forceinline__ float sum16(float v) {
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 8, 64);
-    return v;
-}
-
-// Sum over the 4 lanes that share l % 16.
-__device__ __forceinline__ float sum_kq(float v) {
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
-}
 
 }  // namespace ssd
