@@ -287,6 +287,11 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             const float4 u4 = *(const float4 *)&s_dqdu[par][trow];
             const float dav[4] = {da4.x, da4.y, da4.z, da4.w}, qv4[4] = {q4.x, q4.y, q4.z, q4.w},
                         uv4[4] = {u4.x, u4.y, u4.z, u4.w};
+            // stores through buffer resources: a per-lane row offset plus scalar
+            // and immediate offsets instead of 64-bit addresses
+            const auto rdx = buf_rsrc(prm.dx + xo);
+            const auto rddt = buf_rsrc(prm.ddt + ((int64_t)b * prm.L + t0) * H + h);
+            const int vrow = trow * rowHP4 + 4 * r16;
             float dbias = 0.f, dDp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
@@ -298,14 +303,14 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                                         xa[2][rr] * dxa[2][rr] + xa[3][rr] * dxa[3][rr]);
                 const float ddt = valid ? (Ah * da_t + dqp) * uv4[rr] : 0.f;
                 if (r16 == 0) {
-                    if (valid) prm.ddt[((int64_t)b * prm.L + t0 + t) * H + h] = ddt;
+                    if (valid) buf_store(rddt, trow * H * 4, rr * H * 4, ddt);
                     dbias += ddt;
                 }
 #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) {
                     const float gyv = ga[pb][rr];
                     dDp[pb] += gyv * xa[pb][rr];
-                    if (valid) prm.dx[xo + (int64_t)t * H * P + 16 * pb + r16] = q_t * dxa[pb][rr] + Dv[pb] * gyv;
+                    if (valid) buf_store(rdx, vrow + 64 * pb, rr * rowHP4, q_t * dxa[pb][rr] + Dv[pb] * gyv);
                 }
             }
             dbias = wave_sum(dbias);
@@ -515,15 +520,16 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             if (r == R - 1) {
                 const int64_t t0 = (int64_t)k * T;
                 const int tv = tvalid(k);
+                const int64_t o = (((int64_t)b * prm.L + t0) * G + g) * N;
+                const auto rdB = buf_rsrc(prm.dB + o), rdC = buf_rsrc(prm.dC + o);
+                const int vrow = trow * rowGN4 + 4 * r16;
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    const int t = trow + rr;
-                    if (t < tv) {
-                        const int64_t o = (((int64_t)b * prm.L + t0 + t) * G + g) * N;
+                    if (trow + rr < tv) {
 #pragma unroll
                         for (int nb = 0; nb < 4; ++nb) {
-                            prm.dB[o + 16 * nb + r16] = dBa[nb][rr];
-                            prm.dC[o + 16 * nb + r16] = dCa[nb][rr];
+                            buf_store(rdB, vrow + 64 * nb, rr * rowGN4, dBa[nb][rr]);
+                            buf_store(rdC, vrow + 64 * nb, rr * rowGN4, dCa[nb][rr]);
                         }
                     }
                 }

@@ -341,13 +341,29 @@ __device__ __forceinline__ Frag frag_tp(SplitTile s, int m, int c0) {
     return f;
 }
 
+// fp32 hi + lo of four split values: one mixed-precision FMA each
+// (hi * 1 + lo with both fp16 operands widened, exact, rounded once to fp32),
+// instead of two conversions and an add.  The block ends with the wait states
+// an MFMA reading a VALU result needs, as split2 does.
+__device__ __forceinline__ f32x4 join4(half4 h, half4 l) {
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    const u2 hb = __builtin_bit_cast(u2, h), lb = __builtin_bit_cast(u2, l);
+    float a, b, c, d;
+    asm("v_fma_mix_f32 %0, %4, 1.0, %6 op_sel_hi:[1,0,1]\n\t"
+        "v_fma_mix_f32 %1, %4, 1.0, %6 op_sel:[1,0,1] op_sel_hi:[1,0,1]\n\t"
+        "v_fma_mix_f32 %2, %5, 1.0, %7 op_sel_hi:[1,0,1]\n\t"
+        "v_fma_mix_f32 %3, %5, 1.0, %7 op_sel:[1,0,1] op_sel_hi:[1,0,1]\n\t"
+        "s_nop 1"
+        : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
+        : "v"(hb[0]), "v"(hb[1]), "v"(lb[0]), "v"(lb[1]));
+    return f32x4{a, b, c, d};
+}
+
 // fp32 values of rows row0 + 4 (l / 16) + r, column c0 + l % 16 (r = 0..3):
 // the MFMA accumulator layout of a 16-row block.
 __device__ __forceinline__ f32x4 tile_acc(SplitTile s, int row0, int c0) {
     const int k0 = row0 + 4 * ((threadIdx.x & 63) >> 4);
-    const half4 h = tr4(s.hi, k0, c0), l = tr4(s.lo, k0, c0);
-    return f32x4{(float)h[0] + (float)l[0], (float)h[1] + (float)l[1], (float)h[2] + (float)l[2],
-                 (float)h[3] + (float)l[3]};
+    return join4(tr4(s.hi, k0, c0), tr4(s.lo, k0, c0));
 }
 
 // Value of v in lane `lane` (which must be the same for the whole wave).
@@ -386,6 +402,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_n(const void *p, int 
 // The builtin returns the raw 32 bits (unsigned); reinterpret, do not convert.
 __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, int lane_bytes, int uniform_bytes) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane_bytes, uniform_bytes, 0));
+}
+
+__device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, int lane_bytes, int uniform_bytes, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, lane_bytes, uniform_bytes, 0);
 }
 
 __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int lane_bytes, int uniform_bytes) {
