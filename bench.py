@@ -147,6 +147,11 @@ def fwd_kernel_model(name: str, shape) -> dict:
         # B.dU^T, gy.S, x.dU
         per = f4 * (3 * T * p + 2 * T + 2 * p * n + 4 * T * n / r)
         fl = 2 * (2 * T * T * n / r + 2 * T * T * p + 2 * T * T * n + 3 * T * n * p)
+    elif name == "k_bwd_ws_rev":
+        # reverse fused: as k_bwd_ws without dU in (the state gradient is
+        # carried on chip), plus the dSoff product (gy exp(cs))^T C
+        per = f4 * (3 * T * p + 2 * T + p * n + 4 * T * n / r)
+        fl = 2 * (2 * T * T * n / r + 2 * T * T * p + 2 * T * T * n + 4 * T * n * p)
     else:
         per, fl = float("nan"), float("nan")
     return {"bytes": units * per, "flops": units * fl, "units": units, "bytes_per_unit": per}
@@ -421,7 +426,10 @@ def model_key(short: str) -> str:
             return "k_fwd_seg_state"
         return "k_fwd_seg_save" if len(args) > 1 and args[1] == "true" else "k_fwd_seg"
     base = short.split("<")[0]
-    return base if base in ("k_bwd_ws", "k_bwd_dstate_rev") else short
+    if base == "k_bwd_ws":
+        args = [a.strip() for a in short[len("k_bwd_ws<"):-1].split(",")]
+        return "k_bwd_ws_rev" if len(args) > 1 and args[1] != "0" else "k_bwd_ws"
+    return base if base == "k_bwd_dstate_rev" else short
 
 
 SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs

@@ -300,8 +300,19 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     return ok();
 }
 
+// The reverse fused chunk backward (k_bwd_ws<., R>) walks each (b, g) stream
+// serially, carrying the state gradients of the group's R heads in
+// registers: used for R = 1, 2, 4 with at least this many streams (one
+// workgroup per CU, so fewer streams would leave CUs idle).
+constexpr int64_t kMinFusedStreams = 256;
+
+bool bwd_fused_rev(const Mamba2SsdShape *s) {
+    const int64_t R = s->nheads / s->ngroups;
+    return (R == 1 || R == 2 || R == 4) && s->batch * s->ngroups >= kMinFusedStreams;
+}
+
 // Backward workspace: states [B,H,K,P,N] (unless SAVED_STATES) | log decay [B,H,K]
-// | dstates [B,H,K,P,N]
+// | dstates [B,H,K,P,N] (unless the reverse fused path runs)
 // | dA partials [B,H,K] | ddt_bias partials [B,H,K,slots] | dD partials
 // [B,H,K,slots,P] (slots = one per consumer wave of the chunk kernel).
 struct BwdLayout {
@@ -318,7 +329,7 @@ BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
     l.log_decay = off;
     off += align256(bhk * sizeof(float));
     l.dstates = off;
-    off += align256(bhk * pn * sizeof(float));
+    if (!bwd_fused_rev(s)) off += align256(bhk * pn * sizeof(float));
     l.part_dA = off;
     off += align256(bhk * sizeof(float));
     l.part_db = off;
@@ -431,6 +442,8 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     bp.states = fp.states;
     bp.log_decay = fp.chunk_log_decay;
     bp.dstates = (float *)(ws + lay.dstates);
+    bp.dfinal = a->dfinal_state;
+    bp.dinit = a->dinitial_states;
     bp.part_dA = (float *)(ws + lay.part_dA);
     bp.part_dbias = (float *)(ws + lay.part_db);
     bp.part_dD = (float *)(ws + lay.part_dD);
@@ -457,6 +470,30 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
                            fp.chunk_log_decay, fp.init, fp.states, (float *)nullptr, K, PN);
         if (int rc = launch_status("k_state_pass", tr, st)) return rc;
     }
+    const int64_t bg = (int64_t)B * s->ngroups;
+    if (bwd_fused_rev(s)) {
+        // one pass: reverse chunk order, state gradients carried in registers
+        const dim3 grid((unsigned)bg), block(ssd::kBwsThreads);
+        const int R = bp.R;
+#define SSD_LAUNCH_REV(Z, RR) \
+    hipLaunchKernelGGL((ssd::k_bwd_ws<Z, RR>), grid, block, 0, st, bp, 1, K)
+        if (bp.has_z) {
+            if (R == 1) SSD_LAUNCH_REV(true, 1);
+            else if (R == 2) SSD_LAUNCH_REV(true, 2);
+            else SSD_LAUNCH_REV(true, 4);
+        } else {
+            if (R == 1) SSD_LAUNCH_REV(false, 1);
+            else if (R == 2) SSD_LAUNCH_REV(false, 2);
+            else SSD_LAUNCH_REV(false, 4);
+        }
+#undef SSD_LAUNCH_REV
+        if (int rc = launch_status("k_bwd_ws_rev", tr, st)) return rc;
+        hipLaunchKernelGGL(ssd::k_bwd_finalize_slots, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
+                           bp.part_dbias, bp.part_dD, a->dA, a->ddt_bias, a->dD, B, H, K, 64,
+                           ssd::kBwsSlots, bp.has_D, bp.d_per_channel);
+        if (int rc = launch_status("k_bwd_finalize", tr, st)) return rc;
+        return ok();
+    }
     // state gradients dU_k (and dinitial_states)
     if ((int64_t)B * H >= kMinRevStreams) {
         if (bp.has_z)
@@ -474,7 +511,6 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
         if (int rc = launch_status("k_state_pass_bwd", tr, st)) return rc;
     }
     // chunk backward: (b, g, run of chunks) work units, about kBwdUnits of them
-    const int64_t bg = (int64_t)B * s->ngroups;
     int64_t nseg = (kBwdUnits + bg - 1) / bg;
     nseg = nseg < K ? nseg : K;
     const int M = (int)((K + nseg - 1) / nseg);

@@ -47,8 +47,17 @@ namespace ssd {
 constexpr int kBwsThreads = 512;  // 4 consumer + 4 producer waves
 constexpr int kBwsSlots = 4;      // partial sums per (b, h, k): one per consumer wave
 
-template <bool kHasZ>
+// kRevR = 0: steps in chunk order, the state gradients dU_k read from
+// prm.dstates.  kRevR = R (1, 2 or 4 heads per group, one run per stream):
+// chunks from last to first, and the producers carry each head's state
+// gradient g in registers (the reverse recurrence of k_bwd_dstate_rev fused
+// in), so no dU reaches HBM:
+//   dU_k = g;   g <- dSoff_k + exp(cs_last_k) g,   dSoff_k = (gy exp(cs))^T C,
+// starting from dfinal_state and ending at dinitial_states.
+template <bool kHasZ, int kRevR = 0>
 __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg, int M) {
+    static_assert(kRevR == 0 || kRevR == 1 || kRevR == 2 || kRevR == 4, "heads per group");
+    constexpr bool kRev = kRevR > 0;
     constexpr int T = 64, P = 64, N = 64;
     // x and gy tiles double buffered by step parity (the epilogue of step n
     // still reads them while step n + 1 runs); S, dU, B, C single
@@ -68,12 +77,14 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     const int r16 = lane & 15, kq = lane >> 4;
     const int sg = blockIdx.x % nseg, bg = blockIdx.x / nseg;
     const int g = bg % prm.G, b = bg / prm.G;
-    const int R = prm.R, H = prm.H, G = prm.G, K = prm.K;
+    const int R = kRev ? kRevR : prm.R, H = prm.H, G = prm.G, K = prm.K;
     const int kbeg = sg * M, kend = min(kbeg + M, K);
     const int NS = (kend - kbeg) * R;
     if (NS <= 0) return;
     const int rowHP4 = H * P * 4, rowGN4 = G * N * 4; // token strides, bytes
     auto tvalid = [&](int k) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
+    // chunk of step n: the run in order, or (kRev) from its last chunk back
+    auto chunk_of = [&](int n) { return kRev ? kend - 1 - n / R : kbeg + n / R; };
 
     // ------------------------------------------------------------ producers
     // Every step issues the same global loads, unconditionally (rows past the
@@ -93,7 +104,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         const float *Dp = prm.has_D ? prm.D : prm.A;
         auto load_xg = [&](int n) {
             n = min(n, NS - 1);
-            const int k = kbeg + n / R, h = g * R + n % R, tv = tvalid(k);
+            const int k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
             const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
             const auto rx = buf_rsrc(prm.x + xo);
             const auto rd = buf_rsrc(has_dout ? prm.dout + xo : prm.x + xo);
@@ -120,7 +131,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         auto load_bc = [&](int n) {
             const int range = (n < NS && n % R == 0) ? 0x7fffffff : 0;
             n = min(n, NS - 1);
-            const int k = kbeg + n / R, tv = tvalid(k);
+            const int k = chunk_of(n), tv = tvalid(k);
             const int64_t o = (((int64_t)b * prm.L + (int64_t)k * T) * G + g) * N;
             const auto rb = buf_rsrc_n(prm.B + o, range), rc = buf_rsrc_n(prm.C + o, range);
 #pragma unroll
@@ -130,16 +141,40 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 cr[j] = buf_load4(rc, lo, 0);
             }
         };
+        // kRev: the state-gradient carries of the group's heads, and S in the
+        // same MFMA accumulator layout: gc[r][pb][i] = g[p][n] of head g R + r,
+        // p = 16 pb + l % 16, n = 16 pw + 4 (l / 16) + i
+        f32x4 gc[kRev ? kRevR : 1][4];
+        const int acc_off = (r16 * N + 16 * pw + 4 * kq) * 4; // bytes, + 16 pb rows
+        if constexpr (kRev) {
+#pragma unroll
+            for (int rr = 0; rr < kRevR; ++rr)
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) {
+                    gc[rr][pb] = zero4();
+                    if (prm.dfinal) {
+                        const float4 v = *(const float4 *)((const char *)(prm.dfinal +
+                            ((int64_t)b * H + g * R + rr) * (P * N)) + acc_off + 16 * pb * N * 4);
+                        gc[rr][pb] = f32x4{v.x, v.y, v.z, v.w};
+                    }
+                }
+        }
         auto load_su = [&](int n) {
             n = min(n, NS - 1);
-            const int k = kbeg + n / R, h = g * R + n % R;
+            const int k = chunk_of(n), h = g * R + n % R;
             const int64_t so = (((int64_t)b * H + h) * K + k) * (int64_t)(P * N);
-            const auto rs = buf_rsrc(prm.states + so), ru = buf_rsrc(prm.dstates + so);
-            const int lo = (rt * N + c4) * 4;
+            const auto rs = buf_rsrc(prm.states + so);
+            if constexpr (kRev) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sr[j] = buf_load4(rs, lo, 16 * j * N * 4);
-                ur[j] = buf_load4(ru, lo, 16 * j * N * 4);
+                for (int pb = 0; pb < 4; ++pb) sr[pb] = buf_load4(rs, acc_off, 16 * pb * N * 4);
+            } else {
+                const auto ru = buf_rsrc(prm.dstates + so);
+                const int lo = (rt * N + c4) * 4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sr[j] = buf_load4(rs, lo, 16 * j * N * 4);
+                    ur[j] = buf_load4(ru, lo, 16 * j * N * 4);
+                }
             }
         };
         auto put = [&](SplitTile d, int row, float4 v) {
@@ -149,9 +184,11 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             *(half4 *)&d.lo[row * kTS + c4] = vl;
         };
         auto stage_xg = [&](int n) {
-            const int par = n & 1, k = kbeg + n / R, h = g * R + n % R, tv = tvalid(k);
+            const int par = n & 1, k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
             const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
-            const SplitTile xt = Xt(par), gt = Gt(par);
+            _Float16 *lp = opaque_lds(lds);
+            const SplitTile xt = tile_at(lp, par), gt = tile_at(lp, 2 + par);
+            const auto rdz = buf_rsrc(kHasZ ? prm.dz + xo : prm.x + xo);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = rt + 16 * j;
@@ -171,8 +208,11 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                         dzv[i] = dd[i] * pp[i] * sgm * (1.f + zz[i] * (1.f - sgm));
                     }
                     v = make_float4(gv[0], gv[1], gv[2], gv[3]);
-                    if (ok) *(float4 *)(prm.dz + xo + (int64_t)row * H * P + c4) =
-                        make_float4(dzv[0], dzv[1], dzv[2], dzv[3]);
+                    if (ok)
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned,
+                                               make_float4(dzv[0], dzv[1], dzv[2], dzv[3])),
+                            rdz, (rt * H * P + c4) * 4, 16 * j * rowHP4, 0);
                 }
                 put(gt, row, v);
             }
@@ -196,12 +236,14 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             }
         };
         auto stage_bc = [&](int n) {
-            const int tv = tvalid(kbeg + n / R);
+            const int tv = tvalid(chunk_of(n));
+            _Float16 *lp = opaque_lds(lds);
+            const SplitTile bt = tile_at(lp, 6), ct = tile_at(lp, 7);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const bool ok = rt + 16 * j < tv;
-                put(Bt, rt + 16 * j, ok ? br[j] : z4);
-                put(Ct, rt + 16 * j, ok ? cr[j] : z4);
+                put(bt, rt + 16 * j, ok ? br[j] : z4);
+                put(ct, rt + 16 * j, ok ? cr[j] : z4);
             }
         };
         auto stage_su = [&](int n) {
@@ -215,18 +257,73 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             sdu = wave_sum(sdu);
             if (lane == 0) s_sdu[n & 1][pw] = sdu;
         };
+        // kRev, step n of head slot rr: stage S and dU = the carry, then fold
+        // this chunk into the carry, g <- dSoff + exp2(cs_last) g, with
+        // dSoff^T[n][p] = sum_t (exp2(cs_t) C_t[n]) gy_t[p] from the C and gy
+        // tiles the consumers read in the same phase
+        auto put_acc = [&](SplitTile d, int pb, f32x4 v) {
+            half4 vh, vl;
+            split4(make_float4(v[0], v[1], v[2], v[3]), vh, vl);
+            *(half4 *)&d.hi[(16 * pb + r16) * kTS + 16 * pw + 4 * kq] = vh;
+            *(half4 *)&d.lo[(16 * pb + r16) * kTS + 16 * pw + 4 * kq] = vl;
+        };
+        auto stage_su_rev = [&](int n, auto slot_c) {
+            constexpr int rr = decltype(slot_c)::value;
+            const int par = n & 1;
+            _Float16 *lp = opaque_lds(lds);
+            const SplitTile st_ = tile_at(lp, 4), ut = tile_at(lp, 5), ct = tile_at(lp, 7);
+            float sdu = 0.f;
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) {
+                const f32x4 sv = f32x4{sr[pb].x, sr[pb].y, sr[pb].z, sr[pb].w};
+                put_acc(st_, pb, sv);
+                put_acc(ut, pb, gc[rr][pb]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sdu += sv[i] * gc[rr][pb][i];
+            }
+            sdu = wave_sum(sdu);
+            if (lane == 0) s_sdu[par][pw] = sdu;
+            // A operand: C^T rows 16 pw + l % 16 in the perm32 token order, each
+            // token scaled by exp2(cs_t)
+            Frag ae[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const Frag f = frag_tp(ct, m, 16 * pw);
+                const float4 e0 = *(const float4 *)&s_ecs[par][32 * m + 4 * kq];
+                const float4 e1 = *(const float4 *)&s_ecs[par][32 * m + 16 + 4 * kq];
+                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = ((float)f.h[j] + (float)f.l[j]) * ev[j];
+                ae[m] = pack_frag(v);
+            }
+            const SplitTile gt = tile_at(lp, 2 + par);
+            const float alpha = exp2_f(s_cs[par][T - 1]);
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) {
+                f32x4 d = zero4();
+#pragma unroll
+                for (int m = 0; m < 2; ++m) d = mma3f(ae[m], frag_tp(gt, m, 16 * pb), d);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gc[rr][pb][i] = d[i] + alpha * gc[rr][pb][i];
+                // one p-block's operands in flight at a time: the carries of
+                // every head are live here
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
 
         load_xg(0);
         load_bc(0);
         load_su(0);
         stage_xg(0);
         stage_bc(0);
-        load_xg(1);
-        load_bc(1);
+        if (!kRev) {
+            load_xg(1);
+            load_bc(1);
+        }
         lds_barrier();
         // every step: two barriers, as in the consumer loop
-        for (int n = 0; n < NS; ++n) {
-            stage_su(n);
+        auto step_rest = [&](int n) {
             load_su(n + 1);
             lds_barrier();
             if (n + 1 < NS) {
@@ -236,6 +333,54 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             load_xg(n + 2);
             load_bc(n + 2);
             lds_barrier();
+        };
+        if constexpr (kRev) {
+            // one chunk (its kRevR heads) per round, so each head's carry is a
+            // fixed register slot.  The tiles of step n + 1 are loaded after
+            // the carry update of step n and staged once the consumers leave
+            // phase A (half a step of latency cover, which keeps those
+            // registers free while the carries and the dSoff operands are
+            // live); B, C only by the step before a chunk's first.
+            auto rev_step = [&](int n, auto pos_c) {
+                constexpr int pos = decltype(pos_c)::value;
+                stage_su_rev(n, pos_c);
+                load_su(n + 1);
+                load_xg(n + 1);
+                if constexpr ((pos + 1) % kRevR == 0) load_bc(n + 1);
+                lds_barrier();
+                if (n + 1 < NS) {
+                    stage_xg(n + 1);
+                    if constexpr ((pos + 1) % kRevR == 0) stage_bc(n + 1);
+                }
+                lds_barrier();
+            };
+            using I0 = std::integral_constant<int, 0>;
+            using I1 = std::integral_constant<int, 1>;
+            using I2 = std::integral_constant<int, 2>;
+            using I3 = std::integral_constant<int, 3>;
+            for (int n0 = 0; n0 < NS; n0 += kRevR) {
+                rev_step(n0, I0{});
+                if constexpr (kRevR >= 2) rev_step(n0 + 1, I1{});
+                if constexpr (kRevR == 4) {
+                    rev_step(n0 + 2, I2{});
+                    rev_step(n0 + 3, I3{});
+                }
+            }
+            // the carries now hold the gradients of the initial states
+            if (prm.dinit) {
+#pragma unroll
+                for (int rr = 0; rr < kRevR; ++rr)
+#pragma unroll
+                    for (int pb = 0; pb < 4; ++pb)
+                        *(float4 *)((char *)(prm.dinit + ((int64_t)b * H + g * R + rr) * (P * N)) +
+                                    acc_off + 16 * pb * N * 4) =
+                            make_float4(gc[rr][pb][0], gc[rr][pb][1], gc[rr][pb][2], gc[rr][pb][3]);
+            }
+        } else {
+            for (int n = 0; n < NS; ++n) {
+                stage_su(n);
+                step_rest(n);
+            }
         }
         return;
     }
@@ -255,7 +400,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 
         // epilogue of step n (dxa holds its dxdt)
         auto epilogue = [&](int n) {
-            const int k = kbeg + n / R, h = g * R + n % R, par = n & 1;
+            const int k = chunk_of(n), h = g * R + n % R, par = n & 1;
             const int64_t t0 = (int64_t)k * T;
             const int tv = tvalid(k);
             const int64_t bhk = ((int64_t)b * H + h) * K + k;
@@ -331,7 +476,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 
         lds_barrier(); // first tiles staged
         for (int n = 0; n < NS; ++n) {
-            const int k = kbeg + n / R, r = n % R, par = n & 1;
+            const int k = chunk_of(n), r = n % R, par = n & 1;
             if (n > 0) epilogue(n - 1);
             _Float16 *la = opaque_lds(lds);
             const SplitTile xt = tile_at(la, par), gt = tile_at(la, 2 + par);

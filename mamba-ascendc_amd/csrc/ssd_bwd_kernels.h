@@ -29,7 +29,10 @@ struct BwdParams {
     float *dx, *ddt, *dB, *dC, *dz;
     const float *states;    // [B, H, K, P, N] state entering each chunk
     float *log_decay;       // [B, H, K] chunk sum of A q (written by k_bwd_dstate)
-    float *dstates;         // [B, H, K, P, N]: dSoff, then dU
+    float *dstates;         // [B, H, K, P, N]: dSoff, then dU (not used by the
+                            // reverse fused chunk kernel)
+    const float *dfinal;    // [B, H, P, N] or NULL (zero)
+    float *dinit;           // [B, H, P, N] or NULL
     float *part_dA;         // [B, H, K]
     float *part_dbias;      // [B, H, K]
     float *part_dD;         // [B, H, K, P] (per-channel D) or [B, H, K]

@@ -83,6 +83,11 @@ CASES = [
     # >= 512 (b, h) streams: the fused reverse state-gradient pass
     ([2, 200, 256, 64, 64, 64, 64], ("D2", "z", "bias", "init"), True, (0.0, math.inf), "both"),
     ([1, 192, 512, 64, 64, 64, 128], (), True, (0.0, math.inf), "final"),
+    # >= 256 (b, g) streams with 1, 2 or 4 heads per group: one reverse pass
+    # with the state gradients carried in the chunk kernel
+    ([4, 200, 256, 64, 64, 64, 64], ("D2", "z", "bias", "init"), True, (0.0, math.inf), "both"),
+    ([2, 130, 256, 64, 64, 64, 128], ("D", "bias"), True, (0.0, math.inf), "out"),
+    ([1, 100, 256, 64, 64, 64, 256], ("init",), True, (0.0, math.inf), "final"),
 ]
 
 
@@ -105,13 +110,15 @@ def test_backward_parity_small(shape, features, softplus, limit, mode):
         assert rl <= 2e-4, (k, rl)
 
 
-def test_backward_deterministic():
+@pytest.mark.parametrize("shape", [[2, 256, 8, 64, 64, 64, 2], [4, 130, 256, 64, 64, 64, 64]],
+                         ids=["split", "fused-reverse"])
+def test_backward_deterministic(shape):
     _need_gpu()
-    shape = [2, 256, 8, 64, 64, 64, 2]
+    b, l, h, p, n, _, _ = shape
     inp = make_inputs(shape, seed=3, features=("D", "bias"))
     gen = torch.Generator().manual_seed(6)
-    gy = torch.randn(2, 256, 8, 64, generator=gen)
-    gf = torch.randn(2, 8, 64, 64, generator=gen)
+    gy = torch.randn(b, l, h, p, generator=gen)
+    gf = torch.randn(b, h, p, n, generator=gen)
     a = _grads_gpu(inp, 64, True, (0.0, math.inf), gy, gf)
     c = _grads_gpu(inp, 64, True, (0.0, math.inf), gy, gf)
     for k in a:
@@ -177,8 +184,9 @@ def test_forward_chunk_states_are_prefix_final_states():
         assert rl <= 1e-5, (k, rl)
 
 
-@pytest.mark.parametrize("shape", [[2, 130, 8, 64, 64, 64, 2], [2, 130, 256, 64, 64, 64, 64]],
-                         ids=["chunk-parallel-dstate", "reverse-dstate"])
+@pytest.mark.parametrize("shape", [[2, 130, 8, 64, 64, 64, 2], [2, 130, 256, 64, 64, 64, 64],
+                                   [4, 130, 256, 64, 64, 64, 64]],
+                         ids=["chunk-parallel-dstate", "reverse-dstate", "fused-reverse"])
 def test_backward_saved_states_match_recompute(shape):
     """The backward from the forward's saved chunk states and the backward that
     recomputes them give the same gradients."""

@@ -80,7 +80,10 @@ def test_workspace_size_formula():
     """Forward plan: P = N = 64 runs the fused segment-serial kernel, which
     needs no workspace when there are >= 1024 (b, h) streams (C3) and a
     per-segment state buffer otherwise; N = 128 runs the chunk path with a
-    [B,H,K,P,N] state buffer.  The backward needs states, dstates and partials."""
+    [B,H,K,P,N] state buffer.  The backward needs states (unless the forward's
+    are passed in), per-chunk partials, and dstates only where the state
+    gradients are not carried in the reverse fused chunk kernel (fewer than
+    256 (b, g) streams, or other than 1, 2 or 4 heads per group)."""
     lib = rt.load_library()
     nbytes = ctypes.c_size_t(0)
 
@@ -100,12 +103,20 @@ def test_workspace_size_formula():
     bwd = lib.mamba2_ssd_bwd_m1_workspace_size
     k = 4096 // 64
     state_buf = 8 * 256 * k * 64 * 64 * 4
+    # C3: 512 (b, g) streams, 4 heads per group -> reverse fused, no dstates
     full = ws(bwd, batch=8, seqlen=4096, nheads=256, ngroups=64)
-    assert full >= 2 * state_buf
+    assert state_buf <= full < 2 * state_buf
     # with the forward's chunk states passed in, the recompute buffer goes away
     assert bwd(ctypes.byref(_shape(batch=8, seqlen=4096, nheads=256, ngroups=64)), rt.SAVED_STATES,
                ctypes.byref(nbytes)) == 0
     assert full - nbytes.value == state_buf
+    assert nbytes.value < state_buf // 8  # partials only
+    # 8 heads per group: split path with a dstates buffer
+    split = ws(bwd, batch=8, seqlen=4096, nheads=256, ngroups=32)
+    assert split >= 2 * state_buf
+    # too few streams for one reverse pass per (b, g): split path
+    k = 2048 // 64
+    assert ws(bwd, batch=4, seqlen=2048, nheads=16, ngroups=4) >= 2 * 4 * 16 * k * 64 * 64 * 4
 
 
 def test_fwd_rejects_null_and_flag_mismatch_without_gpu():
