@@ -68,8 +68,8 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     __shared__ float s_dcs[2][T], s_rd[2][T], s_sdu[2][4], s_A[2];
     __shared__ __attribute__((aligned(16))) float s_da[4][T]; // epilogue: da of a step, per consumer wave
 
-    auto Xt = [&](int par) { return tile_at(lds, par); };
-    auto Gt = [&](int par) { return tile_at(lds, 2 + par); };
+    auto Xt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, par); };
+    auto Gt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, 2 + par); };
     const SplitTile St = tile_at(lds, 4), Ut = tile_at(lds, 5), Bt = tile_at(lds, 6),
                     Ct = tile_at(lds, 7);
 
@@ -82,9 +82,9 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     const int NS = (kend - kbeg) * R;
     if (NS <= 0) return;
     const int rowHP4 = H * P * 4, rowGN4 = G * N * 4; // token strides, bytes
-    auto tvalid = [&](int k) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
+    auto tvalid = [&](int k) __attribute__((always_inline)) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
     // chunk of step n: the run in order, or (kRev) from its last chunk back
-    auto chunk_of = [&](int n) { return kRev ? kend - 1 - n / R : kbeg + n / R; };
+    auto chunk_of = [&](int n) __attribute__((always_inline)) { return kRev ? kend - 1 - n / R : kbeg + n / R; };
 
     // ------------------------------------------------------------ producers
     // Every step issues the same global loads, unconditionally (rows past the
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         float dtr = 0.f, Ahr = 0.f, biasr = 0.f, Dr = 0.f;
         const float *dtb = prm.dt_bias ? prm.dt_bias : prm.A; // read unconditionally
         const float *Dp = prm.has_D ? prm.D : prm.A;
-        auto load_xg = [&](int n) {
+        auto load_xg = [&](int n) __attribute__((always_inline)) {
             n = min(n, NS - 1);
             const int k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
             const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         // B, C of the chunk of step n, read for real only when step n starts
         // a chunk (the only steps whose B, C get staged); the other steps
         // issue the same loads through an empty-range resource
-        auto load_bc = [&](int n) {
+        auto load_bc = [&](int n) __attribute__((always_inline)) {
             const int range = (n < NS && n % R == 0) ? 0x7fffffff : 0;
             n = min(n, NS - 1);
             const int k = chunk_of(n), tv = tvalid(k);
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                     }
                 }
         }
-        auto load_su = [&](int n) {
+        auto load_su = [&](int n) __attribute__((always_inline)) {
             n = min(n, NS - 1);
             const int k = chunk_of(n), h = g * R + n % R;
             const int64_t so = (((int64_t)b * H + h) * K + k) * (int64_t)(P * N);
@@ -177,23 +177,25 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 }
             }
         };
-        auto put = [&](SplitTile d, int row, float4 v) {
+        auto put = [&](SplitTile d, int row, float4 v) __attribute__((always_inline)) {
             half4 vh, vl;
             split4(v, vh, vl);
             *(half4 *)&d.hi[row * kTS + c4] = vh;
             *(half4 *)&d.lo[row * kTS + c4] = vl;
         };
-        auto stage_xg = [&](int n) {
+        auto stage_xg = [&](int n) __attribute__((always_inline)) {
             const int par = n & 1, k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
             const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
             _Float16 *lp = opaque_lds(lds);
             const SplitTile xt = tile_at(lp, par), gt = tile_at(lp, 2 + par);
             const auto rdz = buf_rsrc(kHasZ ? prm.dz + xo : prm.x + xo);
+            float4 dD4 = z4; // sum over this lane's rows of x gy, columns c4 .. c4 + 3
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = rt + 16 * j;
                 const bool ok = row < tv;
-                put(xt, row, ok ? xr[j] : z4);
+                const float4 xv = ok ? xr[j] : z4;
+                put(xt, row, xv);
                 const float4 dv = (ok && has_dout) ? gr[j] : z4;
                 float4 v = dv;
                 if (kHasZ) {
@@ -215,6 +217,21 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                             rdz, (rt * H * P + c4) * 4, 16 * j * rowHP4, 0);
                 }
                 put(gt, row, v);
+                dD4.x += xv.x * v.x;
+                dD4.y += xv.y * v.y;
+                dD4.z += xv.z * v.z;
+                dD4.w += xv.w * v.w;
+            }
+            // dD partials of this wave's rows: slot pw of (b, h, k)
+            if (prm.has_D) {
+                const int64_t bhk = ((int64_t)b * H + h) * K + k;
+                if (prm.d_per_channel) {
+                    const float4 t4 = make_float4(sum_kq(dD4.x), sum_kq(dD4.y), sum_kq(dD4.z), sum_kq(dD4.w));
+                    if (lane < 16) *(float4 *)(prm.part_dD + (bhk * kBwsSlots + pw) * P + c4) = t4;
+                } else {
+                    const float tot = wave_sum(dD4.x + dD4.y + dD4.z + dD4.w);
+                    if (lane == 0) prm.part_dD[bhk * kBwsSlots + pw] = tot;
+                }
             }
             if (pw == 0) {
                 float q = 0.f, a = 0.f, dq = 0.f;
@@ -235,7 +252,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 if (lane == 0) s_A[par] = Ahr;
             }
         };
-        auto stage_bc = [&](int n) {
+        auto stage_bc = [&](int n) __attribute__((always_inline)) {
             const int tv = tvalid(chunk_of(n));
             _Float16 *lp = opaque_lds(lds);
             const SplitTile bt = tile_at(lp, 6), ct = tile_at(lp, 7);
@@ -246,7 +263,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 put(ct, rt + 16 * j, ok ? cr[j] : z4);
             }
         };
-        auto stage_su = [&](int n) {
+        auto stage_su = [&](int n) __attribute__((always_inline)) {
             float sdu = 0.f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -261,13 +278,13 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         // this chunk into the carry, g <- dSoff + exp2(cs_last) g, with
         // dSoff^T[n][p] = sum_t (exp2(cs_t) C_t[n]) gy_t[p] from the C and gy
         // tiles the consumers read in the same phase
-        auto put_acc = [&](SplitTile d, int pb, f32x4 v) {
+        auto put_acc = [&](SplitTile d, int pb, f32x4 v) __attribute__((always_inline)) {
             half4 vh, vl;
             split4(make_float4(v[0], v[1], v[2], v[3]), vh, vl);
             *(half4 *)&d.hi[(16 * pb + r16) * kTS + 16 * pw + 4 * kq] = vh;
             *(half4 *)&d.lo[(16 * pb + r16) * kTS + 16 * pw + 4 * kq] = vl;
         };
-        auto stage_su_rev = [&](int n, auto slot_c) {
+        auto stage_su_rev = [&](int n, auto slot_c) __attribute__((always_inline)) {
             constexpr int rr = decltype(slot_c)::value;
             const int par = n & 1;
             _Float16 *lp = opaque_lds(lds);
@@ -323,7 +340,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         }
         lds_barrier();
         // every step: two barriers, as in the consumer loop
-        auto step_rest = [&](int n) {
+        auto step_rest = [&](int n) __attribute__((always_inline)) {
             load_su(n + 1);
             lds_barrier();
             if (n + 1 < NS) {
@@ -341,7 +358,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             // phase A (half a step of latency cover, which keeps those
             // registers free while the carries and the dSoff operands are
             // live); B, C only by the step before a chunk's first.
-            auto rev_step = [&](int n, auto pos_c) {
+            auto rev_step = [&](int n, auto pos_c) __attribute__((always_inline)) {
                 constexpr int pos = decltype(pos_c)::value;
                 stage_su_rev(n, pos_c);
                 load_su(n + 1);
@@ -387,10 +404,16 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 
     // ------------------------------------------------------------ consumers
     // No global loads: every operand comes from LDS, every output is a store.
-    auto consumer = [&](auto wave_c) {
+    // The products that end in per-token outputs are formed transposed
+    // (operands swapped), so each lane owns token `own` and channels
+    // 16 blk + 4 (l / 16) + 0..3 of every 16-channel block: per-token factors
+    // are per-lane scalars, the sums over channels a 4-lane reduction, and
+    // the dx, dB, dC rows leave as 16-byte stores.
+    auto consumer = [&](auto wave_c) __attribute__((always_inline)) {
         constexpr int W = decltype(wave_c)::value;
-        const int own = 16 * W + r16;     // operand row of this lane
-        const int trow = 16 * W + 4 * kq; // first of the 4 accumulator rows of this lane
+        const int own = 16 * W + r16; // token of this lane (its operand row)
+        const int cq = 4 * kq;        // first of its 4 channels in each 16-channel block
+        // dxa[pb][i] = dxdt[own][16 pb + cq + i]; dBa, dCa likewise over n
         f32x4 dBa[4], dCa[4], dxa[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -399,7 +422,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         }
 
         // epilogue of step n (dxa holds its dxdt)
-        auto epilogue = [&](int n) {
+        auto epilogue = [&](int n) __attribute__((always_inline)) {
             const int k = chunk_of(n), h = g * R + n % R, par = n & 1;
             const int64_t t0 = (int64_t)k * T;
             const int tv = tvalid(k);
@@ -415,63 +438,51 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             }
             const float Ah = s_A[par];
             const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
-            f32x4 xa[4], ga[4];
-            float Dv[4];
+            f32x4 xa[4], ga[4], Dv[4];
             _Float16 *le = opaque_lds(lds);
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
-                xa[pb] = tile_acc(tile_at(le, par), 16 * W, 16 * pb);
-                ga[pb] = tile_acc(tile_at(le, 2 + par), 16 * W, 16 * pb);
-                Dv[pb] = s_D[par][prm.d_per_channel ? 16 * pb + r16 : 0];
-            }
-            // da of this lane's 4 accumulator rows: through this wave's LDS row
-            // (written and read back by the same wave, so no barrier)
-            s_da[W][lane] = da;
-            const float4 da4 = *(const float4 *)&s_da[W][trow];
-            const float4 q4 = *(const float4 *)&s_q[par][trow];
-            const float4 u4 = *(const float4 *)&s_dqdu[par][trow];
-            const float dav[4] = {da4.x, da4.y, da4.z, da4.w}, qv4[4] = {q4.x, q4.y, q4.z, q4.w},
-                        uv4[4] = {u4.x, u4.y, u4.z, u4.w};
-            // stores through buffer resources: a per-lane row offset plus scalar
-            // and immediate offsets instead of 64-bit addresses
-            const auto rdx = buf_rsrc(prm.dx + xo);
-            const auto rddt = buf_rsrc(prm.ddt + ((int64_t)b * prm.L + t0) * H + h);
-            const int vrow = trow * rowHP4 + 4 * r16;
-            float dbias = 0.f, dDp[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int t = trow + rr;
-                const bool valid = t < tv;
-                const float da_t = dav[rr];
-                const float q_t = qv4[rr];
-                const float dqp = sum16(xa[0][rr] * dxa[0][rr] + xa[1][rr] * dxa[1][rr] +
-                                        xa[2][rr] * dxa[2][rr] + xa[3][rr] * dxa[3][rr]);
-                const float ddt = valid ? (Ah * da_t + dqp) * uv4[rr] : 0.f;
-                if (r16 == 0) {
-                    if (valid) buf_store(rddt, trow * H * 4, rr * H * 4, ddt);
-                    dbias += ddt;
+                xa[pb] = tile_row4(tile_at(le, par), own, 16 * pb + cq);
+                ga[pb] = tile_row4(tile_at(le, 2 + par), own, 16 * pb + cq);
+                if (prm.d_per_channel) {
+                    const float4 d4 = *(const float4 *)&s_D[par][16 * pb + cq];
+                    Dv[pb] = f32x4{d4.x, d4.y, d4.z, d4.w};
+                } else {
+                    const float d1 = s_D[par][0];
+                    Dv[pb] = f32x4{d1, d1, d1, d1};
                 }
+            }
+            // da of token own: through this wave's LDS row (written and read
+            // back by the same wave, so no barrier)
+            s_da[W][lane] = da;
+            const float da_o = s_da[W][own];
+            const float q_o = s_q[par][own], u_o = s_dqdu[par][own];
+            float dqp = 0.f;
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dqp += xa[pb][i] * dxa[pb][i];
+            dqp = sum_kq(dqp);
+            const bool valid = own < tv;
+            const float ddt = valid ? (Ah * da_o + dqp) * u_o : 0.f;
+            // stores through buffer resources: a per-lane row offset plus
+            // immediate offsets instead of 64-bit addresses
+            if (valid) {
+                if (kq == 0)
+                    buf_store(buf_rsrc(prm.ddt + ((int64_t)b * prm.L + t0) * H + h), own * H * 4, 0, ddt);
+                const auto rdx = buf_rsrc(prm.dx + xo);
 #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) {
-                    const float gyv = ga[pb][rr];
-                    dDp[pb] += gyv * xa[pb][rr];
-                    if (valid) buf_store(rdx, vrow + 64 * pb, rr * rowHP4, q_t * dxa[pb][rr] + Dv[pb] * gyv);
-                }
-            }
-            dbias = wave_sum(dbias);
-            if (lane == 0) prm.part_dbias[bhk * kBwsSlots + W] = dbias;
-            if (prm.has_D) {
-                if (prm.d_per_channel) {
+                    f32x4 o;
 #pragma unroll
-                    for (int pb = 0; pb < 4; ++pb) {
-                        const float vv = sum_kq(dDp[pb]);
-                        if (kq == 0) prm.part_dD[(bhk * kBwsSlots + W) * P + 16 * pb + r16] = vv;
-                    }
-                } else {
-                    const float tot = wave_sum(dDp[0] + dDp[1] + dDp[2] + dDp[3]);
-                    if (lane == 0) prm.part_dD[bhk * kBwsSlots + W] = tot;
+                    for (int i = 0; i < 4; ++i) o[i] = q_o * dxa[pb][i] + Dv[pb][i] * ga[pb][i];
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o), rdx,
+                        own * rowHP4 + (16 * pb + cq) * 4, 0, 0);
                 }
             }
+            const float dbias = wave_sum(kq == 0 ? ddt : 0.f);
+            if (lane == 0) prm.part_dbias[bhk * kBwsSlots + W] = dbias;
         };
 
         lds_barrier(); // first tiles staged
@@ -569,26 +580,27 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 cols = sum_kq(cols);
                 if (kq == 0) s_dcs[par][own] = rows - cols;
 
-                // dxdt = W^T gy (rows s of this wave)
+                // dxdt^T = gy^T W (column s = own)
 #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) dxa[pb] = zero4();
 #pragma unroll
                 for (int m = 0; m < 2; ++m)
                     if (2 * m + 1 >= W)
 #pragma unroll
-                        for (int pb = 0; pb < 4; ++pb) dxa[pb] = mma3f(WS[m], frag_tp(gt, m, 16 * pb), dxa[pb]);
-                // dC += dCB B (rows t), dB += dCB^T C (rows s)
+                        for (int pb = 0; pb < 4; ++pb) dxa[pb] = mma3f(frag_tp(gt, m, 16 * pb), WS[m], dxa[pb]);
+                // dC^T += B^T dCB^T (column t = own), dB^T += C^T dCB (column s = own)
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
                     if (2 * m <= W)
 #pragma unroll
-                        for (int nb = 0; nb < 4; ++nb) dCa[nb] = mma3f(DCT[m], frag_tp(Bt, m, 16 * nb), dCa[nb]);
+                        for (int nb = 0; nb < 4; ++nb) dCa[nb] = mma3f(frag_tp(Bt, m, 16 * nb), DCT[m], dCa[nb]);
                     if (2 * m + 1 >= W)
 #pragma unroll
-                        for (int nb = 0; nb < 4; ++nb) dBa[nb] = mma3f(DCS[m], frag_tp(Ct, m, 16 * nb), dBa[nb]);
+                        for (int nb = 0; nb < 4; ++nb) dBa[nb] = mma3f(frag_tp(Ct, m, 16 * nb), DCS[m], dBa[nb]);
                 }
+                // C[own][.] for phase B (the producers may restage C then)
 #pragma unroll
-                for (int nb = 0; nb < 4; ++nb) ca[nb] = tile_acc(Ct, 16 * W, 16 * nb);
+                for (int nb = 0; nb < 4; ++nb) ca[nb] = tile_row4(Ct, own, 16 * nb + cq);
             }
             lds_barrier(); // S, dU staged; B, C of the next chunk may now be staged
 
@@ -596,33 +608,25 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             _Float16 *lb = opaque_lds(lds);
             const SplitTile xb = tile_at(lb, par), gb = tile_at(lb, 2 + par);
             const SplitTile St = tile_at(lb, 4), Ut = tile_at(lb, 5);
-            float tq[4], tdte[4], tecs[4];
+            const float q_o = s_q[par][own], dte_o = s_dte[par][own], ecs_o = s_ecs[par][own];
+            float rpart = 0.f, gpart = 0.f;
             {
-                const float4 a = *(const float4 *)&s_q[par][trow];
-                const float4 d = *(const float4 *)&s_dte[par][trow];
-                const float4 e = *(const float4 *)&s_ecs[par][trow];
-                tq[0] = a.x, tq[1] = a.y, tq[2] = a.z, tq[3] = a.w;
-                tdte[0] = d.x, tdte[1] = d.y, tdte[2] = d.z, tdte[3] = d.w;
-                tecs[0] = e.x, tecs[1] = e.y, tecs[2] = e.z, tecs[3] = e.w;
-            }
-            float rpart[4] = {0.f, 0.f, 0.f, 0.f}, gpart[4] = {0.f, 0.f, 0.f, 0.f};
-            {
-                // B dU^T: [t][p]
+                // (B dU^T)^T: [p][t]
 #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) {
                     f32x4 rm = zero4();
 #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) rm = mma3f(Bo[ks], frag(Ut, 16 * pb + r16, ks), rm);
-                    const f32x4 xv = tile_acc(xb, 16 * W, 16 * pb);
+                    for (int ks = 0; ks < 2; ++ks) rm = mma3f(frag(Ut, 16 * pb + r16, ks), Bo[ks], rm);
+                    const f32x4 xv = tile_row4(xb, own, 16 * pb + cq);
 #pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) {
-                        dxa[pb][rr] += tdte[rr] * rm[rr];
-                        rpart[rr] += xv[rr] * rm[rr];
+                    for (int i = 0; i < 4; ++i) {
+                        dxa[pb][i] += dte_o * rm[i];
+                        rpart += xv[i] * rm[i];
                     }
                 }
             }
             {
-                // gy S: [t][n]
+                // (gy S)^T: [n][t]
                 Frag Go[2];
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) Go[ks] = frag(gb, own, ks);
@@ -630,52 +634,49 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 for (int nb = 0; nb < 4; ++nb) {
                     f32x4 co = zero4();
 #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) co = mma3f(Go[ks], frag_tn(St, ks, 16 * nb), co);
+                    for (int ks = 0; ks < 2; ++ks) co = mma3f(frag_tn(St, ks, 16 * nb), Go[ks], co);
 #pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) {
-                        const float vv = tecs[rr] * co[rr];
-                        dCa[nb][rr] += vv;
-                        gpart[rr] += vv * ca[nb][rr];
+                    for (int i = 0; i < 4; ++i) {
+                        const float vv = ecs_o * co[i];
+                        dCa[nb][i] += vv;
+                        gpart += vv * ca[nb][i];
                     }
                 }
             }
             {
-                // x dU: [t][n]
+                // (x dU)^T: [n][t]
                 Frag Xo[2];
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) Xo[ks] = frag(xb, own, ks);
+                const float sq = dte_o * q_o;
 #pragma unroll
                 for (int nb = 0; nb < 4; ++nb) {
                     f32x4 bs = zero4();
 #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) bs = mma3f(Xo[ks], frag_tn(Ut, ks, 16 * nb), bs);
+                    for (int ks = 0; ks < 2; ++ks) bs = mma3f(frag_tn(Ut, ks, 16 * nb), Xo[ks], bs);
 #pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) dBa[nb][rr] += tdte[rr] * tq[rr] * bs[rr];
+                    for (int i = 0; i < 4; ++i) dBa[nb][i] += sq * bs[i];
                 }
             }
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const float rd = sum16(rpart[rr]) * tq[rr] * tdte[rr];
-                const float gp = sum16(gpart[rr]);
-                if (r16 == 0) {
-                    s_dcs[par][trow + rr] += gp - rd;
-                    s_rd[par][trow + rr] = rd;
+            {
+                const float rd = sum_kq(rpart) * q_o * dte_o;
+                const float gp = sum_kq(gpart);
+                if (kq == 0) {
+                    s_dcs[par][own] += gp - rd;
+                    s_rd[par][own] = rd;
                 }
             }
             if (r == R - 1) {
                 const int64_t t0 = (int64_t)k * T;
-                const int tv = tvalid(k);
-                const int64_t o = (((int64_t)b * prm.L + t0) * G + g) * N;
-                const auto rdB = buf_rsrc(prm.dB + o), rdC = buf_rsrc(prm.dC + o);
-                const int vrow = trow * rowGN4 + 4 * r16;
+                if (own < tvalid(k)) {
+                    const int64_t o = (((int64_t)b * prm.L + t0) * G + g) * N;
+                    const auto rdB = buf_rsrc(prm.dB + o), rdC = buf_rsrc(prm.dC + o);
+                    typedef __attribute__((ext_vector_type(4))) unsigned u4;
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    if (trow + rr < tv) {
-#pragma unroll
-                        for (int nb = 0; nb < 4; ++nb) {
-                            buf_store(rdB, vrow + 64 * nb, rr * rowGN4, dBa[nb][rr]);
-                            buf_store(rdC, vrow + 64 * nb, rr * rowGN4, dCa[nb][rr]);
-                        }
+                    for (int nb = 0; nb < 4; ++nb) {
+                        const int off = own * rowGN4 + (16 * nb + cq) * 4;
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, dBa[nb]), rdB, off, 0, 0);
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, dCa[nb]), rdC, off, 0, 0);
                     }
                 }
 #pragma unroll

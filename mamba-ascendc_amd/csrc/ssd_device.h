@@ -366,6 +366,11 @@ __device__ __forceinline__ f32x4 tile_acc(SplitTile s, int row0, int c0) {
     return join4(tr4(s.hi, k0, c0), tr4(s.lo, k0, c0));
 }
 
+// fp32 values of tile[row][c0 .. c0 + 3] (one 8-byte read of each half).
+__device__ __forceinline__ f32x4 tile_row4(SplitTile s, int row, int c0) {
+    return join4(*(const half4 *)&s.hi[row * kTS + c0], *(const half4 *)&s.lo[row * kTS + c0]);
+}
+
 // Value of v in lane `lane` (which must be the same for the whole wave).
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
