@@ -325,6 +325,47 @@ def copy_bandwidth(torch, nbytes=1 << 30, reps=5):
     return 2 * nbytes / (best * 1e-3) / 1e9
 
 
+def bench_state_passing(torch, lib, shape, steps=10, warmup=3):
+    """The standalone inter-chunk state-passing op (C ABI
+    mamba2_ssd_state_passing, the reference's mamba2_ssd_state_passing stage) on
+    this configuration's [B, H, K, P, N] chunk states: ms per call and GB/s of
+    its algorithmic traffic (chunk states in, states_start out, the log decays
+    and final state)."""
+    b, l, h, p, n, _chunk, _g = shape
+    k = math.ceil(l / EXEC_CHUNK)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    states = torch.randn(b, h, k, p, n, device="cuda", generator=gen)
+    log_decay = -torch.rand(b, h, k, device="cuda", generator=gen)
+    start = torch.empty_like(states)
+    final = torch.empty(b, h, p, n, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    V = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def call():
+        rc = lib.mamba2_ssd_state_passing(V(states), V(log_decay), None, V(start), V(final),
+                                          b, h, k, p, n, stream)
+        if rc != 0:
+            raise RuntimeError(f"mamba2_ssd_state_passing failed ({rc})")
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(steps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        call()
+        e.record()
+        e.synchronize()
+        samples.append(s.elapsed_time(e))
+    ms = statistics.median(samples)
+    nbytes = 4 * (2 * b * h * k * p * n + b * h * k + b * h * p * n)
+    del states, start, final, log_decay
+    torch.cuda.empty_cache()
+    return {"ms": round(ms, 5), "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes,
+            "frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
 def bench_api(torch, api, inp, chunk, steps, warmup):
     """Per-call device-event time through the public Python API."""
     def call():
@@ -697,6 +738,11 @@ def main(argv=None):
         f"{d['GB_s'] / copy_gbs:.2f} of it")
     roofline["copy_GB_s"] = round(copy_gbs, 1)
     roofline["frac_of_copy"] = d["GB_s"] / copy_gbs
+    state_pass = bench_state_passing(torch, lib, shape)
+    state_pass["frac_of_copy"] = state_pass["GB_s"] / copy_gbs
+    log(f"state passing op on [B,H,K,P,N] = {shape[0]},{shape[2]},{math.ceil(shape[1] / EXEC_CHUNK)},"
+        f"{shape[3]},{shape[4]}: {state_pass['ms']:.4f} ms, {state_pass['GB_s']:.0f} GB/s "
+        f"({100 * state_pass['frac']:.0f} % of 8 TB/s)")
 
     cpu = None
     if not args.no_cpu:
@@ -730,6 +776,7 @@ def main(argv=None):
         "api_fwd_bwd_ms": None if api_fwd_bwd_ms is None else round(api_fwd_bwd_ms, 5),
         "bwd_kernels": bwd_kern,
         "api_fwd_ms": round(api_ms, 5),
+        "state_passing": state_pass,
         "op": {
             "flops": flops,
             "bytes": nbytes,
