@@ -100,6 +100,20 @@ class HipEvents:
 
 # ----------------------------------------------------------------------------- work model
 
+def fwd_segments(shape):
+    """(nseg, nsplit) of the fused forward's plan (mamba2_ssd.hip fwd_plan):
+    dstate 128 runs as two state halves, and segments are added until there
+    are about 1024 (b, h, half) work units."""
+    b, l, h, p, n, _chunk, g = shape
+    k = math.ceil(l / EXEC_CHUNK)
+    nsplit = n // 64
+    streams = b * h * nsplit
+    nseg = 1 if streams >= 1024 else -(-1024 // streams)
+    nseg = min(nseg, k)
+    m = -(-k // nseg)
+    return -(-k // m), nsplit
+
+
 def fwd_kernel_model(name: str, shape) -> dict:
     """Algorithmic bytes and flops of one launch of a forward kernel.
 
@@ -118,13 +132,16 @@ def fwd_kernel_model(name: str, shape) -> dict:
         per = f4 * (T * p + T + T * n / r + p * n + 1)
         fl = 2 * T * p * n
     elif name == "k_state_pass":
+        # between the fused forward's segments: segment states in and out
+        nseg, _ = fwd_segments(shape)
+        su = b * h * nseg
         per = f4 * (2 * p * n + 1)
-        fl = 2 * p * n
-        return {"bytes": units * per + b * h * p * n * f4, "flops": units * fl, "units": units,
+        return {"bytes": su * per + b * h * p * n * f4, "flops": su * 2 * p * n, "units": su,
                 "bytes_per_unit": per}
-    elif name == "k_chunk_scan":
-        per = f4 * (2 * T * p + T + p * n + 2 * T * n / r)
-        fl = 2 * (T * T * n / r + T * T * p + T * n * p)
+    elif name == "k_fwd_combine":
+        # dstate 128: the two halves' outputs in, the sum out
+        per = f4 * 3 * T * p
+        fl = T * p
     elif name == "k_fwd_seg":
         # fused: x, dt, B, C in, y out; the state stays on chip (segment
         # entry/exit states are a few per stream and not counted)

@@ -63,24 +63,20 @@ int check_shape(const Mamba2SsdShape *s, uint32_t flags) {
     return MAMBA2_SSD_OK;
 }
 
-// Shapes served by the MFMA chunk kernels; everything else runs the generic
-// token recurrence.
-bool fast_path(const Mamba2SsdShape *s) {
-    return s->headdim == 64 && (s->dstate == 64 || s->dstate == 128);
-}
-
 int64_t nchunks(const Mamba2SsdShape *s) { return (s->seqlen + ssd::kChunk - 1) / ssd::kChunk; }
 
-// Forward plan.  headdim = dstate = 64 runs the fused segment-serial kernel:
-// segments are added only when there are fewer than kMinStreams (b, h)
-// streams, so that the grid still has about that many workgroups.  Other
-// MFMA shapes run the three-kernel chunk path.
+// Forward plan.  headdim = 64 with dstate = 64 or 128 runs the fused
+// segment-serial kernel (dstate 128 as two 64-column state halves, one
+// workgroup each): segments are added only when there are fewer than
+// kMinStreams (b, h, half) streams, so that the grid still has about that
+// many workgroups.
 constexpr int64_t kMinStreams = 1024;
 
 struct FwdPlan {
-    bool fused = false, chunked = false;
-    int nseg = 1, M = 1;
+    bool fused = false;
+    int nseg = 1, M = 1, nsplit = 1;
     size_t seg_state = 0, seg_decay = 0; // workspace offsets (fused, nseg > 1)
+    size_t y_half = 0;                   // workspace offset (fused, nsplit = 2)
     size_t ws = 0;
 };
 
@@ -89,23 +85,28 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s) {
     if (s->seqlen == 0) return pl;
     const int64_t K = nchunks(s), streams = s->batch * s->nheads;
     const size_t pn = (size_t)s->headdim * s->dstate;
-    if (s->headdim == 64 && s->dstate == 64) {
+    if (s->headdim == 64 && (s->dstate == 64 || s->dstate == 128)) {
         pl.fused = true;
-        int64_t nseg = streams >= kMinStreams ? 1 : (kMinStreams + streams - 1) / streams;
+        pl.nsplit = (int)(s->dstate / 64);
+        const int64_t wstreams = streams * pl.nsplit;
+        int64_t nseg = wstreams >= kMinStreams ? 1 : (kMinStreams + wstreams - 1) / wstreams;
         nseg = nseg < K ? nseg : K;
         const int64_t M = (K + nseg - 1) / nseg;
         pl.M = (int)M;
         pl.nseg = (int)((K + M - 1) / M);
+        size_t off = 0;
         if (pl.nseg > 1) {
             const size_t units = (size_t)streams * pl.nseg;
-            pl.seg_state = 0;
-            pl.seg_decay = align256(units * pn * sizeof(float));
-            pl.ws = pl.seg_decay + align256(units * sizeof(float));
+            pl.seg_state = off;
+            off += align256(units * pn * sizeof(float));
+            pl.seg_decay = off;
+            off += align256(units * sizeof(float));
         }
-    } else if (fast_path(s)) {
-        pl.chunked = true;
-        const size_t bhk = (size_t)streams * K;
-        pl.ws = align256(bhk * pn * sizeof(float)) + align256(bhk * sizeof(float));
+        if (pl.nsplit > 1) {
+            pl.y_half = off;
+            off += align256((size_t)s->batch * s->seqlen * s->nheads * s->headdim * sizeof(float));
+        }
+        pl.ws = off;
     }
     return pl;
 }
@@ -139,21 +140,6 @@ int launch_status(const char *what, Trace *tr = nullptr, hipStream_t st = nullpt
     if (e != hipSuccess)
         return fail(MAMBA2_SSD_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
     return record(tr, st, what);
-}
-
-template <int P, int N>
-int launch_fwd_fast(const ssd::FwdParams &prm, int B, hipStream_t st, Trace *tr) {
-    const dim3 grid(prm.K, prm.H, B);
-    if (int rc = record(tr, st, nullptr)) return rc;
-    hipLaunchKernelGGL((ssd::k_chunk_state<P, N>), grid, dim3(ssd::kThreads), 0, st, prm);
-    if (int rc = launch_status("k_chunk_state", tr, st)) return rc;
-    const int PN = P * N;
-    const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
-    hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, prm.states,
-                       prm.chunk_log_decay, prm.init, prm.states, prm.final_state, prm.K, PN);
-    if (int rc = launch_status("k_state_pass", tr, st)) return rc;
-    hipLaunchKernelGGL((ssd::k_chunk_scan<P, N>), grid, dim3(ssd::kThreads), 0, st, prm);
-    return launch_status("k_chunk_scan", tr, st);
 }
 
 }  // namespace
@@ -252,14 +238,24 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         ssd::SegParams sp{};
         sp.nseg = pl.nseg;
         sp.M = pl.M;
-        const unsigned units = (unsigned)(s->batch * s->nheads * pl.nseg);
+        sp.nsplit = pl.nsplit;
+        const unsigned units = (unsigned)(s->batch * s->nheads * pl.nseg * pl.nsplit);
+        // with two state halves the halves' sum, D x, pre_gate and the z gate
+        // are applied by k_fwd_combine
+        ssd::FwdParams kp = prm;
+        if (pl.nsplit > 1) {
+            sp.y_half = (float *)((char *)workspace + pl.y_half);
+            kp.has_D = 0;
+            kp.has_z = 0;
+            kp.pre_gate = nullptr;
+        }
         if (int rc = record(tr, st, nullptr)) return rc;
         if (pl.nseg > 1) {
             sp.seg_state = (float *)((char *)workspace + pl.seg_state);
             sp.seg_log_decay = (float *)((char *)workspace + pl.seg_decay);
-            hipLaunchKernelGGL(ssd::k_fwd_seg<true>, dim3(units), dim3(ssd::kWsThreads), 0, st, prm, sp);
+            hipLaunchKernelGGL(ssd::k_fwd_seg<true>, dim3(units), dim3(ssd::kWsThreads), 0, st, kp, sp);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
-            const int PN = 64 * 64;
+            const int PN = (int)(s->headdim * s->dstate);
             const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
             hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, sp.seg_state,
                                sp.seg_log_decay, prm.init, sp.seg_state, prm.final_state, pl.nseg, PN);
@@ -271,23 +267,22 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         }
         if (prm.chunk_states) {
             hipLaunchKernelGGL((ssd::k_fwd_seg<false, true>), dim3(units), dim3(ssd::kWsThreads), 0, st,
-                               prm, sp);
+                               kp, sp);
             if (int rc = launch_status("k_fwd_seg_save", tr, st)) return rc;
         } else {
             hipLaunchKernelGGL((ssd::k_fwd_seg<false, false>), dim3(units), dim3(ssd::kWsThreads), 0, st,
-                               prm, sp);
+                               kp, sp);
             if (int rc = launch_status("k_fwd_seg", tr, st)) return rc;
         }
+        if (pl.nsplit > 1) {
+            const int64_t n4 = s->batch * s->seqlen * s->nheads * s->headdim / 4;
+            int64_t blocks = (n4 + ssd::kThreads - 1) / ssd::kThreads;
+            blocks = blocks < 4096 ? blocks : 4096;
+            hipLaunchKernelGGL(ssd::k_fwd_combine, dim3((unsigned)blocks), dim3(ssd::kThreads), 0, st,
+                               prm, (const float *)sp.y_half, n4);
+            if (int rc = launch_status("k_fwd_combine", tr, st)) return rc;
+        }
         return ok();
-    }
-    if (pl.chunked) {
-        const size_t bhk = (size_t)s->batch * s->nheads * prm.K;
-        prm.states = (float *)workspace;
-        prm.chunk_log_decay =
-            (float *)((char *)workspace + align256(bhk * s->headdim * s->dstate * sizeof(float)));
-        int rc = s->dstate == 64 ? launch_fwd_fast<64, 64>(prm, B, st, tr)
-                                 : launch_fwd_fast<64, 128>(prm, B, st, tr);
-        return rc ? rc : ok();
     }
     if (s->dstate > 256)
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "dstate=%lld > 256 is not supported",

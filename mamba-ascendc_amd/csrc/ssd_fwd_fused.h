@@ -9,6 +9,13 @@
 //         (+ D x_t, * silu(z_t))
 //   S  <- exp(cs_last) S + sum_t decay_t q_t x_t (x) B_t
 //
+// dstate N = 128 runs as two independent 64-column halves of the state
+// (nsplit = 2): with W_a, W_b the decayed C.B^T of each half of the columns,
+//   y = (W_a + W_b)(q x) + exp(cs) (C_a . S_a + C_b . S_b) = y_a + y_b,
+// so one workgroup per half runs the N = 64 algorithm on its columns of B, C
+// and the state, writes y_a to out and y_b to sp.y_half, and
+// k_fwd_combine adds them (and applies D and z).
+//
 // Long sequences with few (b, h) streams are cut into segments so the grid
 // still fills the GPU: a state-only pass (kStateOnly) computes each
 // segment's state contribution from zero and its total log decay, the
@@ -53,6 +60,8 @@ struct SegParams {
     float *seg_log_decay;  // [B, H, nseg]
     const float *seg_in;   // [B, H, nseg, P, N] state entering each segment, or NULL
     int write_final;       // full pass writes final_state (single segment)
+    int nsplit;            // 64-column state halves per head: 1 (N = 64) or 2 (N = 128)
+    float *y_half;         // nsplit = 2: [B, L, H, P] output of the second half
 };
 
 constexpr int kXcds = 8; // MI355X: workgroups go round-robin over 8 XCDs
@@ -92,15 +101,20 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     auto T3 = [&](int s) { return tile_at(lds, kStateOnly ? 2 * s + 1 : 3 * s + 2); };
     auto T4 = [&](int s) { return tile_at(lds, 6 + s); };
 
-    // unit = ((b * G + g) * nseg + sg) * R + r
+    // unit = (((b * G + g) * nseg + sg) * nsplit + nh) * R + r
     const int u = xcd_unit(blockIdx.x, (int)gridDim.x, prm.R);
     const int r = u % prm.R;
-    const int sg = (u / prm.R) % sp.nseg;
-    const int bg = u / (prm.R * sp.nseg);
+    const int nh = (u / prm.R) % sp.nsplit;
+    const int sg = (u / (prm.R * sp.nsplit)) % sp.nseg;
+    const int bg = u / (prm.R * sp.nsplit * sp.nseg);
     const int g = bg % prm.G, b = bg / prm.G;
     const int h = g * prm.R + r;
     const int H = prm.H, G = prm.G;
-    const int64_t rowHP = (int64_t)H * P, rowGN = (int64_t)G * N;
+    // NS: dstate (row stride of B, C and of every state); this unit's
+    // columns start at n0
+    const int NS = N * sp.nsplit, n0 = N * nh;
+    const int64_t rowHP = (int64_t)H * P, rowGN = (int64_t)G * NS;
+    const int64_t PNS = (int64_t)P * NS;
     const int kbeg = sg * sp.M, kend = min(kbeg + sp.M, prm.K);
 
     // ------------------------------------------------------------ producer
@@ -127,7 +141,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         const int tv = (int)min((int64_t)T, prm.L - t0);
         const int range = real ? 0x7fffffff : 0;
         const auto rx = buf_rsrc_n(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P, range);
-        const auto rb = buf_rsrc_n(prm.B + (((int64_t)b * prm.L + t0) * G + g) * N, range);
+        const auto rb = buf_rsrc_n(prm.B + (((int64_t)b * prm.L + t0) * G + g) * NS + n0, range);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = min(rt + 16 * j, tv - 1);
@@ -224,9 +238,9 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             const bool real = k < kend;
             const int64_t t0 = (int64_t)(real ? k : kbeg) * T;
             const int tv = (int)min((int64_t)T, prm.L - t0);
-            const auto rc = buf_rsrc_n(prm.C + (((int64_t)b * prm.L + t0) * G + g) * N,
+            const auto rc = buf_rsrc_n(prm.C + (((int64_t)b * prm.L + t0) * G + g) * NS + n0,
                                        real ? 0x7fffffff : 0);
-            const int vo = (min(own, tv - 1) * G * N + 8 * kq) * 4;
+            const int vo = (min(own, tv - 1) * G * NS + 8 * kq) * 4;
     #pragma unroll
             for (int j = 0; j < 4; ++j) cr[sl][j] = buf_load4(rc, vo + (32 * (j >> 1) + 4 * (j & 1)) * 4, 0);
         };
@@ -247,14 +261,14 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             const float *s0 = nullptr;
             if (!kStateOnly) {
                 if (sp.seg_in)
-                    s0 = sp.seg_in + (((int64_t)b * H + h) * sp.nseg + sg) * (int64_t)(P * N);
+                    s0 = sp.seg_in + (((int64_t)b * H + h) * sp.nseg + sg) * PNS + n0;
                 else if (prm.init)
-                    s0 = prm.init + ((int64_t)b * H + h) * (int64_t)(P * N);
+                    s0 = prm.init + ((int64_t)b * H + h) * PNS + n0;
             }
     #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
                 if (s0) {
-                    const float4 v = *(const float4 *)(s0 + (16 * pb + r16) * N + 16 * W + 4 * kq);
+                    const float4 v = *(const float4 *)(s0 + (16 * pb + r16) * NS + 16 * W + 4 * kq);
                     Sr[pb] = f32x4{v.x, v.y, v.z, v.w};
                 } else {
                     Sr[pb] = zero4();
@@ -282,10 +296,10 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             log_decay_sum += cs_last;
             if (kSave) {
                 // saved for the backward: the state entering chunk k
-                float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * (int64_t)(P * N);
+                float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * PNS + n0;
     #pragma unroll
                 for (int pb = 0; pb < 4; ++pb)
-                    *(float4 *)(cst + (16 * pb + r16) * N + 16 * W + 4 * kq) =
+                    *(float4 *)(cst + (16 * pb + r16) * NS + 16 * W + 4 * kq) =
                         make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
             }
             const SplitTile t2 = T2(s), t3 = T3(s);
@@ -375,7 +389,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                             v.z *= silu_f(zv.z);
                             v.w *= silu_f(zv.w);
                         }
-                        *(float4 *)(prm.out + row + p) = v;
+                        *(float4 *)((nh ? sp.y_half : prm.out) + row + p) = v;
                     }
                 }
             }
@@ -415,15 +429,15 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         float *dst = nullptr;
         if (kStateOnly) {
             const int64_t si = ((int64_t)b * H + h) * sp.nseg + sg;
-            dst = sp.seg_state + si * (int64_t)(P * N);
-            if (tid == 0) sp.seg_log_decay[si] = log_decay_sum * kLn2; // natural units
+            dst = sp.seg_state + si * PNS + n0;
+            if (tid == 0 && nh == 0) sp.seg_log_decay[si] = log_decay_sum * kLn2; // natural units
         } else if (sp.write_final && prm.final_state) {
-            dst = prm.final_state + ((int64_t)b * H + h) * (int64_t)(P * N);
+            dst = prm.final_state + ((int64_t)b * H + h) * PNS + n0;
         }
         if (dst) {
     #pragma unroll
             for (int pb = 0; pb < 4; ++pb)
-                *(float4 *)(dst + (16 * pb + r16) * N + 16 * W + 4 * kq) =
+                *(float4 *)(dst + (16 * pb + r16) * NS + 16 * W + 4 * kq) =
                     make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
         }
     };
@@ -432,6 +446,38 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     case 1: consumer(std::integral_constant<int, 1>{}); break;
     case 2: consumer(std::integral_constant<int, 2>{}); break;
     default: consumer(std::integral_constant<int, 3>{}); break;
+    }
+}
+
+// nsplit = 2 epilogue, elementwise over [B, L, H, P] in float4s: out holds
+// y_a, y_half y_b; out = (y_a + y_b + D x) (* silu z), pre_gate = y + D x.
+__global__ __launch_bounds__(kThreads) void k_fwd_combine(FwdParams prm, const float *y_half,
+                                                          int64_t n4) {
+    constexpr int P = 64;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t e = 4 * i;
+        const float4 a = *(const float4 *)(prm.out + e), c = *(const float4 *)(y_half + e);
+        float4 v = make_float4(a.x + c.x, a.y + c.y, a.z + c.z, a.w + c.w);
+        if (prm.has_D) {
+            const int p = (int)(e % P), h = (int)((e / P) % prm.H);
+            const float4 xv = *(const float4 *)(prm.x + e);
+            const float4 d = prm.d_per_channel ? *(const float4 *)(prm.D + h * P + p)
+                                               : make_float4(prm.D[h], prm.D[h], prm.D[h], prm.D[h]);
+            v.x += d.x * xv.x;
+            v.y += d.y * xv.y;
+            v.z += d.z * xv.z;
+            v.w += d.w * xv.w;
+        }
+        if (prm.pre_gate) *(float4 *)(prm.pre_gate + e) = v;
+        if (prm.has_z) {
+            const float4 zv = *(const float4 *)(prm.z + e);
+            v.x *= silu_f(zv.x);
+            v.y *= silu_f(zv.y);
+            v.z *= silu_f(zv.z);
+            v.w *= silu_f(zv.w);
+        }
+        *(float4 *)(prm.out + e) = v;
     }
 }
 
