@@ -153,38 +153,66 @@ __global__ __launch_bounds__(kThreads) void k_chunk_state(FwdParams prm) {
 // --------------------------------------------------------------------------
 // state passing (elementwise over P*N, serial over chunks)
 // --------------------------------------------------------------------------
-constexpr int kStateDepth = 8;
+constexpr int kStateDepth = 8;  // batch prefetch of k_state_pass_bwd
+constexpr int kStateRing = 16;  // chunks in flight per thread in k_state_pass
 
 __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_states,
                                                          const float *log_decay,
                                                          const float *init, float *states_start,
                                                          float *final_state, int K, int PN) {
+    constexpr int D = kStateRing;
     const int64_t bh = blockIdx.y;
     const int idx = (blockIdx.x * kThreads + threadIdx.x) * 4;
     if (idx >= PN) return;
-    const float *u = chunk_states + bh * K * (int64_t)PN + idx;
+    const float *u = chunk_states + bh * K * (int64_t)PN;
     float *so = states_start + bh * K * (int64_t)PN + idx;
     const float *ld = log_decay + bh * K;
     float4 s = init ? *(const float4 *)(init + bh * PN + idx) : make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k0 = 0; k0 < K; k0 += kStateDepth) {
-        float4 buf[kStateDepth];
-        float dec[kStateDepth];
+    // a ring of D chunks in flight: chunk k sits in slot k % D and is loaded
+    // D chunks before it is used.  The loads are unconditional: chunks past K
+    // read through a resource whose range ends at chunk K (zeros, no memory
+    // traffic), so every round issues the same loads and the wait counts
+    // stay exact.
+    auto rsrc_from = [&](int k) {
+        const int64_t left = (int64_t)(K - k) * PN * 4;
+        return buf_rsrc_n(u + (int64_t)k * PN, (int)(left < 0 ? 0 : (left > 0x7fffffff ? 0x7fffffff : left)));
+    };
+    // the log decays ride in the same ring (every lane reads the chunk's one value)
+    const auto rl = buf_rsrc_n(ld, K * 4);
+    float4 buf[D];
+    float lv[D];
+    {
+        const auto r = rsrc_from(0);
 #pragma unroll
-        for (int i = 0; i < kStateDepth; ++i) {
-            if (k0 + i < K) {
-                buf[i] = *(const float4 *)(u + (int64_t)(k0 + i) * PN);
-                dec[i] = __expf(ld[k0 + i]);
-            }
+        for (int i = 0; i < D; ++i) {
+            buf[i] = buf_load4(r, (i * PN + idx) * 4, 0);
+            lv[i] = buf_load(rl, 0, i * 4);
         }
+    }
+    int k0 = 0;
+    for (; k0 + D <= K; k0 += D) {
+        const auto r = rsrc_from(k0 + D);
 #pragma unroll
-        for (int i = 0; i < kStateDepth; ++i) {
-            if (k0 + i < K) {
-                *(float4 *)(so + (int64_t)(k0 + i) * PN) = s;
-                s.x = dec[i] * s.x + buf[i].x;
-                s.y = dec[i] * s.y + buf[i].y;
-                s.z = dec[i] * s.z + buf[i].z;
-                s.w = dec[i] * s.w + buf[i].w;
-            }
+        for (int i = 0; i < D; ++i) {
+            const float dec = __expf(lv[i]);
+            *(float4 *)(so + (int64_t)(k0 + i) * PN) = s;
+            s.x = dec * s.x + buf[i].x;
+            s.y = dec * s.y + buf[i].y;
+            s.z = dec * s.z + buf[i].z;
+            s.w = dec * s.w + buf[i].w;
+            buf[i] = buf_load4(r, (i * PN + idx) * 4, 0);
+            lv[i] = buf_load(rl, 0, (k0 + D + i) * 4);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        if (k0 + i < K) {
+            const float dec = __expf(lv[i]);
+            *(float4 *)(so + (int64_t)(k0 + i) * PN) = s;
+            s.x = dec * s.x + buf[i].x;
+            s.y = dec * s.y + buf[i].y;
+            s.z = dec * s.z + buf[i].z;
+            s.w = dec * s.w + buf[i].w;
         }
     }
     if (final_state) *(float4 *)(final_state + bh * PN + idx) = s;
