@@ -65,7 +65,8 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     // per-token (and per-channel D) values of a step, double buffered by step parity
     __shared__ __attribute__((aligned(16))) float s_q[2][T], s_cs[2][T], s_dqdu[2][T], s_dte[2][T],
         s_ecs[2][T], s_D[2][P];
-    __shared__ float s_dcs[2][T], s_rd[2][T], s_sdu[2][4], s_A[2];
+    __shared__ float s_dcs[2][T], s_rd[2][T], s_A[2];
+    __shared__ __attribute__((aligned(16))) float s_sdu[2][4];
     __shared__ __attribute__((aligned(16))) float s_da[4][T]; // epilogue: da of a step, per consumer wave
 
     auto Xt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, par); };
@@ -427,10 +428,12 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             const int64_t t0 = (int64_t)k * T;
             const int tv = tvalid(k);
             const int64_t bhk = ((int64_t)b * H + h) * K + k;
-            float v = s_dcs[par][lane];
+            // the chunk-end terms join the last token's dcs (branch-free: every
+            // lane forms them from wave-uniform values)
             const float rd_tot = wave_sum(s_rd[par][lane]);
-            const float sdu = s_sdu[par][0] + s_sdu[par][1] + s_sdu[par][2] + s_sdu[par][3];
-            if (lane == T - 1) v += rd_tot + exp2_f(s_cs[par][T - 1]) * sdu;
+            const float4 sdu4 = *(const float4 *)&s_sdu[par][0];
+            const float tail = rd_tot + exp2_f(s_cs[par][T - 1]) * (sdu4.x + sdu4.y + sdu4.z + sdu4.w);
+            const float v = s_dcs[par][lane] + (lane == T - 1 ? tail : 0.f);
             const float da = wave_suffix_scan(v);
             if (W == 0) {
                 const float dA_p = wave_sum(da * s_q[par][lane]);
@@ -444,13 +447,9 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             for (int pb = 0; pb < 4; ++pb) {
                 xa[pb] = tile_row4(tile_at(le, par), own, 16 * pb + cq);
                 ga[pb] = tile_row4(tile_at(le, 2 + par), own, 16 * pb + cq);
-                if (prm.d_per_channel) {
-                    const float4 d4 = *(const float4 *)&s_D[par][16 * pb + cq];
-                    Dv[pb] = f32x4{d4.x, d4.y, d4.z, d4.w};
-                } else {
-                    const float d1 = s_D[par][0];
-                    Dv[pb] = f32x4{d1, d1, d1, d1};
-                }
+                // s_D holds D per channel (a scalar D repeated, 0 without D)
+                const float4 d4 = *(const float4 *)&s_D[par][16 * pb + cq];
+                Dv[pb] = f32x4{d4.x, d4.y, d4.z, d4.w};
             }
             // da of token own: through this wave's LDS row (written and read
             // back by the same wave, so no barrier)
