@@ -88,6 +88,8 @@ CASES = [
     ([4, 200, 256, 64, 64, 64, 64], ("D2", "z", "bias", "init"), True, (0.0, math.inf), "both"),
     ([2, 130, 256, 64, 64, 64, 128], ("D", "bias"), True, (0.0, math.inf), "out"),
     ([1, 100, 256, 64, 64, 64, 256], ("init",), True, (0.0, math.inf), "final"),
+    ([2, 70, 256, 64, 64, 64, 128], ("z", "init"), False, (0.05, 2.0), "both"),
+    ([1, 150, 256, 64, 64, 64, 256], ("D2", "z", "bias"), True, (0.0, math.inf), "both"),
 ]
 
 
