@@ -263,16 +263,68 @@ def bench_forward(torch, lib, rt, api, hip, inp, shape, steps, warmup):
     return res, names, wall, ok, ws.numel()
 
 
-def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup):
+def full_features(torch, shape, seed):
+    """The reference benchmark's "full" feature set (mamba2_backward_bench.py:
+    159-165, 219-241): D [H, P], z, dt_bias, initial states, softplus and
+    dt_limit (1e-3, 1); seeded GPU tensors of those shapes."""
+    b, l, h, p, n, _chunk, g = shape
+    gen = torch.Generator(device="cuda").manual_seed(seed + 1)
+    kw = dict(device="cuda", dtype=torch.float32, generator=gen)
+    return {"D": torch.randn(h, p, **kw), "z": torch.randn(b, l, h, p, **kw),
+            "dt_bias": torch.randn(h, **kw) * 0.1,
+            "initial_states": torch.randn(b, h, p, n, **kw) / 5, "dt_limit": (1e-3, 1.0)}
+
+
+def feature_flags(rt, feats):
+    if not feats:
+        return rt.DT_SOFTPLUS, 0.0, math.inf
+    return (rt.DT_SOFTPLUS | rt.HAS_D | rt.D_PER_CHANNEL | rt.HAS_Z | rt.HAS_DT_BIAS
+            | rt.HAS_INITIAL), feats["dt_limit"][0], feats["dt_limit"][1]
+
+
+def bench_fwd_features(torch, lib, rt, inp, shape, feats, steps, warmup):
+    """Inference forward through the C ABI with the given feature tensors:
+    median ms of `steps` calls (HIP events on the launch stream)."""
+    x, dt, A, B, C = (inp[k] for k in ("x", "dt", "A", "B", "C"))
+    b, l, h, p, n, chunk, g = shape
+    shp = rt.Mamba2SsdShape(b, l, h, p, g, n, chunk)
+    flags, lo, hi = feature_flags(rt, feats)
+    nb = ctypes.c_size_t(0)
+    rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shp), flags, ctypes.byref(nb)), "ws", lib)
+    P = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    out = torch.empty_like(x)
+    final = torch.empty(b, h, p, n, device=x.device, dtype=torch.float32)
+    ws = torch.empty(max(1, nb.value), dtype=torch.uint8, device=x.device)
+    fargs = rt.Mamba2SsdFwdArgs(shp, flags, lo, hi, P(x), P(dt), P(A), P(B), P(C),
+                                P(feats["D"]), P(feats["z"]), P(feats["dt_bias"]),
+                                P(feats["initial_states"]), P(out), P(final), None, None)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(warmup):
+        rt.check(lib.mamba2_ssd_fwd(ctypes.byref(fargs), P(ws), ws.numel(), stream), "fwd", lib)
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(steps):
+        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        rt.check(lib.mamba2_ssd_fwd(ctypes.byref(fargs), P(ws), ws.numel(), stream), "fwd", lib)
+        e0.record()
+        e0.synchronize()
+        samples.append(s0.elapsed_time(e0))
+    return statistics.median(samples)
+
+
+def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup, feats=None):
     """Training forward (saving the chunk-start states) + M1 bwd through the C
     ABI with per-kernel events; upstream gradients of the loss mean(y^2) +
-    mean(final^2).  None if unsupported."""
+    mean(final^2).  `feats`: optional full-feature tensors (full_features).
+    None if unsupported."""
     x, dt, A, B, C = (inp[k] for k in ("x", "dt", "A", "B", "C"))
     b, l, h, p, n, chunk, g = shape
     shp = rt.Mamba2SsdShape(b, l, h, p, g, n, chunk)
     if p != 64 or n != 64:
         return None
-    flags = rt.DT_SOFTPLUS | rt.SAVED_STATES
+    flags, lo, hi = feature_flags(rt, feats)
+    flags |= rt.SAVED_STATES
     fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0)
     rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shp), flags, ctypes.byref(fb)), "ws", lib)
     rt.check(lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(shp), flags, ctypes.byref(bb)), "ws", lib)
@@ -284,12 +336,19 @@ def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup):
     grads = {k: torch.empty_like(v) for k, v in inp.items()}
     dout = torch.empty_like(x)
     dfinal = torch.empty_like(final)
-    fargs = rt.Mamba2SsdFwdArgs(shp, flags, 0.0, math.inf, P(x), P(dt), P(A), P(B), P(C),
-                                None, None, None, None, P(out), P(final), None, P(states))
-    bargs = rt.Mamba2SsdBwdArgs(shp, flags, 0.0, math.inf, P(x), P(dt), P(A), P(B), P(C),
-                                None, None, None, None, P(dout), P(dfinal), None, P(states),
+    f = feats or {"D": None, "z": None, "dt_bias": None, "initial_states": None}
+    fg = {k: (None if v is None else torch.empty_like(v)) for k, v in f.items() if k != "dt_limit"}
+    grads.update({"d" + k: v for k, v in fg.items() if v is not None})
+    pre_gate = torch.empty_like(x) if f["z"] is not None else None
+    fargs = rt.Mamba2SsdFwdArgs(shp, flags, lo, hi, P(x), P(dt), P(A), P(B), P(C),
+                                P(f["D"]), P(f["z"]), P(f["dt_bias"]), P(f["initial_states"]),
+                                P(out), P(final), P(pre_gate), P(states))
+    bargs = rt.Mamba2SsdBwdArgs(shp, flags, lo, hi, P(x), P(dt), P(A), P(B), P(C),
+                                P(f["D"]), P(f["z"]), P(f["dt_bias"]), P(f["initial_states"]),
+                                P(dout), P(dfinal), P(pre_gate), P(states),
                                 P(grads["x"]), P(grads["dt"]), P(grads["A"]), P(grads["B"]),
-                                P(grads["C"]), None, None, None, None)
+                                P(grads["C"]), P(fg["D"]), P(fg["z"]), P(fg["dt_bias"]),
+                                P(fg["initial_states"]))
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     rt.check(lib.mamba2_ssd_fwd(ctypes.byref(fargs), P(ws), ws.numel(), stream), "fwd", lib)
     torch.mul(out, 2.0 / out.numel(), out=dout)
@@ -626,6 +685,8 @@ def main(argv=None):
     ap.add_argument("--config", type=int, default=HEADLINE, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--no-bwd", action="store_true", help="skip the fwd+bwd timing")
+    ap.add_argument("--no-full", action="store_true",
+                    help="skip the full-feature (D, z, dt_bias, initial states, dt_limit) timings")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run 3 plain 1 GiB device copies (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--cpu-budget", type=float, default=20.0,
@@ -732,6 +793,26 @@ def main(argv=None):
             log(f"bwd median {bwd_ms:.4f} ms; fwd+bwd median {fwd_bwd_ms:.4f} ms")
             api_fwd_bwd_ms, _ = bench_fwd_bwd(torch, api, inp, chunk, max(5, args.steps // 3), 3)
             log(f"public API (autograd) fwd+bwd median {api_fwd_bwd_ms:.4f} ms")
+    full = None
+    if not args.no_full:
+        # the reference's headline feature set on the same shape
+        feats = full_features(torch, shape, seed)
+        nfs = max(5, args.steps // 3)
+        full = {"features": "D [H,P], z, dt_bias, initial_states, softplus, dt_limit (1e-3, 1)",
+                "fwd_ms": round(bench_fwd_features(torch, lib, rt, inp, shape, feats, nfs, 3), 5)}
+        log(f"full features: forward median {full['fwd_ms']:.4f} ms")
+        if not args.no_bwd:
+            tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, nfs, 3, feats)
+            if tr is not None:
+                fres, bres = tr[0], tr[1]
+                full["fwd_train_ms"] = round(statistics.median(r[0] for r in fres), 5)
+                full["bwd_ms"] = round(statistics.median(r[0] for r in bres), 5)
+                full["fwd_bwd_ms"] = round(statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres)), 5)
+                full["grads_finite"] = bool(tr[3])
+                log(f"full features: training forward {full['fwd_train_ms']:.4f} ms, bwd "
+                    f"{full['bwd_ms']:.4f} ms, fwd+bwd {full['fwd_bwd_ms']:.4f} ms")
+        del feats
+        torch.cuda.empty_cache()
     if args.copy_calib:
         copy_calibration(torch, 1 << 30)
         log("copy calibration: 3 x 1 GiB device copies")
@@ -794,6 +875,7 @@ def main(argv=None):
         "bwd_kernels": bwd_kern,
         "api_fwd_ms": round(api_ms, 5),
         "state_passing": state_pass,
+        "full_features": full,
         "op": {
             "flops": flops,
             "bytes": nbytes,
