@@ -265,13 +265,18 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         } else {
             sp.write_final = 1;
         }
+        const dim3 grid(units), block(ssd::kWsThreads);
         if (prm.chunk_states) {
-            hipLaunchKernelGGL((ssd::k_fwd_seg<false, true>), dim3(units), dim3(ssd::kWsThreads), 0, st,
-                               kp, sp);
+            if (kp.has_z)
+                hipLaunchKernelGGL((ssd::k_fwd_seg<false, true, true>), grid, block, 0, st, kp, sp);
+            else
+                hipLaunchKernelGGL((ssd::k_fwd_seg<false, true, false>), grid, block, 0, st, kp, sp);
             if (int rc = launch_status("k_fwd_seg_save", tr, st)) return rc;
         } else {
-            hipLaunchKernelGGL((ssd::k_fwd_seg<false, false>), dim3(units), dim3(ssd::kWsThreads), 0, st,
-                               kp, sp);
+            if (kp.has_z)
+                hipLaunchKernelGGL((ssd::k_fwd_seg<false, false, true>), grid, block, 0, st, kp, sp);
+            else
+                hipLaunchKernelGGL((ssd::k_fwd_seg<false, false, false>), grid, block, 0, st, kp, sp);
             if (int rc = launch_status("k_fwd_seg", tr, st)) return rc;
         }
         if (pl.nsplit > 1) {

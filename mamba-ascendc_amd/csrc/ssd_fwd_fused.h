@@ -30,10 +30,12 @@
 // Tiles (split fp16, LDS, all stored row-major in their first index), for
 // the chunk being processed:
 //   T1 = B [t][n]          (A operand of C.B^T, rows s)
-//   T2 = q x [t][p]        (A operand of y^T and B operand of U^T, both
-//                           contracting over t: transposed reads)
-//   T3 = decay B [t][n]    (A operand of U^T, transposed reads)
+//   T2 = x [t][p]          (A operand of y^T and B operand of U^T, both
+//                           contracting over t: transposed reads; also the
+//                           x of the D x term, so x is read from HBM once)
+//   T3 = decay q B [t][n]  (A operand of U^T, transposed reads)
 //   T4 = S [p][n]          (A operand of the C.S term)
+// with q_s folded into the W^T tiles instead of into x.
 // and, in registers, C_t for the lane's own token row t = 16 w + l % 16.
 // Outputs are produced transposed (y^T[p][t], U^T[n][p]) so that the C.B^T
 // tiles feed the next product straight from registers (see perm32; the
@@ -81,7 +83,8 @@ __device__ __forceinline__ int xcd_unit(int id, int total, int R) {
 constexpr int kWsThreads = 512; // 4 producer + 4 consumer waves
 
 // kSave: also write the state entering every chunk to prm.chunk_states.
-template <bool kStateOnly, bool kSave = false>
+// kGate: the z gate (prm.has_z), whose z rows the consumers prefetch a chunk ahead.
+template <bool kStateOnly, bool kSave = false, bool kGate = false>
 __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams sp) {
     constexpr int T = 64, P = 64, N = 64;
     // stage tiles, double buffered by chunk parity s: full pass T1(s), T2(s),
@@ -89,7 +92,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     // T2(s), T3(s) = tiles 2 s, 2 s + 1
     constexpr int kTiles = kStateOnly ? 4 : 8;
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * kTiles * kTile];
-    __shared__ float s_cs[2][T];
+    __shared__ __attribute__((aligned(16))) float s_cs[2][T], s_q[2][T];
+    __shared__ __attribute__((aligned(16))) float s_Dv[P]; // D per channel (a scalar D repeated)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const bool producer = wave >= 4;
@@ -167,15 +171,18 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         }
         const float cs = wave_inclusive_scan(a);
         const float cs_last = readlane_f(cs, T - 1);
-        if (w == 0) s_cs[s][lane] = cs;
+        if (w == 0) {
+            s_cs[s][lane] = cs;
+            s_q[s][lane] = q;
+        }
         const float dec = exp2_f(cs_last - cs);
         const SplitTile t1 = T1(s), t2 = T2(s), t3 = T3(s);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = rt + 16 * j;
-            const float qr = __shfl(q, row, kWave), dr = __shfl(dec, row, kWave);
+            const float dr = __shfl(dec * q, row, kWave);
             const float4 xv = xr[sl][j], bv = br[sl][j];
-            put(t2, row, make_float4(xv.x * qr, xv.y * qr, xv.z * qr, xv.w * qr));
+            put(t2, row, xv);
             put(t3, row, make_float4(bv.x * dr, bv.y * dr, bv.z * dr, bv.w * dr));
             if (!kStateOnly) put(t1, row, bv);
         }
@@ -246,6 +253,20 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         };
         using C0 = std::integral_constant<int, 0>;
         using C1 = std::integral_constant<int, 1>;
+        // z of row `own` for the next chunk's gate, loaded one chunk ahead (an
+        // empty-range read without z or past the segment end)
+        float4 zr[4];
+        auto z_load = [&](int k) {
+            if (!kGate) return;
+            const bool real = k < kend;
+            const int64_t t0 = (int64_t)(real ? k : kbeg) * T;
+            const int tv = (int)min((int64_t)T, prm.L - t0);
+            const auto rz = buf_rsrc_n(prm.z + (((int64_t)b * prm.L + t0) * H + h) * P,
+                                       real ? 0x7fffffff : 0);
+            const int vo = (min(own, tv - 1) * H * P + 4 * kq) * 4;
+    #pragma unroll
+            for (int pb = 0; pb < 4; ++pb) zr[pb] = buf_load4(rz, vo + 64 * pb, 0);
+        };
         auto write_T4 = [&](int s) {
             const SplitTile t4 = T4(s);
     #pragma unroll
@@ -278,6 +299,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 write_T4(0);
                 c_load(kbeg, C0{});
                 c_load(kbeg + 1, C1{});
+                z_load(kbeg);
+                if (W == 0) {
+                    const float dv = prm.has_D ? prm.D[prm.d_per_channel ? h * P + lane : h] : 0.f;
+                    s_Dv[lane] = dv;
+                }
             }
         }
         lds_barrier();
@@ -331,14 +357,14 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int so = 16 * j + 4 * kq + i;
-                            const float e = (j <= W && so <= own) ? exp2_f(cs_own - s_cs[s][so]) : 0.f;
+                            const float e = (j <= W && so <= own) ? exp2_f(cs_own - s_cs[s][so]) * s_q[s][so] : 0.f;
                             wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
                         }
                     }
                     WT[0] = pack_frag(wv[0]);
                     WT[1] = pack_frag(wv[1]);
                 }
-                // y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] (q x)_s
+                // y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] q_s x_s
                 f32x4 acc[4];
     #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) {
@@ -352,7 +378,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 for (int pb = 0; pb < 4; ++pb)
     #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[pb][i] *= ecs;
-                // each (q x) fragment feeds both y^T (W part) and U^T
+                // each x fragment feeds both y^T (W part) and U^T
     #pragma unroll
                 for (int m = 0; m < 2; ++m) {
                     const Frag a3 = frag_tp(t3, m, 16 * W);
@@ -370,20 +396,17 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         const int p = 16 * pb + 4 * kq;
                         float4 v = make_float4(acc[pb][0], acc[pb][1], acc[pb][2], acc[pb][3]);
                         if (prm.has_D) {
-                            const float4 xv = *(const float4 *)(prm.x + row + p);
-                            float4 d;
-                            if (prm.d_per_channel)
-                                d = *(const float4 *)(prm.D + h * P + p);
-                            else
-                                d = make_float4(prm.D[h], prm.D[h], prm.D[h], prm.D[h]);
+                            const f32x4 xa = tile_row4(t2, own, p); // x from the staged tile
+                            const float4 xv = make_float4(xa[0], xa[1], xa[2], xa[3]);
+                            const float4 d = *(const float4 *)&s_Dv[p];
                             v.x += d.x * xv.x;
                             v.y += d.y * xv.y;
                             v.z += d.z * xv.z;
                             v.w += d.w * xv.w;
                         }
                         if (prm.pre_gate) *(float4 *)(prm.pre_gate + row + p) = v;
-                        if (prm.has_z) {
-                            const float4 zv = *(const float4 *)(prm.z + row + p);
+                        if (kGate) {
+                            const float4 zv = zr[pb];
                             v.x *= silu_f(zv.x);
                             v.y *= silu_f(zv.y);
                             v.z *= silu_f(zv.z);
@@ -392,6 +415,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         *(float4 *)((nh ? sp.y_half : prm.out) + row + p) = v;
                     }
                 }
+                z_load(k + 1);
             }
             // S <- exp2(cs_last) S + U, U^T[n][p] = T3 x T2 (the full pass forms
             // U together with y)
