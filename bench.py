@@ -505,6 +505,43 @@ def bench_fwd_bwd(torch, api, inp, chunk, steps, warmup):
     return statistics.median(samples), None
 
 
+def autograd_memory(torch, api, inp, chunk):
+    """Saved-tensor bytes and peak memory of one autograd forward + backward
+    (the reference backward bench's saved-tensor and extra-peak figures,
+    mamba2_backward_bench.py:168-215, 420-489).  saved: bytes of the distinct
+    storages autograd keeps between the passes beyond the inputs; peak_extra:
+    the allocator's peak during forward + backward above what was allocated
+    before (inputs and upstream gradients)."""
+    leaves = {k: v.detach().clone().requires_grad_(True) for k, v in inp.items()}
+    inputs = {v.untyped_storage().data_ptr() for v in leaves.values()}
+    seen = {}
+
+    def pack(t):
+        st = t.untyped_storage()
+        if st.data_ptr() not in inputs:
+            seen[st.data_ptr()] = st.nbytes()
+        return t
+
+    with torch.no_grad():
+        out, fin = api.mamba2_ssd_fwd(leaves["x"], leaves["dt"], leaves["A"], leaves["B"],
+                                      leaves["C"], chunk, dt_softplus=True, return_final_state=True)
+        gy, gf = out * (2.0 / out.numel()), fin * (2.0 / fin.numel())
+        del out, fin
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+        out, fin = api.mamba2_ssd_fwd(leaves["x"], leaves["dt"], leaves["A"], leaves["B"],
+                                      leaves["C"], chunk, dt_softplus=True, return_final_state=True)
+    torch.autograd.backward((out, fin), (gy, gf))
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    del out, fin, gy, gf, leaves
+    torch.cuda.empty_cache()
+    return {"saved_bytes": int(sum(seen.values())), "peak_extra_bytes": int(peak)}
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def host_info():
@@ -758,6 +795,7 @@ def main(argv=None):
     log(f"public API forward median {api_ms:.4f} ms")
 
     fwd_bwd_ms, bwd_note, api_fwd_bwd_ms, bwd_kern, bwd_ms = None, "skipped (--no-bwd)", None, {}, None
+    memory = None
     fwd_train_ms = None
     if not args.no_bwd:
         tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, args.steps, args.warmup)
@@ -793,6 +831,9 @@ def main(argv=None):
             log(f"bwd median {bwd_ms:.4f} ms; fwd+bwd median {fwd_bwd_ms:.4f} ms")
             api_fwd_bwd_ms, _ = bench_fwd_bwd(torch, api, inp, chunk, max(5, args.steps // 3), 3)
             log(f"public API (autograd) fwd+bwd median {api_fwd_bwd_ms:.4f} ms")
+            memory = autograd_memory(torch, api, inp, chunk)
+            log(f"autograd memory: saved {memory['saved_bytes'] / 2**30:.3f} GiB beyond the inputs, "
+                f"peak {memory['peak_extra_bytes'] / 2**30:.3f} GiB above inputs + upstream grads")
     full = None
     if not args.no_full:
         # the reference's headline feature set on the same shape
@@ -875,6 +916,7 @@ def main(argv=None):
         "bwd_kernels": bwd_kern,
         "api_fwd_ms": round(api_ms, 5),
         "state_passing": state_pass,
+        "autograd_memory": memory,
         "full_features": full,
         "op": {
             "flops": flops,
