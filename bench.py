@@ -442,6 +442,47 @@ def bench_state_passing(torch, lib, shape, steps=10, warmup=3):
             "frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_decode(torch, shape, batch=64, steps=20, warmup=5):
+    """The decode step (selective_state_update, Mamba-2 tied form with D, z and
+    dt_bias) for `batch` sequences on this configuration's model dims (H, P, N,
+    G): median ms and GB/s of its algorithmic traffic (the state in and out,
+    plus x, z, out, B, C)."""
+    from ascend_kernel import selective_state_update
+
+    _b, _l, h, p, n, _chunk, g = shape
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    kw = dict(device="cuda", dtype=torch.float32, generator=gen)
+    state = torch.randn(batch, h, p, n, **kw)
+    x, z = torch.randn(batch, h, p, **kw), torch.randn(batch, h, p, **kw)
+    dt = torch.rand(batch, h, **kw)[..., None].expand(batch, h, p)
+    A = (-torch.rand(h, **kw))[:, None, None].expand(h, p, n)
+    B, C = torch.randn(batch, g, n, **kw), torch.randn(batch, g, n, **kw)
+    D = torch.randn(h, **kw)[:, None].expand(h, p)
+    bias = torch.randn(h, **kw)[:, None].expand(h, p)
+
+    def call():
+        return selective_state_update(state, x, dt, A, B, C, D=D, z=z, dt_bias=bias, dt_softplus=True)
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(steps):
+        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        call()
+        e0.record()
+        e0.synchronize()
+        samples.append(s0.elapsed_time(e0))
+    ms = statistics.median(samples)
+    nbytes = 4 * (2 * batch * h * p * n + 3 * batch * h * p + 2 * batch * g * n)
+    del state, x, z, B, C
+    torch.cuda.empty_cache()
+    return {"batch": batch, "shape": [batch, h, p, n, g], "ms": round(ms, 5),
+            "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "note": "per call through the Python API (includes its small host-side tensor prep)"}
+
+
 def bench_api(torch, api, inp, chunk, steps, warmup):
     """Per-call device-event time through the public Python API."""
     def call():
@@ -877,6 +918,9 @@ def main(argv=None):
         f"{d['GB_s'] / copy_gbs:.2f} of it")
     roofline["copy_GB_s"] = round(copy_gbs, 1)
     roofline["frac_of_copy"] = d["GB_s"] / copy_gbs
+    decode = bench_decode(torch, shape)
+    log(f"decode step (selective_state_update) batch {decode['batch']} on [H,P,N,G] = "
+        f"{decode['shape'][1:]}: {decode['ms']:.4f} ms, {decode['GB_s']:.0f} GB/s")
     state_pass = bench_state_passing(torch, lib, shape)
     state_pass["frac_of_copy"] = state_pass["GB_s"] / copy_gbs
     log(f"state passing op on [B,H,K,P,N] = {shape[0]},{shape[2]},{math.ceil(shape[1] / EXEC_CHUNK)},"
@@ -916,6 +960,7 @@ def main(argv=None):
         "bwd_kernels": bwd_kern,
         "api_fwd_ms": round(api_ms, 5),
         "state_passing": state_pass,
+        "decode_step": decode,
         "autograd_memory": memory,
         "full_features": full,
         "op": {

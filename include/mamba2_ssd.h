@@ -26,6 +26,9 @@
  *                          _Mamba2SsdAutogradM1.backward (mamba2.py:1782-1838)
  *   mamba2_ssd_state_passing -- torch.ops.mamba_ascend.mamba2_ssd_state_passing
  *                          (register.cpp:89-90; op_host mamba2_ssd_state_passing.cpp:12-78)
+ *   mamba2_selective_state_update -- the single-token decode step
+ *                          selective_state_update of the reference's Triton port
+ *                          (mamba_triton_ascend/mamba2/ops/triton/selective_state_update.py:134-213)
  *   *_workspace_size    -- the ACLNN GetWorkspaceSize phase
  *                          (mamba_ascendc/csrc/utils/torch_aclnn_helper.h:536-546)
  */
@@ -39,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MAMBA2_SSD_ABI_VERSION 2
+#define MAMBA2_SSD_ABI_VERSION 3
 
 /* status codes */
 #define MAMBA2_SSD_OK 0
@@ -150,6 +153,38 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
                              const float *initial_states, float *states_start,
                              float *final_state, int64_t batch, int64_t nheads,
                              int64_t nchunks, int64_t headdim, int64_t dstate, void *stream);
+
+/* ---- decode step ---------------------------------------------------------- */
+
+/* dt [B, H], A [H], dt_bias [H] (the tied head-dim case, Mamba-2 decoding);
+ * without it dt [B, H, P], A [H, P, N], dt_bias [H, P] */
+#define MAMBA2_SSU_TIED (1u << 16)
+
+typedef struct Mamba2SsuArgs {
+    int64_t batch, nheads, headdim, dstate, ngroups;
+    uint32_t flags;     /* MAMBA2_SSU_TIED, MAMBA2_SSD_DT_SOFTPLUS, _HAS_D,
+                           _D_PER_CHANNEL (D [H, P], else [H]), _HAS_Z, _HAS_DT_BIAS */
+    float *state;       /* slots of [H, P, N] (contiguous within a slot), updated in place */
+    int64_t state_slots;       /* number of slots (state batch) */
+    int64_t state_slot_stride; /* floats between consecutive slots (>= H * P * N) */
+    const int32_t *state_batch_indices; /* [B]: slot of each sequence; < 0 (or >= the
+                                           slot count) = padding: no update, output 0;
+                                           NULL = slot b */
+    const float *x;     /* [B, H, P] */
+    const float *dt;    /* [B, H] (TIED) or [B, H, P] */
+    const float *A;     /* [H] (TIED) or [H, P, N] */
+    const float *B, *C; /* [B, G, N] */
+    const float *D;     /* [H] or [H, P], or NULL */
+    const float *z;     /* [B, H, P] or NULL */
+    const float *dt_bias; /* [H] (TIED) or [H, P], or NULL */
+    float *out;         /* [B, H, P] */
+} Mamba2SsuArgs;
+
+/* One decode step: for each sequence b and head h, S = exp(A q) S + q x B^T
+ * on its state slot and out = S C (+ D x) (* silu z), q = softplus?(dt + dt_bias).
+ * dstate must be a multiple of 4 and at most 256; every pointer 16-byte aligned.
+ * No workspace; enqueued on `stream`. */
+int mamba2_selective_state_update(const Mamba2SsuArgs *args, void *stream);
 
 /* Thread-local message of the last failing call on this thread ("" if none). */
 const char *mamba2_ssd_last_error(void);

@@ -17,7 +17,7 @@ _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIBRARY_NAME = "libmamba2_ssd.so"
 LIBRARY_PATH = os.environ.get("MAMBA2_SSD_LIBRARY", os.path.join(_PKG_ROOT, LIBRARY_NAME))
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DT_SOFTPLUS = 1 << 0
 HAS_D = 1 << 1
@@ -26,6 +26,7 @@ HAS_Z = 1 << 3
 HAS_DT_BIAS = 1 << 4
 HAS_INITIAL = 1 << 5
 SAVED_STATES = 1 << 6
+SSU_TIED = 1 << 16
 
 STATUS_NAMES = {
     0: "OK",
@@ -79,6 +80,19 @@ class Mamba2SsdBwdArgs(ctypes.Structure):
     ]
 
 
+class Mamba2SsuArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int64), ("nheads", ctypes.c_int64), ("headdim", ctypes.c_int64),
+        ("dstate", ctypes.c_int64), ("ngroups", ctypes.c_int64),
+        ("flags", ctypes.c_uint32),
+        ("state", _c_fp), ("state_slots", ctypes.c_int64), ("state_slot_stride", ctypes.c_int64),
+        ("state_batch_indices", _c_fp),
+        ("x", _c_fp), ("dt", _c_fp), ("A", _c_fp), ("B", _c_fp), ("C", _c_fp),
+        ("D", _c_fp), ("z", _c_fp), ("dt_bias", _c_fp),
+        ("out", _c_fp),
+    ]
+
+
 # Every symbol include/mamba2_ssd.h declares, with its ctypes signature.
 EXPORTS = {
     "mamba2_ssd_abi_version": ([], ctypes.c_int),
@@ -113,6 +127,10 @@ EXPORTS = {
     ),
     "mamba2_ssd_state_passing": (
         [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 5 + [ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "mamba2_selective_state_update": (
+        [ctypes.POINTER(Mamba2SsuArgs), ctypes.c_void_p],
         ctypes.c_int,
     ),
 }

@@ -14,6 +14,7 @@
 #include "../../include/mamba2_ssd.h"
 #include "ssd_bwd_fused.h"
 #include "ssd_bwd_kernels.h"
+#include "ssd_decode.h"
 #include "ssd_fwd_fused.h"
 #include "ssd_fwd_kernels.h"
 
@@ -571,6 +572,81 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
                        chunk_states, chunk_log_decay, initial_states, states_start, final_state,
                        (int)nchunks_, (int)PN);
     if (int rc = launch_status("k_state_pass")) return rc;
+    return ok();
+}
+
+int mamba2_selective_state_update(const Mamba2SsuArgs *a, void *stream) {
+    if (!a) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "args is NULL");
+    constexpr uint32_t kKnown = MAMBA2_SSU_TIED | MAMBA2_SSD_DT_SOFTPLUS | MAMBA2_SSD_HAS_D |
+                                MAMBA2_SSD_D_PER_CHANNEL | MAMBA2_SSD_HAS_Z | MAMBA2_SSD_HAS_DT_BIAS;
+    const uint32_t f = a->flags;
+    if (f & ~kKnown) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "unknown flag bits 0x%x", f & ~kKnown);
+    if (a->batch <= 0 || a->nheads <= 0 || a->headdim <= 0 || a->dstate <= 0 || a->ngroups <= 0)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "non-positive dimension");
+    if (a->nheads % a->ngroups)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "nheads (%lld) must be divisible by ngroups (%lld)",
+                    (long long)a->nheads, (long long)a->ngroups);
+    if (!a->state || !a->x || !a->dt || !a->A || !a->B || !a->C || !a->out)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "state, x, dt, A, B, C and out must be non-NULL");
+    if (bool(f & MAMBA2_SSD_HAS_D) != (a->D != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "D pointer and HAS_D flag disagree");
+    if (bool(f & MAMBA2_SSD_HAS_Z) != (a->z != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "z pointer and HAS_Z flag disagree");
+    if (bool(f & MAMBA2_SSD_HAS_DT_BIAS) != (a->dt_bias != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "dt_bias pointer and HAS_DT_BIAS flag disagree");
+    if (a->dstate % 4 || a->dstate > 256)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "dstate must be a multiple of 4 and <= 256 (got %lld)",
+                    (long long)a->dstate);
+    const int64_t slot_elems = a->nheads * a->headdim * a->dstate;
+    if (a->state_slots <= 0 || a->state_slot_stride < slot_elems || a->state_slot_stride % 4)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "state needs >= 1 slot and a slot stride >= H*P*N, a multiple of 4");
+    if (!a->state_batch_indices && a->state_slots < a->batch)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "fewer state slots (%lld) than sequences (%lld)",
+                    (long long)a->state_slots, (long long)a->batch);
+    for (const void *ptr : {(const void *)a->state, (const void *)a->B, (const void *)a->C,
+                            (const void *)((f & MAMBA2_SSU_TIED) ? nullptr : a->A)})
+        if ((uintptr_t)ptr % 16)
+            return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "state, B, C (and A [H, P, N]) must be 16-byte aligned");
+    if (a->batch * a->nheads > 65535 || a->headdim > (1 << 24))
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "batch * nheads must be <= 65535");
+    ssd::SsuParams prm{};
+    prm.state = a->state;
+    prm.state_bstride = a->state_slot_stride;
+    prm.nslots = a->state_slots;
+    prm.x = a->x;
+    prm.dt = a->dt;
+    prm.A = a->A;
+    prm.B = a->B;
+    prm.C = a->C;
+    prm.D = a->D;
+    prm.z = a->z;
+    prm.dt_bias = a->dt_bias;
+    prm.slot = a->state_batch_indices;
+    prm.out = a->out;
+    prm.H = (int)a->nheads;
+    prm.P = (int)a->headdim;
+    prm.N = (int)a->dstate;
+    prm.G = (int)a->ngroups;
+    prm.R = (int)(a->nheads / a->ngroups);
+    int lpr = 1;
+    while (lpr * 4 < prm.N) lpr *= 2;
+    prm.lpr = lpr;
+    prm.tied = (f & MAMBA2_SSU_TIED) != 0;
+    prm.softplus = (f & MAMBA2_SSD_DT_SOFTPLUS) != 0;
+    prm.has_D = (f & MAMBA2_SSD_HAS_D) != 0;
+    prm.d_per_channel = (f & MAMBA2_SSD_D_PER_CHANNEL) != 0;
+    prm.has_z = (f & MAMBA2_SSD_HAS_Z) != 0;
+    // one workgroup per (b, h) walks all rows; with few (b, h) pairs the rows
+    // are split over up to 8 workgroups so the grid still has ~2k of them
+    const int rows = 256 / lpr;
+    const int64_t passes = (prm.P + rows - 1) / rows, bh = a->batch * a->nheads;
+    int64_t gx = (2048 + bh - 1) / bh;
+    gx = gx < passes ? gx : passes;
+    gx = gx < 8 ? gx : 8;
+    const dim3 grid((unsigned)gx, (unsigned)bh);
+    hipLaunchKernelGGL(ssd::k_ssu, grid, dim3(256), 0, (hipStream_t)stream, prm);
+    if (int rc = launch_status("k_ssu")) return rc;
     return ok();
 }
 

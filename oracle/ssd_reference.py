@@ -19,6 +19,11 @@ Functions and the reference lines whose behaviour they follow:
                                z gate, cast back to input dtype, fp32 final)
 * ``ssd_sequential_ref``    -- mamba_torch/ssd_reference.py:10-77 (token-by-token
                                recurrence; never forces fp32)
+* ``selective_state_update_ref`` -- mamba_triton_ascend/mamba2/ops/triton/
+                               selective_state_update.py:216-275 (one decode
+                               step: state update in place, out = S.C + D x,
+                               z gate; plus the padding slots of the kernel,
+                               58-64)
 * ``discretize``            -- mamba_torch/ssd_reference.py:237-248 and
                                mamba_ascendc/csrc/ops/mamba2_ssd_dt_bwd/design.md
                                (u = dt + bias, q = clamp(softplus(u)))
@@ -32,6 +37,10 @@ How each function is pinned (tests/test_oracle.py):
   float64 C implementation (``oracle/ssd_seq.c``); partition invariance over
   chunk sizes; closed forms (B == 0 gives y = D*x gated; A == 0 gives a prefix
   sum of outer products; L == 1 gives y = q*(B.C)*x).
+* ``selective_state_update_ref``: L decode steps from an initial state equal
+  ``ssd_sequential_ref`` on the same tokens (tied head-dim case); the untied
+  case against an element-by-element loop; padding slots leave the state
+  untouched and give zeros.
 * backward: torch autograd of the restatement is checked against the float64
   C adjoint recurrence (``ssd_seq_bwd``) and central finite differences.
 """
@@ -259,6 +268,43 @@ def ssd_sequential_ref(
     out = torch.stack(outs, dim=1)
     if return_final_state:
         return out, S
+    return out
+
+
+def selective_state_update_ref(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+                               dt_softplus=False, state_batch_indices=None):
+    """One decode step on 4-D inputs, updating ``state`` [slots, H, P, N] in place.
+
+    x, dt, z: [B, H, P]; A: [H, P, N]; B, C: [B, G, N]; D, dt_bias: [H, P];
+    state_batch_indices: [B] slot per sequence, negative = padding (state left
+    alone, output 0).  q = softplus(dt + dt_bias) (softplus with threshold 20);
+    S = exp(q A) S + q x B;  out = sum_n S C + D x, times silu(z).
+    Follows mamba_triton_ascend/mamba2/ops/triton/selective_state_update.py:216-275
+    (and the padding behaviour of its kernel, 58-64).
+    """
+    batch, h, p = x.shape
+    g = B.shape[1]
+    r = h // g
+    if dt_bias is not None:
+        dt = dt + dt_bias
+    if dt_softplus:
+        dt = torch.where(dt <= 20.0, F.softplus(dt), dt)
+    out = torch.zeros_like(x)
+    for bi in range(batch):
+        slot = bi if state_batch_indices is None else int(state_batch_indices[bi])
+        if slot < 0:
+            continue
+        q = dt[bi][..., None]                      # [H, P, 1]
+        Bh = B[bi].repeat_interleave(r, dim=0)     # [H, N]
+        Ch = C[bi].repeat_interleave(r, dim=0)
+        S = state[slot]
+        S.copy_(torch.exp(q * A) * S + q * x[bi][..., None] * Bh[:, None, :])
+        y = (S * Ch[:, None, :]).sum(-1)
+        if D is not None:
+            y = y + D * x[bi]
+        if z is not None:
+            y = y * F.silu(z[bi])
+        out[bi] = y
     return out
 
 

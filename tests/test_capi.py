@@ -27,7 +27,7 @@ HEADER = os.path.join(ROOT, "include", "mamba2_ssd.h")
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mamba2_ssd_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mamba2_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_expected_entry_points():
@@ -39,7 +39,7 @@ def test_header_declares_expected_entry_points():
 def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", rt.LIBRARY_PATH], capture_output=True,
                          text=True, check=True).stdout
-    exported = set(re.findall(r"\bT (mamba2_ssd_\w+)", out))
+    exported = set(re.findall(r"\bT (mamba2_\w+)", out))
     for name in _declared_functions():
         assert name in exported, name
     lib = rt.load_library()
@@ -157,6 +157,53 @@ def test_state_passing_rejects_bad_arguments():
     assert lib.mamba2_ssd_state_passing(None, fake, None, fake, None, 1, 1, 1, 64, 64, None) == -1
     assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 1, 1, 0, 64, 64, None) == -1
     assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 1, 1, 1, 3, 3, None) == -2
+
+
+def test_decode_step_rejects_bad_arguments():
+    """mamba2_selective_state_update validates before any GPU work."""
+    lib = rt.load_library()
+    fake = ctypes.c_void_p(0x1000)
+
+    def args(**kw):
+        a = rt.Mamba2SsuArgs(2, 4, 64, 128, 2, rt.SSU_TIED, fake, 2, 4 * 64 * 128, None,
+                             fake, fake, fake, fake, fake, None, None, None, fake)
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return a
+
+    assert lib.mamba2_selective_state_update(None, None) == -1
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(x=None)), None) == -1
+    assert "non-NULL" in rt.last_error(lib)
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(ngroups=3)), None) == -1
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(flags=rt.SSU_TIED | rt.HAS_D)), None) == -1
+    assert "HAS_D" in rt.last_error(lib)
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(flags=1 << 20)), None) == -1
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(dstate=130)), None) == -2
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(dstate=512)), None) == -2
+    # slot stride smaller than a slot, too few slots for the batch
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(state_slot_stride=100)), None) == -1
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(state_slots=1)), None) == -1
+    # misaligned state
+    assert lib.mamba2_selective_state_update(ctypes.byref(args(state=ctypes.c_void_p(0x1004))), None) == -1
+
+
+def test_decode_step_python_shape_errors():
+    """The Python entry point checks shapes (the reference's asserts) before
+    touching the GPU."""
+    from ascend_kernel import selective_state_update
+
+    b, h, p, n = 2, 4, 8, 16
+    state, x = torch.zeros(b, h, p, n), torch.zeros(b, h, p)
+    dt, A = torch.zeros(b, h, p), torch.zeros(h, p, n)
+    B = C = torch.zeros(b, 2, n)
+    with pytest.raises(ValueError, match="x must be"):
+        selective_state_update(state, torch.zeros(b, h, p + 1), dt, A, B, C)
+    with pytest.raises(ValueError, match="divisible"):
+        selective_state_update(state, x, dt, A, torch.zeros(b, 3, n), torch.zeros(b, 3, n))
+    with pytest.raises(ValueError, match="D must be"):
+        selective_state_update(state, x, dt, A, B, C, D=torch.zeros(h, p + 1))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        selective_state_update(state, x, dt, A, B, C)
 
 
 def _cpu_inputs():

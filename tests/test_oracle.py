@@ -20,6 +20,7 @@ from oracle.ssd_reference import (
     ssd_chunk_scan_ref,
     ssd_chunked_core,
     ssd_sequential_ref,
+    selective_state_update_ref,
 )
 from oracle.ssd_seq import seq_bwd, seq_fwd
 
@@ -285,3 +286,76 @@ def test_autograd_finite_reference_style():
     out.sum().backward()
     for k, v in leaves.items():
         assert v.grad is not None and torch.isfinite(v.grad).all(), k
+
+
+# ----------------------------------------------------------------------------- decode step
+
+def test_decode_steps_equal_sequential_recurrence():
+    """L tied decode steps from an initial state reproduce the token-by-token
+    recurrence (output of every token and the final state)."""
+    b, l, h, p, n, g = 2, 5, 4, 3, 8, 2
+    gen = torch.Generator().manual_seed(31)
+    x = torch.randn(b, l, h, p, generator=gen, dtype=torch.float64)
+    dt = torch.rand(b, l, h, generator=gen, dtype=torch.float64)
+    A = -torch.rand(h, generator=gen, dtype=torch.float64)
+    B = torch.randn(b, l, g, n, generator=gen, dtype=torch.float64)
+    C = torch.randn(b, l, g, n, generator=gen, dtype=torch.float64)
+    D = torch.randn(h, generator=gen, dtype=torch.float64)
+    z = torch.randn(b, l, h, p, generator=gen, dtype=torch.float64)
+    bias = torch.randn(h, generator=gen, dtype=torch.float64) * 0.1
+    S0 = torch.randn(b, h, p, n, generator=gen, dtype=torch.float64)
+    want, want_final = ssd_sequential_ref(x, dt, A, B, C, D=D, z=z, dt_bias=bias, dt_softplus=True,
+                                          initial_states=S0.clone(), return_final_state=True)
+    state = S0.clone()
+    A3 = A[:, None, None].expand(h, p, n)
+    for t in range(l):
+        out = selective_state_update_ref(state, x[:, t], dt[:, t, :, None].expand(b, h, p), A3,
+                                         B[:, t], C[:, t], D=D[:, None].expand(h, p), z=z[:, t],
+                                         dt_bias=bias[:, None].expand(h, p), dt_softplus=True)
+        torch.testing.assert_close(out, want[:, t], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(state, want_final, rtol=1e-12, atol=1e-12)
+
+
+def test_decode_untied_matches_element_loop():
+    """Per-(head, dim) dt and per-element A against a direct loop over every
+    state element."""
+    b, h, p, n, g = 2, 2, 3, 4, 1
+    gen = torch.Generator().manual_seed(32)
+    r = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64)  # noqa: E731
+    x, dt, A, B, C, D, z = r(b, h, p), r(b, h, p), -r(h, p, n).abs(), r(b, g, n), r(b, g, n), r(h, p), r(b, h, p)
+    bias = r(h, p)
+    S0 = r(b, h, p, n)
+    state = S0.clone()
+    out = selective_state_update_ref(state, x, dt, A, B, C, D=D, z=z, dt_bias=bias, dt_softplus=True)
+    for bi in range(b):
+        for hi in range(h):
+            for pi in range(p):
+                u = float(dt[bi, hi, pi] + bias[hi, pi])
+                q = u if u > 20 else math.log1p(math.exp(u))
+                acc = 0.0
+                for ni in range(n):
+                    s = math.exp(q * float(A[hi, pi, ni])) * float(S0[bi, hi, pi, ni]) + \
+                        q * float(x[bi, hi, pi]) * float(B[bi, 0, ni])
+                    assert abs(s - float(state[bi, hi, pi, ni])) < 1e-12
+                    acc += s * float(C[bi, 0, ni])
+                acc += float(D[hi, pi]) * float(x[bi, hi, pi])
+                zz = float(z[bi, hi, pi])
+                acc *= zz / (1.0 + math.exp(-zz))
+                assert abs(acc - float(out[bi, hi, pi])) < 1e-10
+
+
+def test_decode_padding_slots():
+    """A negative slot leaves the state alone and outputs zeros; the other
+    sequences update their own slots."""
+    b, h, p, n = 3, 2, 2, 4
+    gen = torch.Generator().manual_seed(33)
+    r = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64)  # noqa: E731
+    state = r(4, h, p, n)
+    before = state.clone()
+    idx = torch.tensor([2, -1, 0])
+    out = selective_state_update_ref(state, r(b, h, p), torch.rand(b, h, p, dtype=torch.float64),
+                                     -torch.rand(h, p, n, dtype=torch.float64), r(b, 1, n), r(b, 1, n),
+                                     state_batch_indices=idx)
+    assert torch.equal(out[1], torch.zeros(h, p, dtype=torch.float64))
+    assert torch.equal(state[1], before[1]) and torch.equal(state[3], before[3])
+    assert not torch.equal(state[2], before[2]) and not torch.equal(state[0], before[0])
