@@ -10,10 +10,11 @@ package loads the HIP library (no GPU work) and registers the
 
 from ._runtime import LIBRARY_PATH, load_library
 from .mamba2 import mamba2_ssd_fwd, mamba_chunk_scan_combined, register_ops
+from .modules import SsdCore
 from .selective_state_update import selective_state_update
 
 load_library()
 register_ops()
 
-__all__ = ["mamba2_ssd_fwd", "mamba_chunk_scan_combined", "selective_state_update",
+__all__ = ["mamba2_ssd_fwd", "mamba_chunk_scan_combined", "selective_state_update", "SsdCore",
            "load_library", "LIBRARY_PATH"]

@@ -206,6 +206,16 @@ def test_decode_step_python_shape_errors():
         selective_state_update(state, x, dt, A, B, C)
 
 
+def test_ssdcore_rejects_unknown_backend_and_cpu():
+    from ascend_kernel import SsdCore
+
+    with pytest.raises(ValueError):
+        SsdCore(backend="tpu")
+    x, dt, A, B, C = _cpu_inputs()
+    with pytest.raises(RuntimeError, match="ROCm"):
+        SsdCore()(x, dt, A, B, C, 64, D=None, z=None, dt_bias=None)
+
+
 def _cpu_inputs():
     g = torch.Generator().manual_seed(0)
     x = torch.randn(1, 64, 2, 64, generator=g)
