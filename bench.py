@@ -151,6 +151,13 @@ def fwd_kernel_model(name: str, shape) -> dict:
         # training forward: as k_fwd_seg plus the state entering every chunk
         per = f4 * (2 * T * p + T + 2 * T * n / r + p * n)
         fl = 2 * (T * T * n / r + T * T * p + 2 * T * n * p)
+    elif name in ("k_fwd_seg_gate", "k_fwd_seg_save_gate"):
+        # z-gated forms: as k_fwd_seg / k_fwd_seg_save plus z in, and for
+        # training the pre-gate output y + D x out (D, dt_bias and the
+        # initial states are a few values per head or stream)
+        save = name == "k_fwd_seg_save_gate"
+        per = f4 * ((4 if save else 3) * T * p + T + 2 * T * n / r + (p * n if save else 0))
+        fl = 2 * (T * T * n / r + T * T * p + 2 * T * n * p)
     elif name == "k_fwd_seg_state":
         per = f4 * (T * p + T + T * n / r)
         fl = 2 * T * p * n
@@ -168,6 +175,11 @@ def fwd_kernel_model(name: str, shape) -> dict:
         # reverse fused: as k_bwd_ws without dU in (the state gradient is
         # carried on chip), plus the dSoff product (gy exp(cs))^T C
         per = f4 * (3 * T * p + 2 * T + p * n + 4 * T * n / r)
+        fl = 2 * (2 * T * T * n / r + 2 * T * T * p + 2 * T * T * n + 4 * T * n * p)
+    elif name == "k_bwd_ws_rev_z":
+        # with the z gate: z and the pre-gate output in, dz out, besides
+        # k_bwd_ws_rev's tensors
+        per = f4 * (6 * T * p + 2 * T + p * n + 4 * T * n / r)
         fl = 2 * (2 * T * T * n / r + 2 * T * T * p + 2 * T * T * n + 4 * T * n * p)
     else:
         per, fl = float("nan"), float("nan")
@@ -643,18 +655,25 @@ def _short(name: str) -> str:
 
 
 def model_key(short: str) -> str:
-    """Kernel-model / trace name of a (templated) kernel: the C ABI traces
-    k_fwd_seg<false, true> as k_fwd_seg_save, k_fwd_seg<true, ...> as
-    k_fwd_seg_state, and drops the feature template of the others."""
+    """Kernel-model / trace name of a (templated) kernel.
+
+    k_fwd_seg<state only, save states, z gate>: <true, ...> is k_fwd_seg_state,
+    <false, true, ...> k_fwd_seg_save, <false, false, ...> k_fwd_seg, with a
+    "_gate" suffix for the z-gated form.  k_bwd_ws<has z, heads per group>:
+    a group size above 0 is the reverse fused k_bwd_ws_rev ("_z" with z).
+    The others drop their template arguments."""
     if short.startswith("k_fwd_seg<"):
         args = [a.strip() for a in short[len("k_fwd_seg<"):-1].split(",")]
         if args[0] == "true":
             return "k_fwd_seg_state"
-        return "k_fwd_seg_save" if len(args) > 1 and args[1] == "true" else "k_fwd_seg"
+        key = "k_fwd_seg_save" if len(args) > 1 and args[1] == "true" else "k_fwd_seg"
+        return key + "_gate" if len(args) > 2 and args[2] == "true" else key
     base = short.split("<")[0]
     if base == "k_bwd_ws":
         args = [a.strip() for a in short[len("k_bwd_ws<"):-1].split(",")]
-        return "k_bwd_ws_rev" if len(args) > 1 and args[1] != "0" else "k_bwd_ws"
+        if len(args) > 1 and args[1] != "0":
+            return "k_bwd_ws_rev_z" if args[0] == "true" else "k_bwd_ws_rev"
+        return "k_bwd_ws"
     return base if base == "k_bwd_dstate_rev" else short
 
 
