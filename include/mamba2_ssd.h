@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MAMBA2_SSD_ABI_VERSION 3
+#define MAMBA2_SSD_ABI_VERSION 4
 
 /* status codes */
 #define MAMBA2_SSD_OK 0
@@ -61,6 +61,15 @@ extern "C" {
 /* forward: write chunk_states; backward: read them instead of recomputing
  * (headdim == dstate == 64 only) */
 #define MAMBA2_SSD_SAVED_STATES (1u << 6)
+/* packed sequences: seq_idx [B, L] gives every token's sequence id (the
+ * seq_idx argument of the reference's Triton port,
+ * mamba_triton_ascend/mamba2/ops/triton/ssd_combined.py:359-409); forward
+ * only, headdim 64 with dstate 64 or 128 */
+#define MAMBA2_SSD_HAS_SEQ_IDX (1u << 7)
+/* forward: also write the state at the end of every sequence of a batch-1
+ * input split by cu_seqlens (ssd_combined.py:406-409, chunk_state_varlen);
+ * chunk_size must be a multiple of 64 */
+#define MAMBA2_SSD_VARLEN_STATES (1u << 8)
 
 typedef struct Mamba2SsdShape {
     int64_t batch;
@@ -90,6 +99,19 @@ typedef struct Mamba2SsdFwdArgs {
                             mamba2.py:228,322,408-418 return_states_start,
                             mamba_ascendc_ops/mamba2_ssd_chunk_mix/op_kernel/
                             mamba2_ssd_state_epilogue_train_states.cpp:15) */
+    /* members below added in ABI 4 */
+    const int32_t *seq_idx;    /* [B, L] iff HAS_SEQ_IDX, else NULL.  With e_k the id of
+                                  64-token chunk k's last token (e_{-1} = 0): C_t.B_s
+                                  counts only for equal ids, a token enters the state
+                                  only if its id is e_k >= 0, the state carries over
+                                  chunk k only if e_k == e_{k-1}, and a token reads the
+                                  state entering its chunk only if its id is e_{k-1}.
+                                  For non-negative, non-decreasing ids this is every
+                                  sequence run on its own (the one with id 0 from
+                                  initial_states) at any logical chunk size. */
+    const int32_t *cu_seqlens; /* [nseqs + 1] token offsets iff VARLEN_STATES, else NULL */
+    int64_t nseqs;
+    float *varlen_states;      /* [nseqs, H, P, N] iff VARLEN_STATES, else NULL */
 } Mamba2SsdFwdArgs;
 
 typedef struct Mamba2SsdBwdArgs {
@@ -108,7 +130,8 @@ typedef struct Mamba2SsdBwdArgs {
     float *dD, *dz, *ddt_bias, *dinitial_states; /* required iff the feature is flagged */
 } Mamba2SsdBwdArgs;
 
-/* Bytes of device workspace mamba2_ssd_fwd needs for this shape/flags. */
+/* Bytes of device workspace mamba2_ssd_fwd needs for this shape/flags
+ * (VARLEN_STATES without SAVED_STATES adds the chunk states it reads). */
 int mamba2_ssd_fwd_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes);
 
 /* Forward: out (and final_state when non-NULL). */

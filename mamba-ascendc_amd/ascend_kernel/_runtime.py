@@ -17,7 +17,7 @@ _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIBRARY_NAME = "libmamba2_ssd.so"
 LIBRARY_PATH = os.environ.get("MAMBA2_SSD_LIBRARY", os.path.join(_PKG_ROOT, LIBRARY_NAME))
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DT_SOFTPLUS = 1 << 0
 HAS_D = 1 << 1
@@ -26,6 +26,8 @@ HAS_Z = 1 << 3
 HAS_DT_BIAS = 1 << 4
 HAS_INITIAL = 1 << 5
 SAVED_STATES = 1 << 6
+HAS_SEQ_IDX = 1 << 7
+VARLEN_STATES = 1 << 8
 SSU_TIED = 1 << 16
 
 STATUS_NAMES = {
@@ -63,6 +65,10 @@ class Mamba2SsdFwdArgs(ctypes.Structure):
         ("final_state", _c_fp),
         ("pre_gate", _c_fp),
         ("chunk_states", _c_fp),
+        ("seq_idx", _c_fp),
+        ("cu_seqlens", _c_fp),
+        ("nseqs", ctypes.c_int64),
+        ("varlen_states", _c_fp),
     ]
 
 

@@ -99,6 +99,41 @@ def _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
         raise RuntimeError(f"{op}: all tensors must be on the same device")
 
 
+def _packed_shape_ok(x, B) -> bool:
+    return x.shape[-1] == 64 and B.shape[-1] in (64, 128)
+
+
+def _check_seq_idx(x, seq_idx, chunk_size, B) -> Optional[torch.Tensor]:
+    """seq_idx [B, L] of any integer dtype on x's device -> int32 contiguous."""
+    if seq_idx is None:
+        return None
+    if not isinstance(seq_idx, torch.Tensor) or seq_idx.dtype.is_floating_point or seq_idx.is_complex():
+        raise RuntimeError("mamba2_ssd_fwd: seq_idx must be an integer tensor")
+    if tuple(seq_idx.shape) != tuple(x.shape[:2]):
+        raise RuntimeError(f"mamba2_ssd_fwd: seq_idx must have shape {tuple(x.shape[:2])}")
+    if seq_idx.device != x.device:
+        raise RuntimeError("mamba2_ssd_fwd: seq_idx must be on x's device")
+    if not _packed_shape_ok(x, B):
+        raise NotImplementedError("mamba2_ssd_fwd: seq_idx needs headdim 64 with dstate 64 or 128")
+    return seq_idx.to(torch.int32).contiguous()
+
+
+def _check_cu_seqlens(x, cu_seqlens, chunk_size, B) -> torch.Tensor:
+    """cu_seqlens [nseq + 1] of any integer dtype on x's device -> int32 contiguous."""
+    if not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.dtype.is_floating_point:
+        raise RuntimeError("mamba2_ssd_fwd: cu_seqlens must be an integer tensor")
+    if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+        raise RuntimeError("mamba2_ssd_fwd: cu_seqlens must be 1-D with at least 2 entries")
+    if cu_seqlens.device != x.device:
+        raise RuntimeError("mamba2_ssd_fwd: cu_seqlens must be on x's device")
+    if x.shape[0] != 1:
+        raise RuntimeError("mamba2_ssd_fwd: varlen states need batch 1")
+    if not _packed_shape_ok(x, B) or int(chunk_size) % 64:
+        raise NotImplementedError("mamba2_ssd_fwd: varlen states need headdim 64, dstate 64 or "
+                                  "128 and a chunk_size that is a multiple of 64")
+    return cu_seqlens.to(torch.int32).contiguous()
+
+
 def _flags(D, z, dt_bias, initial_states, dt_softplus) -> int:
     f = 0
     if dt_softplus:
@@ -143,16 +178,22 @@ def _nchunks(x) -> int:
 
 def _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softplus,
              dt_limit_min, dt_limit_max, want_final=True, want_pre_gate=False,
-             want_states=False):
-    """Returns (out, final_state or None, pre_gate or None, chunk_states or None);
-    pre_gate (y + D x before the z gate) is produced only when z is given and it
-    is asked for; chunk_states [B, H, ceil(L/64), P, N] (the state entering each
-    64-token chunk, for the backward) only when asked for."""
+             want_states=False, seq_idx=None, cu_seqlens=None):
+    """Returns (out, final_state or None, pre_gate or None, chunk_states or None,
+    varlen_states or None); pre_gate (y + D x before the z gate) is produced
+    only when z is given and it is asked for; chunk_states [B, H, ceil(L/64),
+    P, N] (the state entering each 64-token chunk, for the backward) only when
+    asked for; varlen_states [nseq, H, P, N] when ``cu_seqlens`` (int32,
+    validated) is given.  ``seq_idx`` is an int32 [B, L] tensor or None."""
     lib = rt.load_library()
     shape = _shape(x, B, chunk_size)
     flags = _flags(D, z, dt_bias, initial_states, dt_softplus)
     if want_states:
         flags |= rt.SAVED_STATES
+    if seq_idx is not None:
+        flags |= rt.HAS_SEQ_IDX
+    if cu_seqlens is not None:
+        flags |= rt.VARLEN_STATES
     nbytes = ctypes.c_size_t(0)
     rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shape), flags, ctypes.byref(nbytes)),
              "mamba2_ssd_fwd_workspace_size", lib)
@@ -162,17 +203,21 @@ def _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softp
     pre_gate = torch.empty_like(x) if (want_pre_gate and z is not None) else None
     states = (torch.empty(b, h, _nchunks(x), p, B.shape[3], device=x.device, dtype=torch.float32)
               if want_states else None)
+    nseqs = 0 if cu_seqlens is None else cu_seqlens.numel() - 1
+    varlen = (torch.empty(nseqs, h, p, B.shape[3], device=x.device, dtype=torch.float32)
+              if cu_seqlens is not None else None)
     ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=x.device)
     args = rt.Mamba2SsdFwdArgs(
         shape, flags, float(dt_limit_min), _limit(dt_limit_max),
         _ptr(x), _ptr(dt), _ptr(A), _ptr(B), _ptr(C),
         _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(initial_states),
         _ptr(out), _ptr(final), _ptr(pre_gate), _ptr(states),
+        _ptr(seq_idx), _ptr(cu_seqlens), nseqs, _ptr(varlen),
     )
     with torch.cuda.device(x.device):
         rt.check(lib.mamba2_ssd_fwd(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(x.device)),
                  "mamba2_ssd_fwd", lib)
-    return out, final, pre_gate, states
+    return out, final, pre_gate, states, varlen
 
 
 def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, chunk_size,
@@ -236,8 +281,8 @@ def _op_fwd_cuda(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=No
                  dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.402823466e+38):
     _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
                   dt_limit_min, dt_limit_max)
-    out, final, _, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
-                                dt_softplus, dt_limit_min, dt_limit_max)
+    out, final, _, _, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
+                                   dt_softplus, dt_limit_min, dt_limit_max)
     return out, final
 
 
@@ -375,7 +420,7 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
         # as the reference's Train forward does (mamba2.py:1682-1770)
         # and so are the chunk-start states (the reference's training forward
         # returns states_start for its backward, mamba2.py:228,322,408-418)
-        out, final_state, pre_gate, states = _fwd_raw(
+        out, final_state, pre_gate, states, _ = _fwd_raw(
             x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
             float(dt_limit_min), float(dt_limit_max), want_final=True,
             want_pre_gate=z is not None, want_states=True)
@@ -429,7 +474,12 @@ def mamba2_ssd_fwd(
     dt_limit: Tuple[float, float] = (0.0, float("inf")),
     initial_states: Optional[torch.Tensor] = None,
     return_final_state: bool = False,
-) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    *,
+    seq_idx: Optional[torch.Tensor] = None,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    return_varlen_states: bool = False,
+    return_final_states: Optional[bool] = None,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, ...]]:
     """Mamba-2 SSD forward (chunked selective scan) on MI355X.
 
     Shapes: x [B,L,H,P], dt [B,L,H], A [H], B/C [B,L,G,N], D [H] or [H,P],
@@ -437,10 +487,28 @@ def mamba2_ssd_fwd(
     ROCm tensors.  Returns ``out`` [B,L,H,P], plus ``final_state`` [B,H,P,N]
     when ``return_final_state``.  When any input requires grad the call goes
     through the M1 autograd function.
+
+    Keyword-only, from the reference's Triton port
+    (mamba_triton_ascend/mamba2/ops/triton/ssd_combined.py:612-659):
+    ``seq_idx`` [B,L] integer sequence id per token (packed sequences);
+    ``cu_seqlens`` [nseq + 1] with ``return_varlen_states`` (batch 1) appends
+    the state at the end of every sequence [nseq,H,P,N], giving ``(out,
+    varlen_states)`` or ``(out, final_state, varlen_states)``;
+    ``return_final_states`` is that port's name for ``return_final_state``.
+    Both need headdim 64 with dstate 64 or 128; varlen states also a
+    chunk_size that is a multiple of 64.
     """
     register_ops()
+    if return_final_states is not None:
+        return_final_state = bool(return_final_states)
     lo, hi = float(dt_limit[0]), float(dt_limit[1])
+    if return_varlen_states and cu_seqlens is None:
+        raise ValueError("mamba2_ssd_fwd: return_varlen_states needs cu_seqlens")
+    seq32 = _check_seq_idx(x, seq_idx, chunk_size, B)
+    cu32 = _check_cu_seqlens(x, cu_seqlens, chunk_size, B) if return_varlen_states else None
     if _requires_grad(x, dt, A, B, C, D, z, dt_bias, initial_states):
+        if seq32 is not None or cu32 is not None:
+            raise NotImplementedError("mamba2_ssd_fwd: seq_idx and varlen states are forward-only")
         if not _can_use_native_bwd_m1(x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states):
             raise NotImplementedError(
                 "mamba2_ssd_fwd backward requires contiguous FP32 GPU tensors with "
@@ -451,8 +519,11 @@ def mamba2_ssd_fwd(
     else:
         _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
                       initial_states, lo, hi)
-        out, final_state, _, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
-                                    dt_softplus, lo, hi, want_final=return_final_state)
+        out, final_state, _, _, varlen = _fwd_raw(
+            x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softplus, lo, hi,
+            want_final=return_final_state, seq_idx=seq32, cu_seqlens=cu32)
+        if cu32 is not None:
+            return (out, final_state, varlen) if return_final_state else (out, varlen)
     if return_final_state:
         return out, final_state
     return out

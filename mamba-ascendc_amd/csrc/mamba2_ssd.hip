@@ -17,6 +17,7 @@
 #include "ssd_decode.h"
 #include "ssd_fwd_fused.h"
 #include "ssd_fwd_kernels.h"
+#include "ssd_varlen.h"
 
 namespace {
 
@@ -40,7 +41,8 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 constexpr uint32_t kKnownFlags = MAMBA2_SSD_DT_SOFTPLUS | MAMBA2_SSD_HAS_D |
                                  MAMBA2_SSD_D_PER_CHANNEL | MAMBA2_SSD_HAS_Z |
                                  MAMBA2_SSD_HAS_DT_BIAS | MAMBA2_SSD_HAS_INITIAL |
-                                 MAMBA2_SSD_SAVED_STATES;
+                                 MAMBA2_SSD_SAVED_STATES | MAMBA2_SSD_HAS_SEQ_IDX |
+                                 MAMBA2_SSD_VARLEN_STATES;
 
 int check_shape(const Mamba2SsdShape *s, uint32_t flags) {
     if (!s) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "shape is NULL");
@@ -78,15 +80,20 @@ struct FwdPlan {
     int nseg = 1, M = 1, nsplit = 1;
     size_t seg_state = 0, seg_decay = 0; // workspace offsets (fused, nseg > 1)
     size_t y_half = 0;                   // workspace offset (fused, nsplit = 2)
+    size_t states = 0;                   // chunk states for VARLEN_STATES without SAVED_STATES
     size_t ws = 0;
 };
 
-FwdPlan fwd_plan(const Mamba2SsdShape *s) {
+bool fused_shape(const Mamba2SsdShape *s) {
+    return s->headdim == 64 && (s->dstate == 64 || s->dstate == 128);
+}
+
+FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags) {
     FwdPlan pl;
     if (s->seqlen == 0) return pl;
     const int64_t K = nchunks(s), streams = s->batch * s->nheads;
     const size_t pn = (size_t)s->headdim * s->dstate;
-    if (s->headdim == 64 && (s->dstate == 64 || s->dstate == 128)) {
+    if (fused_shape(s)) {
         pl.fused = true;
         pl.nsplit = (int)(s->dstate / 64);
         const int64_t wstreams = streams * pl.nsplit;
@@ -107,12 +114,35 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s) {
             pl.y_half = off;
             off += align256((size_t)s->batch * s->seqlen * s->nheads * s->headdim * sizeof(float));
         }
+        if ((flags & MAMBA2_SSD_VARLEN_STATES) && !(flags & MAMBA2_SSD_SAVED_STATES)) {
+            pl.states = off;
+            off += align256((size_t)streams * K * pn * sizeof(float));
+        }
         pl.ws = off;
     }
     return pl;
 }
 
-size_t fwd_ws_bytes(const Mamba2SsdShape *s) { return fwd_plan(s).ws; }
+size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags) { return fwd_plan(s, flags).ws; }
+
+// k_fwd_seg full pass for the runtime feature set (save states, z gate, packed sequences)
+template <bool kSave, bool kGate, bool kSeq>
+void launch_seg(dim3 grid, hipStream_t st, const ssd::FwdParams &kp, const ssd::SegParams &sp) {
+    hipLaunchKernelGGL((ssd::k_fwd_seg<false, kSave, kGate, kSeq>), grid, dim3(ssd::kWsThreads), 0,
+                       st, kp, sp);
+}
+
+using SegLaunch = void (*)(dim3, hipStream_t, const ssd::FwdParams &, const ssd::SegParams &);
+
+SegLaunch seg_launcher(bool save, bool gate, bool seq) {
+    static const SegLaunch table[8] = {
+        launch_seg<false, false, false>, launch_seg<false, false, true>,
+        launch_seg<false, true, false>,  launch_seg<false, true, true>,
+        launch_seg<true, false, false>,  launch_seg<true, false, true>,
+        launch_seg<true, true, false>,   launch_seg<true, true, true>,
+    };
+    return table[(save ? 4 : 0) + (gate ? 2 : 0) + (seq ? 1 : 0)];
+}
 
 // Optional per-kernel event trace: events[0] is recorded before the first
 // kernel and events[i + 1] right after kernel i, all on the launch stream.
@@ -154,7 +184,7 @@ const char *mamba2_ssd_last_error(void) { return g_err; }
 int mamba2_ssd_fwd_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes) {
     if (int rc = check_shape(shape, flags)) return rc;
     if (!bytes) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "bytes is NULL");
-    *bytes = fwd_ws_bytes(shape);
+    *bytes = fwd_ws_bytes(shape, flags);
     return ok();
 }
 
@@ -184,11 +214,34 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     if (bool(f & MAMBA2_SSD_SAVED_STATES) != (a->chunk_states != nullptr))
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
                     "chunk_states pointer and SAVED_STATES flag disagree");
-    if ((f & MAMBA2_SSD_SAVED_STATES) && !(s->headdim == 64 && s->dstate == 64))
+    if ((f & (MAMBA2_SSD_SAVED_STATES | MAMBA2_SSD_HAS_SEQ_IDX | MAMBA2_SSD_VARLEN_STATES)) &&
+        !fused_shape(s))
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
-                    "SAVED_STATES needs headdim == dstate == 64 (got %lld, %lld)",
+                    "SAVED_STATES, HAS_SEQ_IDX and VARLEN_STATES need headdim 64 with dstate 64 "
+                    "or 128 (got %lld, %lld)",
                     (long long)s->headdim, (long long)s->dstate);
-    const size_t need = fwd_ws_bytes(s);
+    if (bool(f & MAMBA2_SSD_HAS_SEQ_IDX) != (a->seq_idx != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "seq_idx pointer and HAS_SEQ_IDX flag disagree");
+    const bool varlen = (f & MAMBA2_SSD_VARLEN_STATES) != 0;
+    if (varlen != (a->cu_seqlens != nullptr) || varlen != (a->varlen_states != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "cu_seqlens / varlen_states pointers and VARLEN_STATES flag disagree");
+    if (varlen) {
+        if (s->batch != 1)
+            return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                        "VARLEN_STATES needs batch 1 (got %lld)", (long long)s->batch);
+        if (a->nseqs <= 0 || a->nseqs > 65535)
+            return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "nseqs must be in [1, 65535], got %lld",
+                        (long long)a->nseqs);
+        if (s->chunk_size % ssd::kChunk)
+            return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
+                        "VARLEN_STATES needs chunk_size a multiple of 64 (got %lld)",
+                        (long long)s->chunk_size);
+        if (s->seqlen > 0x7fffffff || s->chunk_size > 0x40000000)
+            return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
+                        "VARLEN_STATES needs seqlen < 2^31 and chunk_size <= 2^30");
+    }
+    const size_t need = fwd_ws_bytes(s, f);
     if (need && (!workspace || workspace_bytes < need))
         return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need,
                     workspace ? workspace_bytes : (size_t)0);
@@ -208,6 +261,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     prm.final_state = a->final_state;
     prm.pre_gate = (f & MAMBA2_SSD_HAS_Z) ? a->pre_gate : nullptr;
     prm.chunk_states = a->chunk_states;
+    prm.seq_idx = a->seq_idx;
     prm.L = s->seqlen;
     prm.H = (int)s->nheads;
     prm.G = (int)s->ngroups;
@@ -232,9 +286,20 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
             if (e != hipSuccess)
                 return fail(MAMBA2_SSD_ERR_LAUNCH, "final-state copy failed: %s", hipGetErrorString(e));
         }
+        if (varlen) {
+            // every sequence is empty: zero states
+            hipError_t e = hipMemsetAsync(a->varlen_states, 0,
+                                          (size_t)a->nseqs * s->nheads * s->headdim * s->dstate *
+                                              sizeof(float),
+                                          st);
+            if (e != hipSuccess)
+                return fail(MAMBA2_SSD_ERR_LAUNCH, "varlen-state clear failed: %s", hipGetErrorString(e));
+        }
         return ok();
     }
-    const FwdPlan pl = fwd_plan(s);
+    const FwdPlan pl = fwd_plan(s, f);
+    if (varlen && !prm.chunk_states) prm.chunk_states = (float *)((char *)workspace + pl.states);
+    const bool seq = prm.seq_idx != nullptr;
     if (pl.fused) {
         ssd::SegParams sp{};
         sp.nseg = pl.nseg;
@@ -254,7 +319,11 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         if (pl.nseg > 1) {
             sp.seg_state = (float *)((char *)workspace + pl.seg_state);
             sp.seg_log_decay = (float *)((char *)workspace + pl.seg_decay);
-            hipLaunchKernelGGL(ssd::k_fwd_seg<true>, dim3(units), dim3(ssd::kWsThreads), 0, st, kp, sp);
+            if (seq)
+                hipLaunchKernelGGL((ssd::k_fwd_seg<true, false, false, true>), dim3(units),
+                                   dim3(ssd::kWsThreads), 0, st, kp, sp);
+            else
+                hipLaunchKernelGGL(ssd::k_fwd_seg<true>, dim3(units), dim3(ssd::kWsThreads), 0, st, kp, sp);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
             const int PN = (int)(s->headdim * s->dstate);
             const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
@@ -266,20 +335,9 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         } else {
             sp.write_final = 1;
         }
-        const dim3 grid(units), block(ssd::kWsThreads);
-        if (prm.chunk_states) {
-            if (kp.has_z)
-                hipLaunchKernelGGL((ssd::k_fwd_seg<false, true, true>), grid, block, 0, st, kp, sp);
-            else
-                hipLaunchKernelGGL((ssd::k_fwd_seg<false, true, false>), grid, block, 0, st, kp, sp);
-            if (int rc = launch_status("k_fwd_seg_save", tr, st)) return rc;
-        } else {
-            if (kp.has_z)
-                hipLaunchKernelGGL((ssd::k_fwd_seg<false, false, true>), grid, block, 0, st, kp, sp);
-            else
-                hipLaunchKernelGGL((ssd::k_fwd_seg<false, false, false>), grid, block, 0, st, kp, sp);
-            if (int rc = launch_status("k_fwd_seg", tr, st)) return rc;
-        }
+        kp.chunk_states = prm.chunk_states;
+        seg_launcher(kp.chunk_states != nullptr, kp.has_z != 0, seq)(dim3(units), st, kp, sp);
+        if (int rc = launch_status(kp.chunk_states ? "k_fwd_seg_save" : "k_fwd_seg", tr, st)) return rc;
         if (pl.nsplit > 1) {
             const int64_t n4 = s->batch * s->seqlen * s->nheads * s->headdim / 4;
             int64_t blocks = (n4 + ssd::kThreads - 1) / ssd::kThreads;
@@ -287,6 +345,13 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
             hipLaunchKernelGGL(ssd::k_fwd_combine, dim3((unsigned)blocks), dim3(ssd::kThreads), 0, st,
                                prm, (const float *)sp.y_half, n4);
             if (int rc = launch_status("k_fwd_combine", tr, st)) return rc;
+        }
+        if (varlen) {
+            hipLaunchKernelGGL(ssd::k_varlen_states, dim3((unsigned)a->nseqs, prm.H),
+                               dim3(ssd::kVarlenThreads), 0, st, prm, a->cu_seqlens,
+                               (const float *)prm.chunk_states, a->varlen_states,
+                               (int)s->chunk_size, (int)s->headdim, (int)s->dstate);
+            if (int rc = launch_status("k_varlen_states", tr, st)) return rc;
         }
         return ok();
     }

@@ -27,6 +27,17 @@
 // Exponentials are taken in the log2 domain: the chunk cumsum is formed over
 // A q log2(e), so every decay factor is a single exp2 of a difference.
 //
+// Packed sequences (kSeq, per-token ids seq_idx): with e_k the id of chunk
+// k's last token and e_{-1} = 0, C_t . B_s counts only for equal ids, token s
+// enters the state only if its id is e_k >= 0, the state carries over chunk k
+// only if e_k == e_{k-1}, and token t reads the state entering its chunk only
+// if its id is e_{k-1} (the masks of the reference's Triton port:
+// mamba_triton_ascend/mamba2/ops/triton/ssd_bmm.py:159-161,
+// ssd_chunk_state.py:208-231, ssd_state_passing.py:62-72,
+// ssd_chunk_scan.py:375-376).  The producers turn the ids into the three
+// per-token / per-chunk factors; a segment whose state is cut reports a log
+// decay of -inf, so the segment recurrence drops the state before it.
+//
 // Tiles (split fp16, LDS, all stored row-major in their first index), for
 // the chunk being processed:
 //   T1 = B [t][n]          (A operand of C.B^T, rows s)
@@ -84,9 +95,11 @@ constexpr int kWsThreads = 512; // 4 producer + 4 consumer waves
 
 // kSave: also write the state entering every chunk to prm.chunk_states.
 // kGate: the z gate (prm.has_z), whose z rows the consumers prefetch a chunk ahead.
-template <bool kStateOnly, bool kSave = false, bool kGate = false>
+// kSeq: packed sequences (prm.seq_idx).
+template <bool kStateOnly, bool kSave = false, bool kGate = false, bool kSeq = false>
 __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams sp) {
     constexpr int T = 64, P = 64, N = 64;
+    constexpr int TS = kSeq ? T : 1; // per-token sequence arrays (kSeq only)
     // stage tiles, double buffered by chunk parity s: full pass T1(s), T2(s),
     // T3(s) = tiles 3 s .. 3 s + 2 and T4(s) = tile 6 + s; state-only pass
     // T2(s), T3(s) = tiles 2 s, 2 s + 1
@@ -94,6 +107,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * kTiles * kTile];
     __shared__ __attribute__((aligned(16))) float s_cs[2][T], s_q[2][T];
     __shared__ __attribute__((aligned(16))) float s_Dv[P]; // D per channel (a scalar D repeated)
+    // kSeq, by chunk parity: token ids, 1 where the token reads the entering
+    // state, 1 where the state carries over the chunk
+    __shared__ __attribute__((aligned(16))) int s_sid[2][TS];
+    __shared__ __attribute__((aligned(16))) float s_off[2][TS];
+    __shared__ float s_carry[2];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const bool producer = wave >= 4;
@@ -131,6 +149,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     const int rt = pt >> 4, c4 = (pt & 15) * 4;
     float4 xr[kDepth][4], br[kDepth][4];
     float dtr[kDepth];
+    int sidr[kDepth], sprv[kDepth]; // kSeq: id of token `lane`, id of the token before the chunk
     const int rowHP4 = (int)(rowHP * 4), rowGN4 = (int)(rowGN * 4); // token strides, bytes
     const float Ah2 = prm.A[h] * kLog2e;                                 // A in log2 units
     const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
@@ -153,6 +172,12 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             br[sl][j] = buf_load4(rb, row * rowGN4 + c4 * 4, 0);
         }
         dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * H + h];
+        if (kSeq) {
+            const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + t0;
+            sidr[sl] = si[min(lane, tv - 1)];
+            const int pv = si[t0 > 0 ? -1 : 0]; // read unconditionally, 0 before the first chunk
+            sprv[sl] = t0 > 0 ? pv : 0;
+        }
     };
     auto put = [&](SplitTile d, int row, float4 v) {
         half4 vh, vl;
@@ -175,7 +200,17 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             s_cs[s][lane] = cs;
             s_q[s][lane] = q;
         }
-        const float dec = exp2_f(cs_last - cs);
+        float dec = exp2_f(cs_last - cs);
+        if (kSeq) {
+            // rows past the sequence end repeat its last token's id
+            const int sid = sidr[sl], e_end = __shfl(sid, T - 1, kWave), e_prev = sprv[sl];
+            if (sid != e_end || e_end < 0) dec = 0.f; // not part of the state leaving the chunk
+            if (w == 0) {
+                s_sid[s][lane] = sid;
+                s_off[s][lane] = sid == e_prev ? 1.f : 0.f;
+                if (lane == 0) s_carry[s] = e_end == e_prev ? 1.f : 0.f;
+            }
+        }
         const SplitTile t1 = T1(s), t2 = T2(s), t3 = T3(s);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -309,6 +344,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         lds_barrier();
 
         float log_decay_sum = 0.f;
+        float seg_carry = 1.f; // kSeq: 0 once the state is cut inside the segment
         // full chunks store unconditionally (a fixed number of stores per
         // chunk keeps the C-row prefetch wait exact); only the last chunk of
         // the sequence can be partial
@@ -343,6 +379,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 c_load(k + 2, slot_c);
                 const SplitTile t1 = T1(s), t4 = T4(s);
                 const float cs_own = s_cs[s][own];
+                const int sid_own = kSeq ? s_sid[s][own] : 0;
                 // W^T tiles: C_t . B_s exp2(cs_t - cs_s), s <= t, t = own
                 Frag WT[2];
                 {
@@ -357,7 +394,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int so = 16 * j + 4 * kq + i;
-                            const float e = (j <= W && so <= own) ? exp2_f(cs_own - s_cs[s][so]) * s_q[s][so] : 0.f;
+                            const bool live = j <= W && so <= own && (!kSeq || s_sid[s][so] == sid_own);
+                            const float e = live ? exp2_f(cs_own - s_cs[s][so]) * s_q[s][so] : 0.f;
                             wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
                         }
                     }
@@ -373,7 +411,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     for (int ks = 0; ks < 2; ++ks)
                         acc[pb] = mma3f(frag(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
                 }
-                const float ecs = exp2_f(cs_own);
+                const float ecs = kSeq ? exp2_f(cs_own) * s_off[s][own] : exp2_f(cs_own);
     #pragma unroll
                 for (int pb = 0; pb < 4; ++pb)
     #pragma unroll
@@ -428,7 +466,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag_tp(t2, m, 16 * pb), U[pb]);
                     }
                 }
-                const float alpha = exp2_f(cs_last);
+                const float alpha = kSeq ? exp2_f(cs_last) * s_carry[s] : exp2_f(cs_last);
+                if (kSeq) seg_carry *= s_carry[s];
     #pragma unroll
                 for (int pb = 0; pb < 4; ++pb)
     #pragma unroll
@@ -454,7 +493,9 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         if (kStateOnly) {
             const int64_t si = ((int64_t)b * H + h) * sp.nseg + sg;
             dst = sp.seg_state + si * PNS + n0;
-            if (tid == 0 && nh == 0) sp.seg_log_decay[si] = log_decay_sum * kLn2; // natural units
+            // natural units; -inf (a factor of 0) where the state was cut
+            if (tid == 0 && nh == 0)
+                sp.seg_log_decay[si] = seg_carry > 0.f ? log_decay_sum * kLn2 : -INFINITY;
         } else if (sp.write_final && prm.final_state) {
             dst = prm.final_state + ((int64_t)b * H + h) * PNS + n0;
         }

@@ -30,6 +30,7 @@ struct FwdParams {
     float *states;          // [B, H, K, P, N]: chunk states, then states at chunk starts
     float *chunk_log_decay; // [B, H, K]
     float *chunk_states;    // [B, H, K, P, N] state entering each chunk (fused forward), or NULL
+    const int32_t *seq_idx; // [B, L] sequence id of every token (packed sequences), or NULL
     int64_t L;
     int H, G, R, K;         // heads, groups, heads per group, chunks
     int softplus, has_D, d_per_channel, has_z;

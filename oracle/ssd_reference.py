@@ -24,6 +24,14 @@ Functions and the reference lines whose behaviour they follow:
                                step: state update in place, out = S.C + D x,
                                z gate; plus the padding slots of the kernel,
                                58-64)
+* ``seq_idx`` (packed sequences, in ``ssd_chunked_core``/``ssd_chunk_scan_ref``)
+                            -- the masks of the reference's Triton port:
+                               mamba_triton_ascend/mamba2/ops/triton/ssd_bmm.py:159-161,
+                               ssd_chunk_state.py:208-231, ssd_state_passing.py:62-72,
+                               ssd_chunk_scan.py:85-93,375-376
+* ``chunk_state_varlen_ref`` -- the same port's chunk_state_varlen
+                               (ssd_chunk_state.py:700-775): the state at the end
+                               of each sequence of a packed batch-1 input
 * ``discretize``            -- mamba_torch/ssd_reference.py:237-248 and
                                mamba_ascendc/csrc/ops/mamba2_ssd_dt_bwd/design.md
                                (u = dt + bias, q = clamp(softplus(u)))
@@ -37,6 +45,14 @@ How each function is pinned (tests/test_oracle.py):
   float64 C implementation (``oracle/ssd_seq.c``); partition invariance over
   chunk sizes; closed forms (B == 0 gives y = D*x gated; A == 0 gives a prefix
   sum of outer products; L == 1 gives y = q*(B.C)*x).
+* ``seq_idx``: all-equal ids reproduce the unmasked path; non-decreasing ids
+  give, token for token, each sequence run alone through the sequential
+  recurrence (the first one from the initial state), at several chunk sizes;
+  ids interleaved inside one chunk give, for the tokens of each id, the
+  sequential recurrence over the chunk with the other ids' x zeroed; all
+  negative ids drop the initial state and give chunk-wise independent runs.
+* ``chunk_state_varlen_ref``: each sequence's state equals the final state of
+  that sequence run alone, at several chunk sizes.
 * ``selective_state_update_ref``: L decode steps from an initial state equal
   ``ssd_sequential_ref`` on the same tokens (tied head-dim case); the untied
   case against an element-by-element loop; padding slots leave the state
@@ -58,6 +74,8 @@ __all__ = [
     "ssd_chunked_core",
     "ssd_chunk_scan_ref",
     "ssd_sequential_ref",
+    "chunk_state_varlen_ref",
+    "selective_state_update_ref",
     "make_inputs",
 ]
 
@@ -94,7 +112,8 @@ def discretize(dt, dt_bias, dt_softplus, dt_limit):
     return q.clamp(min=dt_limit[0], max=dt_limit[1])
 
 
-def ssd_chunked_core(xdt, dA, Bh, Ch, chunk_size, initial_states=None):
+def ssd_chunked_core(xdt, dA, Bh, Ch, chunk_size, initial_states=None, seq_idx=None,
+                     return_states=False):
     """Chunked SSD on per-head, already discretised inputs.
 
     Args:
@@ -102,11 +121,19 @@ def ssd_chunked_core(xdt, dA, Bh, Ch, chunk_size, initial_states=None):
         dA:  [b, l, h]      A * q
         Bh, Ch: [b, l, h, n] (already broadcast from groups to heads)
         initial_states: [b, h, p, n] or None
+        seq_idx: [b, l] integer sequence id of every token, or None
     Returns:
-        y [b, l, h, p] and final state [b, h, p, n].
+        y [b, l, h, p] and final state [b, h, p, n] (and, with
+        ``return_states``, the state entering every chunk [b, k, h, p, n]).
 
     Restates mamba_torch/ssd_reference.py:113-189.  ``l`` must be a multiple of
-    ``chunk_size``.
+    ``chunk_size``.  With ``seq_idx`` the masks of the reference's Triton port
+    apply, per chunk k with e_k the id of its last token and e_{-1} = 0:
+    C_t.B_s only for equal ids (ssd_bmm.py:159-161), a token enters the chunk
+    state only if its id is e_k and e_k >= 0 (ssd_chunk_state.py:208,224-231),
+    the state carries over chunk k only if e_k == e_{k-1}
+    (ssd_state_passing.py:62-72), and token t reads the state entering its
+    chunk only if its id is e_{k-1} (ssd_chunk_scan.py:375-376 with 85-93).
     """
     b, l, h, p = xdt.shape
     n = Bh.shape[-1]
@@ -118,6 +145,10 @@ def ssd_chunked_core(xdt, dA, Bh, Ch, chunk_size, initial_states=None):
     Cc = Ch.reshape(b, k, T, h, n)
     a = dA.reshape(b, k, T, h).permute(0, 3, 1, 2)  # [b, h, k, T]
     cs = a.cumsum(dim=-1)
+
+    if seq_idx is not None:
+        return _chunked_core_seq(xc, a, cs, Bc, Cc, initial_states, seq_idx.reshape(b, k, T),
+                                 return_states)
 
     # (1) intra-chunk: y_diag[t] = sum_{s<=t} (C_t . B_s) exp(cs_t - cs_s) xdt_s
     decay = torch.exp(segsum(a))  # [b, h, k, T, T]
@@ -143,7 +174,46 @@ def ssd_chunked_core(xdt, dA, Bh, Ch, chunk_size, initial_states=None):
     # (4) contribution of the state entering each chunk: exp(cs_t) C_t . S_start
     y_off = torch.einsum("bkthn,bkhpn,bhkt->bkthp", Cc, S_start, torch.exp(cs))
     y = (y_diag + y_off).reshape(b, l, h, p)
+    if return_states:
+        return y, final, S_start
     return y, final
+
+
+def _chunked_core_seq(xc, a, cs, Bc, Cc, initial_states, sid, return_states):
+    """``ssd_chunked_core`` with per-token sequence ids ``sid`` [b, k, T]."""
+    b, k, T, h, p = xc.shape
+    n = Bc.shape[-1]
+    end = sid[:, :, -1]                                   # e_k
+    prev = F.pad(end, (1, 0), value=0)[:, :-1]            # e_{k-1}, 0 before the first chunk
+    same = (sid.unsqueeze(-1) == sid.unsqueeze(-2))       # [b, k, t, s]
+    into_state = (sid == end.unsqueeze(-1)) & (end.unsqueeze(-1) >= 0)
+    reads_state = sid == prev.unsqueeze(-1)
+    carry = end == prev                                   # [b, k]
+    dt_ = xc.dtype
+
+    decay = torch.exp(segsum(a)).permute(0, 2, 1, 3, 4)   # [b, k, h, T, T]
+    cb = torch.einsum("bkthn,bkshn->bkhts", Cc, Bc)
+    w = cb * decay * same.unsqueeze(2).to(dt_)
+    y_diag = torch.einsum("bkhts,bkshp->bkthp", w, xc)
+
+    to_end = torch.exp(cs[..., -1:] - cs) * into_state.unsqueeze(1).to(dt_)  # [b, h, k, T]
+    U = torch.einsum("bkthn,bhkt,bkthp->bkhpn", Bc, to_end, xc)
+
+    S = (torch.zeros(b, h, p, n, dtype=dt_, device=xc.device) if initial_states is None
+         else initial_states)
+    starts = []
+    for kk in range(k):
+        starts.append(S)
+        alpha = torch.exp(cs[:, :, kk, -1]) * carry[:, kk, None].to(dt_)  # [b, h]
+        S = alpha[..., None, None] * S + U[:, kk]
+    S_start = torch.stack(starts, dim=1)                  # [b, k, h, p, n]
+
+    scale = torch.exp(cs) * reads_state.unsqueeze(1).to(dt_)  # [b, h, k, T]
+    y_off = torch.einsum("bkthn,bkhpn,bhkt->bkthp", Cc, S_start, scale)
+    y = (y_diag + y_off).reshape(b, k * T, h, p)
+    if return_states:
+        return y, S, S_start
+    return y, S
 
 
 def ssd_chunk_scan_ref(
@@ -161,11 +231,17 @@ def ssd_chunk_scan_ref(
     initial_states=None,
     return_final_state=False,
     compute_dtype=torch.float32,
+    seq_idx=None,
+    return_chunk_states=False,
 ):
     """Mamba-2 SSD forward, public reference semantics.
 
     Shapes: x [b,l,h,p], dt [b,l,h], A [h], B/C [b,l,g,n], D [h] or [h,p],
-    z [b,l,h,p], dt_bias [h], initial_states [b,h,p,n].
+    z [b,l,h,p], dt_bias [h], initial_states [b,h,p,n], seq_idx [b,l]
+    (integer sequence ids, the masks of ``ssd_chunked_core``; they make the
+    result depend on ``chunk_size`` unless the ids are non-decreasing and
+    non-negative).  ``return_chunk_states`` appends the state entering every
+    logical chunk [b, h, k, p, n] to the returned tuple.
 
     Behaviour follows mamba_torch/ssd_reference.py:192-326: inputs are upcast
     to ``compute_dtype`` (fp32 by default; fp64 for finite differences), L is
@@ -188,28 +264,34 @@ def ssd_chunk_scan_ref(
     xdt = xf * q.unsqueeze(-1)
 
     pad = (-l) % chunk_size
+    sid = None if seq_idx is None else seq_idx.to(torch.int64)
     if pad:
         xdt = F.pad(xdt, (0, 0, 0, 0, 0, pad))
         dA = F.pad(dA, (0, 0, 0, pad))
         Bf = F.pad(Bf, (0, 0, 0, 0, 0, pad))
         Cf = F.pad(Cf, (0, 0, 0, 0, 0, pad))
+        if sid is not None:
+            # the last chunk's id is that of the last real token (the pad adds nothing)
+            sid = torch.cat([sid, sid[:, -1:].expand(-1, pad)], dim=1)
     init = None if initial_states is None else initial_states.to(cd)
     if init is not None and tuple(init.shape) != (b, h, p, n):
         raise ValueError(f"initial_states shape {tuple(init.shape)} != {(b, h, p, n)}")
 
-    ys, finals = [], []
+    ys, finals, starts = [], [], []
     for gi in range(g):
         hs = slice(gi * r, (gi + 1) * r)
         Bg = Bf[:, :, gi : gi + 1, :].expand(-1, -1, r, -1)
         Cg = Cf[:, :, gi : gi + 1, :].expand(-1, -1, r, -1)
-        y_g, f_g = ssd_chunked_core(
+        res = ssd_chunked_core(
             xdt[:, :, hs], dA[:, :, hs], Bg, Cg, chunk_size,
-            None if init is None else init[:, hs],
+            None if init is None else init[:, hs], seq_idx=sid, return_states=True,
         )
-        ys.append(y_g)
-        finals.append(f_g)
+        ys.append(res[0])
+        finals.append(res[1])
+        starts.append(res[2])
     y = torch.cat(ys, dim=2)[:, :l]
     final = torch.cat(finals, dim=1)
+    chunk_states = torch.cat(starts, dim=2).permute(0, 2, 1, 3, 4)  # [b, h, k, p, n]
 
     if D is not None:
         Df = D.to(cd)
@@ -217,9 +299,47 @@ def ssd_chunk_scan_ref(
     if z is not None:
         y = y * F.silu(z.to(cd))
     y = y.to(out_dtype)
+    if return_chunk_states:
+        return (y, final, chunk_states) if return_final_state else (y, chunk_states)
     if return_final_state:
         return y, final
     return y
+
+
+def chunk_state_varlen_ref(x, dt, A, B, chunk_size, cu_seqlens, chunk_states, dt_bias=None,
+                           dt_softplus=False, dt_limit=(0.0, float("inf"))):
+    """State at the end of each packed sequence of a batch-1 input.
+
+    x [1,l,h,p], dt [1,l,h], B [1,l,g,n], cu_seqlens [nseq + 1] (sequence i is
+    tokens cu[i] .. cu[i+1] - 1), chunk_states [1,h,k,p,n] the state entering
+    each logical chunk (``ssd_chunk_scan_ref(..., return_chunk_states=True)``).
+    For the chunk c holding the sequence's last token: the sequence's tokens
+    in that chunk, decayed to its end, plus -- when the sequence began before
+    the chunk -- chunk_states[c] decayed over the chunk's tokens up to the end.
+    Follows mamba_triton_ascend/mamba2/ops/triton/ssd_chunk_state.py:700-775
+    (chunk_state_varlen, 1141-1170).  Returns [nseq, h, p, n].
+    """
+    h = x.shape[2]
+    g = B.shape[2]
+    r = h // g
+    q = discretize(dt, dt_bias, dt_softplus, dt_limit)[0]      # [l, h]
+    a = q * A.reshape(1, h)
+    Bh = B[0].repeat_interleave(r, dim=1)                       # [l, h, n]
+    out = []
+    cu = [int(v) for v in cu_seqlens]
+    for i in range(len(cu) - 1):
+        start, end = cu[i], cu[i + 1]
+        c = (end - 1) // chunk_size
+        c0 = c * chunk_size
+        lo = max(start, c0)
+        cs = a[c0:end].cumsum(0)                                 # chunk-local, [end - c0, h]
+        last = cs[-1]
+        w = torch.exp(last - cs[lo - c0:]) * q[lo:end]           # [end - lo, h]
+        S = torch.einsum("th,thp,thn->hpn", w, x[0, lo:end], Bh[lo:end])
+        if start < c0:
+            S = S + torch.exp(last)[:, None, None] * chunk_states[0, :, c]
+        out.append(S)
+    return torch.stack(out, dim=0)
 
 
 def ssd_sequential_ref(

@@ -165,9 +165,9 @@ def test_forward_chunk_states_are_prefix_final_states():
     _say(f"chunk states {shape}")
     inp = make_inputs(shape, seed=8, features=("bias", "init"))
     dev = {k: v.cuda() for k, v in inp.items()}
-    _, _, _, states = api._fwd_raw(dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"], None, None,
-                                   dev["dt_bias"], dev["initial_states"], 64, True, 0.0, math.inf,
-                                   want_states=True)
+    _, _, _, states, _ = api._fwd_raw(dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"], None, None,
+                                      dev["dt_bias"], dev["initial_states"], 64, True, 0.0, math.inf,
+                                      want_states=True)
     states = states.cpu()
     assert states.shape == (2, 4, 4, 64, 64)
     for k in range(4):
@@ -199,8 +199,8 @@ def test_backward_saved_states_match_recompute(shape):
     inp = make_inputs(shape, seed=9, features=("D", "bias"))
     dev = {k: v.cuda() for k, v in inp.items()}
     args = (dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"])
-    out, fin, _, states = api._fwd_raw(*args, dev["D"], None, dev["dt_bias"], None, 64, True, 0.0,
-                                       math.inf, want_states=True)
+    out, fin, _, states, _ = api._fwd_raw(*args, dev["D"], None, dev["dt_bias"], None, 64, True, 0.0,
+                                          math.inf, want_states=True)
     dout, dfin = torch.randn_like(out), torch.randn_like(fin)
     common = (dout, dfin, dev["D"], None, dev["dt_bias"], None, 64, True, 0.0, math.inf)
     a = api._bwd_raw(*args, *common, chunk_states=states)

@@ -103,6 +103,12 @@ def test_workspace_size_formula():
     y_half = 4 * 2048 * 16 * 64 * 4
     assert seg + y_half <= got <= seg + y_half + 3 * 256 + 4 * 16 * 8 * 4
     assert ws(fwd, seqlen=0) == 0
+    # varlen states without saved states: the chunk states join the workspace
+    one = _shape(batch=1, seqlen=4096, nheads=256, ngroups=64)
+    assert fwd(ctypes.byref(one), rt.VARLEN_STATES, ctypes.byref(nbytes)) == 0
+    with_states = nbytes.value
+    assert fwd(ctypes.byref(one), rt.VARLEN_STATES | rt.SAVED_STATES, ctypes.byref(nbytes)) == 0
+    assert with_states - nbytes.value == 256 * 64 * 64 * 64 * 4
     bwd = lib.mamba2_ssd_bwd_m1_workspace_size
     k = 4096 // 64
     state_buf = 8 * 256 * k * 64 * 64 * 4
@@ -143,9 +149,29 @@ def test_fwd_rejects_null_and_flag_mismatch_without_gpu():
     assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
     assert "SAVED_STATES" in rt.last_error(lib)
     args.chunk_states = fake
-    args.shape = _shape(dstate=128)  # chunk states are saved for the M1 spec only
+    args.shape = _shape(dstate=32)  # chunk states are saved by the fused kernel only
     assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -2
     args.shape, args.flags, args.chunk_states = _shape(), 0, None
+    # packed sequences: flag and pointer must agree; fused shapes only
+    args.flags = rt.HAS_SEQ_IDX
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
+    assert "seq_idx" in rt.last_error(lib)
+    args.seq_idx = fake
+    args.shape = _shape(headdim=32)
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -2
+    args.shape, args.flags, args.seq_idx = _shape(), 0, None
+    # varlen states: batch 1, nseqs >= 1, chunk_size a multiple of 64
+    args.flags = rt.VARLEN_STATES
+    args.cu_seqlens = fake
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1  # no varlen_states
+    args.varlen_states, args.nseqs = fake, 3
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1  # batch 2
+    assert "batch 1" in rt.last_error(lib)
+    args.shape = _shape(batch=1, chunk_size=96)
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -2
+    args.shape, args.nseqs = _shape(batch=1), 0
+    assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
+    args.flags, args.cu_seqlens, args.varlen_states = 0, None, None
     # fast-path shape without workspace
     assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -3
     assert lib.mamba2_ssd_fwd(None, None, 0, None) == -1
@@ -237,6 +263,26 @@ def test_public_api_training_spec_error():
     x.requires_grad_(True)
     with pytest.raises(NotImplementedError):
         api.mamba2_ssd_fwd(x, dt, A, B, C, 64, dt_softplus=True)
+
+
+def test_public_api_packed_sequence_errors():
+    x, dt, A, B, C = _cpu_inputs()
+    b, l = x.shape[:2]
+    with pytest.raises(RuntimeError, match="seq_idx must have shape"):
+        api.mamba2_ssd_fwd(x, dt, A, B, C, 64, seq_idx=torch.zeros(b, l + 1, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="integer"):
+        api.mamba2_ssd_fwd(x, dt, A, B, C, 64, seq_idx=torch.zeros(b, l))
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        api.mamba2_ssd_fwd(x, dt, A, B, C, 64, return_varlen_states=True)
+    two = [torch.cat([t, t]) if t.dim() > 1 else t for t in (x, dt, A, B, C)]
+    with pytest.raises(RuntimeError, match="batch 1"):
+        api.mamba2_ssd_fwd(*two, 64, cu_seqlens=torch.tensor([0, l]), return_varlen_states=True)
+    with pytest.raises(NotImplementedError, match="multiple of 64"):
+        api.mamba2_ssd_fwd(x, dt, A, B, C, 96, cu_seqlens=torch.tensor([0, l]),
+                           return_varlen_states=True)
+    with pytest.raises(NotImplementedError, match="dstate"):
+        api.mamba2_ssd_fwd(x[..., :32].contiguous(), dt, A, B, C, 64,
+                           seq_idx=torch.zeros(b, l, dtype=torch.int32))
 
 
 def test_meta_shape_inference():

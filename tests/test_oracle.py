@@ -359,3 +359,136 @@ def test_decode_padding_slots():
     assert torch.equal(out[1], torch.zeros(h, p, dtype=torch.float64))
     assert torch.equal(state[1], before[1]) and torch.equal(state[3], before[3])
     assert not torch.equal(state[2], before[2]) and not torch.equal(state[0], before[0])
+
+
+# ----------------------------------------------------------------------------- packed sequences
+
+def _ids_from_lengths(lengths, first=0):
+    return torch.cat([torch.full((n,), first + i, dtype=torch.int64) for i, n in enumerate(lengths)])
+
+
+@pytest.mark.parametrize("chunk", [8, 16, 32])
+def test_seq_idx_all_equal_is_unmasked(chunk):
+    inp = _inputs(2, 40, 4, 3, 5, 2, seed=41, features=("D", "init"))
+    ids = torch.zeros(2, 40, dtype=torch.int64)
+    y0, f0 = ssd_chunk_scan_ref(**inp, chunk_size=chunk, dt_softplus=True, return_final_state=True,
+                                compute_dtype=F64)
+    y1, f1 = ssd_chunk_scan_ref(**inp, chunk_size=chunk, dt_softplus=True, return_final_state=True,
+                                compute_dtype=F64, seq_idx=ids)
+    torch.testing.assert_close(y1, y0, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(f1, f0, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("chunk", [8, 16, 32])
+def test_seq_idx_packed_equals_separate_runs(chunk):
+    """Non-decreasing ids: every token's output equals that of its sequence
+    run alone (the first sequence, id 0, from the initial state), and the
+    final state is the last sequence's; boundaries inside chunks, on chunk
+    edges, a one-token sequence and one spanning several chunks."""
+    lengths = [5, 11, 1, 16, 3, 21, 7]
+    L = sum(lengths)
+    inp = _inputs(1, L, 4, 3, 5, 2, seed=42, features=("D2", "z", "bias", "init"))
+    ids = _ids_from_lengths(lengths)[None]
+    y, fin = ssd_chunk_scan_ref(**inp, chunk_size=chunk, dt_softplus=True, return_final_state=True,
+                                compute_dtype=F64, seq_idx=ids)
+    t0 = 0
+    for i, n in enumerate(lengths):
+        part = {k: (v[:, t0:t0 + n] if k in ("x", "dt", "B", "C", "z") else v) for k, v in inp.items()}
+        part["initial_states"] = inp["initial_states"] if i == 0 else None
+        want, want_fin = ssd_sequential_ref(**part, dt_softplus=True, return_final_state=True)
+        torch.testing.assert_close(y[:, t0:t0 + n], want, rtol=1e-10, atol=1e-10)
+        t0 += n
+    torch.testing.assert_close(fin, want_fin, rtol=1e-10, atol=1e-10)
+
+
+def test_seq_idx_first_sequence_not_zero_drops_initial_state():
+    lengths = [9, 12]
+    inp = _inputs(1, 21, 2, 3, 4, 1, seed=43, features=("init",))
+    ids = _ids_from_lengths(lengths, first=3)[None]
+    y, fin = ssd_chunk_scan_ref(**inp, chunk_size=8, dt_softplus=True, return_final_state=True,
+                                compute_dtype=F64, seq_idx=ids)
+    part = {k: (v[:, :9] if k in ("x", "dt", "B", "C") else v) for k, v in inp.items()}
+    part["initial_states"] = None
+    torch.testing.assert_close(y[:, :9], ssd_sequential_ref(**part, dt_softplus=True),
+                               rtol=1e-10, atol=1e-10)
+
+
+def test_seq_idx_interleaved_in_one_chunk():
+    """Ids interleaved inside one chunk: the tokens of id X see the other
+    tokens of id X (decayed through every token in between) and nothing else,
+    which is the sequential recurrence over the chunk with the x of the other
+    ids zeroed."""
+    L = 16
+    inp = _inputs(1, L, 2, 3, 4, 1, seed=44)
+    ids = torch.tensor([[0, 0, 1, 1, 1, 0, 0, 2, 2, 1, 0, 0, 2, 1, 1, 0]])
+    y = ssd_chunk_scan_ref(**inp, chunk_size=L, dt_softplus=True, compute_dtype=F64, seq_idx=ids)
+    for v in (0, 1, 2):
+        sel = ids[0] == v
+        part = dict(inp)
+        part["x"] = inp["x"] * sel[None, :, None, None].to(F64)
+        want = ssd_sequential_ref(**part, dt_softplus=True)
+        torch.testing.assert_close(y[:, sel], want[:, sel], rtol=1e-10, atol=1e-10)
+
+
+def test_seq_idx_negative_ids_are_padding():
+    """All-negative ids: no chunk enters the state and the initial state is
+    dropped, so the final state is zero and every chunk runs on its own."""
+    T, L = 8, 24
+    inp = _inputs(1, L, 2, 3, 4, 1, seed=45, features=("init",))
+    ids = torch.full((1, L), -1)
+    y, fin = ssd_chunk_scan_ref(**inp, chunk_size=T, dt_softplus=True, return_final_state=True,
+                                compute_dtype=F64, seq_idx=ids)
+    assert torch.equal(fin, torch.zeros_like(fin))
+    for c in range(L // T):
+        part = {k: (v[:, c * T:(c + 1) * T] if k in ("x", "dt", "B", "C") else v) for k, v in inp.items()}
+        part["initial_states"] = None
+        torch.testing.assert_close(y[:, c * T:(c + 1) * T], ssd_sequential_ref(**part, dt_softplus=True),
+                                   rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("chunk", [8, 16])
+def test_varlen_states_equal_separate_final_states(chunk):
+    """chunk_state_varlen: the state at the end of every packed sequence is
+    that sequence's final state run alone (a sequence starting on a chunk
+    edge, one spanning several chunks, one token long, one ending the input
+    mid-chunk)."""
+    from oracle.ssd_reference import chunk_state_varlen_ref
+
+    lengths = [5, 11, 16, 1, 20, 6]
+    L = sum(lengths)
+    inp = _inputs(1, L, 4, 3, 5, 2, seed=46, features=("bias",))
+    ids = _ids_from_lengths(lengths)[None]
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)))
+    _, states = ssd_chunk_scan_ref(**inp, chunk_size=chunk, dt_softplus=True, compute_dtype=F64,
+                                   seq_idx=ids, return_chunk_states=True)
+    got = chunk_state_varlen_ref(inp["x"], inp["dt"], inp["A"], inp["B"], chunk, cu, states,
+                                 dt_bias=inp["dt_bias"], dt_softplus=True)
+    assert got.shape == (len(lengths), 4, 3, 5)
+    t0 = 0
+    for i, n in enumerate(lengths):
+        part = {k: (v[:, t0:t0 + n] if k in ("x", "dt", "B", "C") else v) for k, v in inp.items()}
+        _, fin = ssd_sequential_ref(**part, dt_softplus=True, return_final_state=True)
+        torch.testing.assert_close(got[i], fin[0], rtol=1e-10, atol=1e-10)
+        t0 += n
+
+
+@pytest.mark.parametrize("first_len,keeps_init", [(5, False), (11, True)])
+def test_varlen_states_initial_state_only_through_chunk_states(first_len, keeps_init):
+    """chunk_state_varlen adds the initial state only through chunk_states,
+    i.e. only when the first sequence runs past the first chunk (chunk 8: a
+    5-token first sequence ends without it, an 11-token one with it)."""
+    from oracle.ssd_reference import chunk_state_varlen_ref
+
+    lengths = [first_len, 7]
+    L = sum(lengths)
+    inp = _inputs(1, L, 2, 3, 4, 1, seed=47, features=("init",))
+    ids = _ids_from_lengths(lengths)[None]
+    cu = torch.tensor([0, first_len, L])
+    _, states = ssd_chunk_scan_ref(**inp, chunk_size=8, dt_softplus=True, compute_dtype=F64,
+                                   seq_idx=ids, return_chunk_states=True)
+    got = chunk_state_varlen_ref(inp["x"], inp["dt"], inp["A"], inp["B"], 8, cu, states,
+                                 dt_softplus=True)
+    part = {k: (v[:, :first_len] if k in ("x", "dt", "B", "C") else v) for k, v in inp.items()}
+    part["initial_states"] = inp["initial_states"] if keeps_init else None
+    _, fin = ssd_sequential_ref(**part, dt_softplus=True, return_final_state=True)
+    torch.testing.assert_close(got[0], fin[0], rtol=1e-10, atol=1e-10)
