@@ -63,8 +63,8 @@ extern "C" {
 #define MAMBA2_SSD_SAVED_STATES (1u << 6)
 /* packed sequences: seq_idx [B, L] gives every token's sequence id (the
  * seq_idx argument of the reference's Triton port,
- * mamba_triton_ascend/mamba2/ops/triton/ssd_combined.py:359-409); forward
- * only, headdim 64 with dstate 64 or 128 */
+ * mamba_triton_ascend/mamba2/ops/triton/ssd_combined.py:359-409);
+ * forward: headdim 64 with dstate 64 or 128; backward: with SAVED_STATES */
 #define MAMBA2_SSD_HAS_SEQ_IDX (1u << 7)
 /* forward: also write the state at the end of every sequence of a batch-1
  * input split by cu_seqlens (ssd_combined.py:406-409, chunk_state_varlen);
@@ -128,6 +128,9 @@ typedef struct Mamba2SsdBwdArgs {
                                   required iff SAVED_STATES, else NULL */
     float *dx, *ddt, *dA, *dB, *dC;
     float *dD, *dz, *ddt_bias, *dinitial_states; /* required iff the feature is flagged */
+    /* member below added in ABI 4 */
+    const int32_t *seq_idx;    /* [B, L] iff HAS_SEQ_IDX (the forward's ids; needs
+                                  SAVED_STATES from that forward), else NULL */
 } Mamba2SsdBwdArgs;
 
 /* Bytes of device workspace mamba2_ssd_fwd needs for this shape/flags

@@ -83,6 +83,7 @@ class Mamba2SsdBwdArgs(ctypes.Structure):
         ("dout", _c_fp), ("dfinal_state", _c_fp), ("pre_gate", _c_fp), ("chunk_states", _c_fp),
         ("dx", _c_fp), ("ddt", _c_fp), ("dA", _c_fp), ("dB", _c_fp), ("dC", _c_fp),
         ("dD", _c_fp), ("dz", _c_fp), ("ddt_bias", _c_fp), ("dinitial_states", _c_fp),
+        ("seq_idx", _c_fp),
     ]
 
 

@@ -221,12 +221,15 @@ def _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size, dt_softp
 
 
 def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, chunk_size,
-             dt_softplus, dt_limit_min, dt_limit_max, pre_gate=None, chunk_states=None):
+             dt_softplus, dt_limit_min, dt_limit_max, pre_gate=None, chunk_states=None,
+             seq_idx=None):
     lib = rt.load_library()
     shape = _shape(x, B, chunk_size)
     flags = _flags(D, z, dt_bias, initial_states, dt_softplus)
     if chunk_states is not None:
         flags |= rt.SAVED_STATES
+    if seq_idx is not None:
+        flags |= rt.HAS_SEQ_IDX
     nbytes = ctypes.c_size_t(0)
     rt.check(lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(shape), flags, ctypes.byref(nbytes)),
              "mamba2_ssd_bwd_m1_workspace_size", lib)
@@ -246,7 +249,7 @@ def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, 
         _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(initial_states),
         _ptr(dout), _ptr(dfinal_state), _ptr(pre_gate), _ptr(chunk_states),
         _ptr(dx), _ptr(ddt), _ptr(dA), _ptr(dB), _ptr(dC),
-        _ptr(dD), _ptr(dz), _ptr(ddt_bias), _ptr(dinit),
+        _ptr(dD), _ptr(dz), _ptr(ddt_bias), _ptr(dinit), _ptr(seq_idx),
     )
     with torch.cuda.device(x.device):
         rt.check(lib.mamba2_ssd_bwd_m1(ctypes.byref(args), _ptr(ws), ws.numel(), _stream(x.device)),
@@ -267,7 +270,8 @@ _BWD_SCHEMA = (
     "Tensor? dfinal_state=None, Tensor? D=None, Tensor? z=None, Tensor? dt_bias=None, "
     "Tensor? initial_states=None, Tensor? pre_gate=None, Tensor? chunk_states=None, "
     "int chunk_size=64, "
-    "bool dt_softplus=False, float dt_limit_min=0.0, float dt_limit_max=3.402823466e+38) "
+    "bool dt_softplus=False, float dt_limit_min=0.0, float dt_limit_max=3.402823466e+38, "
+    "Tensor? seq_idx=None) "
     "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
     "Tensor, Tensor)"
 )
@@ -299,7 +303,7 @@ def _empty_like_or_none(t, ref):
 def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bias=None,
                  initial_states=None,
                  pre_gate=None, chunk_states=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
-                 dt_limit_max=3.402823466e+38):
+                 dt_limit_max=3.402823466e+38, seq_idx=None):
     op = "mamba2_ssd_bwd_m1"
     _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
                   dt_limit_min, dt_limit_max)
@@ -321,16 +325,20 @@ def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bia
         want = (x.shape[0], x.shape[2], _nchunks(x), x.shape[3], B.shape[3])
         if tuple(chunk_states.shape) != want:
             raise RuntimeError(f"{op}: chunk_states must have shape [B,H,ceil(L/64),P,N] = {list(want)}")
+    if seq_idx is not None:
+        if chunk_states is None:
+            raise RuntimeError(f"{op}: seq_idx needs the packed forward's chunk_states")
+        seq_idx = _check_seq_idx(x, seq_idx, chunk_size, B)
     grads = _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
                      chunk_size, dt_softplus, dt_limit_min, dt_limit_max,
-                     pre_gate if z is not None else None, chunk_states)
+                     pre_gate if z is not None else None, chunk_states, seq_idx)
     return tuple(_empty_like_or_none(g, x) for g in grads)
 
 
 def _op_bwd_meta(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bias=None,
                  initial_states=None,
                  pre_gate=None, chunk_states=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
-                 dt_limit_max=3.402823466e+38):
+                 dt_limit_max=3.402823466e+38, seq_idx=None):
     like = lambda t: x.new_empty(0) if t is None else torch.empty_like(t)  # noqa: E731
     return (torch.empty_like(x), torch.empty_like(dt), torch.empty_like(A), torch.empty_like(B),
             torch.empty_like(C), like(D), like(z), like(dt_bias), like(initial_states))
@@ -409,21 +417,24 @@ def _can_use_native_bwd_m1(x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_st
 class _Mamba2SsdAutogradM1(torch.autograd.Function):
     """Autograd contract of mamba2.py:1661-1838: saves the inputs, the
     chunk-start states (and pre_gate with z), recomputes the other forward
-    intermediates in backward, returns 13 gradients."""
+    intermediates in backward, returns 13 gradients (plus None for the
+    packed-sequence arguments ``seq_idx`` / ``cu_seqlens``, the Triton port's
+    extension, ssd_combined.py:612-637).  The third output, the varlen
+    states, is not differentiable (that port's backward rejects it)."""
 
     @staticmethod
     def forward(ctx, x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus,
-                dt_limit_min, dt_limit_max, initial_states):
+                dt_limit_min, dt_limit_max, initial_states, seq_idx=None, cu_seqlens=None):
         _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
                       initial_states, dt_limit_min, dt_limit_max)
         # the pre-gate output y + D x is saved when z is present (dz needs it),
         # as the reference's Train forward does (mamba2.py:1682-1770)
         # and so are the chunk-start states (the reference's training forward
         # returns states_start for its backward, mamba2.py:228,322,408-418)
-        out, final_state, pre_gate, states, _ = _fwd_raw(
+        out, final_state, pre_gate, states, varlen = _fwd_raw(
             x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
             float(dt_limit_min), float(dt_limit_max), want_final=True,
-            want_pre_gate=z is not None, want_states=True)
+            want_pre_gate=z is not None, want_states=True, seq_idx=seq_idx, cu_seqlens=cu_seqlens)
         empty = x.new_empty(0)
         ctx.save_for_backward(
             x, dt, A, B, C,
@@ -433,17 +444,22 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
             initial_states if initial_states is not None else empty,
             pre_gate if pre_gate is not None else empty,
             states,
+            seq_idx if seq_idx is not None else empty,
         )
-        ctx.has = (D is not None, z is not None, dt_bias is not None, initial_states is not None)
+        ctx.has = (D is not None, z is not None, dt_bias is not None, initial_states is not None,
+                   seq_idx is not None)
         ctx.chunk_size = int(chunk_size)
         ctx.dt_softplus = bool(dt_softplus)
         ctx.dt_limit = (float(dt_limit_min), float(dt_limit_max))
-        return out, final_state
+        if varlen is None:
+            varlen = empty
+        ctx.mark_non_differentiable(varlen)
+        return out, final_state, varlen
 
     @staticmethod
-    def backward(ctx, dout, dfinal_state):
-        x, dt, A, B, C, D, z, dt_bias, initial_states, pre_gate, states = ctx.saved_tensors
-        has_D, has_z, has_bias, has_init = ctx.has
+    def backward(ctx, dout, dfinal_state, _dvarlen):
+        x, dt, A, B, C, D, z, dt_bias, initial_states, pre_gate, states, seq_idx = ctx.saved_tensors
+        has_D, has_z, has_bias, has_init, has_seq = ctx.has
         if dout is None:
             dout = torch.zeros_like(x)
         grads = torch.ops.mamba_ascend.mamba2_ssd_bwd_m1(
@@ -451,11 +467,12 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
             None if dfinal_state is None else dfinal_state.contiguous(),
             D if has_D else None, z if has_z else None, dt_bias if has_bias else None,
             initial_states if has_init else None, pre_gate if has_z else None, states,
-            ctx.chunk_size, ctx.dt_softplus, ctx.dt_limit[0], ctx.dt_limit[1])
+            ctx.chunk_size, ctx.dt_softplus, ctx.dt_limit[0], ctx.dt_limit[1],
+            seq_idx if has_seq else None)
         dx, ddt, dA, dB, dC, dD, dz, ddt_bias, dinit = grads
         return (dx, ddt, dA, dB, dC, None,
                 dD if has_D else None, dz if has_z else None, ddt_bias if has_bias else None,
-                None, None, None, dinit if has_init else None)
+                None, None, None, dinit if has_init else None, None, None)
 
 
 # ----------------------------------------------------------------------------- public API
@@ -507,15 +524,16 @@ def mamba2_ssd_fwd(
     seq32 = _check_seq_idx(x, seq_idx, chunk_size, B)
     cu32 = _check_cu_seqlens(x, cu_seqlens, chunk_size, B) if return_varlen_states else None
     if _requires_grad(x, dt, A, B, C, D, z, dt_bias, initial_states):
-        if seq32 is not None or cu32 is not None:
-            raise NotImplementedError("mamba2_ssd_fwd: seq_idx and varlen states are forward-only")
         if not _can_use_native_bwd_m1(x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states):
             raise NotImplementedError(
                 "mamba2_ssd_fwd backward requires contiguous FP32 GPU tensors with "
                 "headdim == dstate == 64"
             )
-        out, final_state = _Mamba2SsdAutogradM1.apply(
-            x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus, lo, hi, initial_states)
+        out, final_state, varlen = _Mamba2SsdAutogradM1.apply(
+            x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus, lo, hi, initial_states,
+            seq32, cu32)
+        if cu32 is not None:
+            return (out, final_state, varlen) if return_final_state else (out, varlen)
     else:
         _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
                       initial_states, lo, hi)

@@ -452,6 +452,13 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     if (bool(f & MAMBA2_SSD_SAVED_STATES) != (a->chunk_states != nullptr))
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
                     "chunk_states pointer and SAVED_STATES flag disagree");
+    if (bool(f & MAMBA2_SSD_HAS_SEQ_IDX) != (a->seq_idx != nullptr))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "seq_idx pointer and HAS_SEQ_IDX flag disagree");
+    if ((f & MAMBA2_SSD_HAS_SEQ_IDX) && !(f & MAMBA2_SSD_SAVED_STATES))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "HAS_SEQ_IDX needs SAVED_STATES (the chunk states of the packed forward)");
+    if (f & MAMBA2_SSD_VARLEN_STATES)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "VARLEN_STATES is a forward-only flag");
     if (!bwd_supported(s))
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
                     "mamba2_ssd_bwd_m1 needs headdim == dstate == 64 (got %lld, %lld)",
@@ -510,6 +517,8 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     bp.dstates = (float *)(ws + lay.dstates);
     bp.dfinal = a->dfinal_state;
     bp.dinit = a->dinitial_states;
+    bp.seq_idx = a->seq_idx;
+    const bool seq = a->seq_idx != nullptr;
     bp.part_dA = (float *)(ws + lay.part_dA);
     bp.part_dbias = (float *)(ws + lay.part_db);
     bp.part_dD = (float *)(ws + lay.part_dD);
@@ -541,17 +550,22 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
         // one pass: reverse chunk order, state gradients carried in registers
         const dim3 grid((unsigned)bg), block(ssd::kBwsThreads);
         const int R = bp.R;
-#define SSD_LAUNCH_REV(Z, RR) \
-    hipLaunchKernelGGL((ssd::k_bwd_ws<Z, RR>), grid, block, 0, st, bp, 1, K)
+#define SSD_LAUNCH_REV(Z, RR, Q) \
+    hipLaunchKernelGGL((ssd::k_bwd_ws<Z, RR, Q>), grid, block, 0, st, bp, 1, K)
+#define SSD_LAUNCH_REV_R(Z, Q)                \
+    do {                                      \
+        if (R == 1) SSD_LAUNCH_REV(Z, 1, Q);  \
+        else if (R == 2) SSD_LAUNCH_REV(Z, 2, Q); \
+        else SSD_LAUNCH_REV(Z, 4, Q);         \
+    } while (0)
         if (bp.has_z) {
-            if (R == 1) SSD_LAUNCH_REV(true, 1);
-            else if (R == 2) SSD_LAUNCH_REV(true, 2);
-            else SSD_LAUNCH_REV(true, 4);
+            if (seq) SSD_LAUNCH_REV_R(true, true);
+            else SSD_LAUNCH_REV_R(true, false);
         } else {
-            if (R == 1) SSD_LAUNCH_REV(false, 1);
-            else if (R == 2) SSD_LAUNCH_REV(false, 2);
-            else SSD_LAUNCH_REV(false, 4);
+            if (seq) SSD_LAUNCH_REV_R(false, true);
+            else SSD_LAUNCH_REV_R(false, false);
         }
+#undef SSD_LAUNCH_REV_R
 #undef SSD_LAUNCH_REV
         if (int rc = launch_status("k_bwd_ws_rev", tr, st)) return rc;
         hipLaunchKernelGGL(ssd::k_bwd_finalize_slots, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
@@ -562,12 +576,22 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     }
     // state gradients dU_k (and dinitial_states)
     if ((int64_t)B * H >= kMinRevStreams) {
-        if (bp.has_z)
-            hipLaunchKernelGGL(ssd::k_bwd_dstate_rev<true>, dim3((unsigned)(B * H)), dim3(ssd::kWsThreads),
-                               0, st, bp, a->dfinal_state, a->dinitial_states);
-        else
-            hipLaunchKernelGGL(ssd::k_bwd_dstate_rev<false>, dim3((unsigned)(B * H)), dim3(ssd::kWsThreads),
-                               0, st, bp, a->dfinal_state, a->dinitial_states);
+        const dim3 rgrid((unsigned)(B * H)), rblock(ssd::kWsThreads);
+        if (bp.has_z) {
+            if (seq)
+                hipLaunchKernelGGL((ssd::k_bwd_dstate_rev<true, true>), rgrid, rblock, 0, st, bp,
+                                   a->dfinal_state, a->dinitial_states);
+            else
+                hipLaunchKernelGGL((ssd::k_bwd_dstate_rev<true, false>), rgrid, rblock, 0, st, bp,
+                                   a->dfinal_state, a->dinitial_states);
+        } else {
+            if (seq)
+                hipLaunchKernelGGL((ssd::k_bwd_dstate_rev<false, true>), rgrid, rblock, 0, st, bp,
+                                   a->dfinal_state, a->dinitial_states);
+            else
+                hipLaunchKernelGGL((ssd::k_bwd_dstate_rev<false, false>), rgrid, rblock, 0, st, bp,
+                                   a->dfinal_state, a->dinitial_states);
+        }
         if (int rc = launch_status("k_bwd_dstate_rev", tr, st)) return rc;
     } else {
         hipLaunchKernelGGL(ssd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);
@@ -581,12 +605,18 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     nseg = nseg < K ? nseg : K;
     const int M = (int)((K + nseg - 1) / nseg);
     nseg = (K + M - 1) / M;
-    if (bp.has_z)
-        hipLaunchKernelGGL(ssd::k_bwd_ws<true>, dim3((unsigned)(bg * nseg)), dim3(ssd::kBwsThreads), 0,
-                           st, bp, (int)nseg, M);
-    else
-        hipLaunchKernelGGL(ssd::k_bwd_ws<false>, dim3((unsigned)(bg * nseg)), dim3(ssd::kBwsThreads), 0,
-                           st, bp, (int)nseg, M);
+    const dim3 wgrid((unsigned)(bg * nseg)), wblock(ssd::kBwsThreads);
+    if (bp.has_z) {
+        if (seq)
+            hipLaunchKernelGGL((ssd::k_bwd_ws<true, 0, true>), wgrid, wblock, 0, st, bp, (int)nseg, M);
+        else
+            hipLaunchKernelGGL((ssd::k_bwd_ws<true, 0, false>), wgrid, wblock, 0, st, bp, (int)nseg, M);
+    } else {
+        if (seq)
+            hipLaunchKernelGGL((ssd::k_bwd_ws<false, 0, true>), wgrid, wblock, 0, st, bp, (int)nseg, M);
+        else
+            hipLaunchKernelGGL((ssd::k_bwd_ws<false, 0, false>), wgrid, wblock, 0, st, bp, (int)nseg, M);
+    }
     if (int rc = launch_status("k_bwd_ws", tr, st)) return rc;
     hipLaunchKernelGGL(ssd::k_bwd_finalize_slots, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
                        bp.part_dbias, bp.part_dD, a->dA, a->ddt_bias, a->dD, B, H, K, 64,

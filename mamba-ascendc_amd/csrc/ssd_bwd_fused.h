@@ -54,11 +54,18 @@ constexpr int kBwsSlots = 4;      // partial sums per (b, h, k): one per consume
 // in), so no dU reaches HBM:
 //   dU_k = g;   g <- dSoff_k + exp(cs_last_k) g,   dSoff_k = (gy exp(cs))^T C,
 // starting from dfinal_state and ending at dinitial_states.
-template <bool kHasZ, int kRevR = 0>
+//
+// kSeq: packed sequences (prm.seq_idx), the forward's masks in adjoint form:
+// W (and so dW, dCB and their dcs terms) only between equal ids, the state
+// terms through s_dte (tokens that enter the state leaving the chunk) and
+// s_ecs (tokens that read the state entering it), and the carry of the
+// state across the chunk (alpha and the chunk-end dcs term) through s_carry.
+template <bool kHasZ, int kRevR = 0, bool kSeq = false>
 __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg, int M) {
     static_assert(kRevR == 0 || kRevR == 1 || kRevR == 2 || kRevR == 4, "heads per group");
     constexpr bool kRev = kRevR > 0;
     constexpr int T = 64, P = 64, N = 64;
+    constexpr int TS = kSeq ? T : 1;
     // x and gy tiles double buffered by step parity (the epilogue of step n
     // still reads them while step n + 1 runs); S, dU, B, C single
     __shared__ __attribute__((aligned(16))) _Float16 lds[16 * kTile];
@@ -68,6 +75,8 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     __shared__ float s_dcs[2][T], s_rd[2][T], s_A[2];
     __shared__ __attribute__((aligned(16))) float s_sdu[2][4];
     __shared__ __attribute__((aligned(16))) float s_da[4][T]; // epilogue: da of a step, per consumer wave
+    __shared__ __attribute__((aligned(16))) int s_sid[2][TS];   // kSeq: token ids, by step parity
+    __shared__ float s_carry[2];                                 // kSeq: 1 where the state carries over
 
     auto Xt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, par); };
     auto Gt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, 2 + par); };
@@ -101,6 +110,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
         float4 xr[4], gr[4], zr[4], pr[4], sr[4], ur[4], br[4], cr[4];
         float dtr = 0.f, Ahr = 0.f, biasr = 0.f, Dr = 0.f;
+        int sidr = 0, sprv = 0; // kSeq: id of token `lane`, id of the token before the chunk
         const float *dtb = prm.dt_bias ? prm.dt_bias : prm.A; // read unconditionally
         const float *Dp = prm.has_D ? prm.D : prm.A;
         auto load_xg = [&](int n) __attribute__((always_inline)) {
@@ -122,6 +132,12 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 }
             }
             dtr = prm.dt[((int64_t)b * prm.L + (int64_t)k * T + min(lane, tv - 1)) * H + h];
+            if (kSeq) {
+                const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + (int64_t)k * T;
+                sidr = si[min(lane, tv - 1)];
+                const int pv = si[k > 0 ? -1 : 0]; // read unconditionally, 0 before the first chunk
+                sprv = k > 0 ? pv : 0;
+            }
             Dr = Dp[prm.has_D && prm.d_per_channel ? h * P + lane : h];
             Ahr = prm.A[h];
             biasr = dtb[h];
@@ -244,11 +260,19 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 }
                 const float cs = wave_inclusive_scan(a); // log2 units
                 const float last = readlane_f(cs, T - 1);
+                float into = 1.f, reads = 1.f;
+                if (kSeq) {
+                    const int e_end = __shfl(sidr, T - 1, kWave); // rows past the end repeat the last id
+                    into = (sidr == e_end && e_end >= 0) ? 1.f : 0.f;
+                    reads = sidr == sprv ? 1.f : 0.f;
+                    s_sid[par][lane] = sidr;
+                    if (lane == 0) s_carry[par] = e_end == sprv ? 1.f : 0.f;
+                }
                 s_q[par][lane] = q;
                 s_cs[par][lane] = cs;
                 s_dqdu[par][lane] = dq;
-                s_dte[par][lane] = exp2_f(last - cs);
-                s_ecs[par][lane] = exp2_f(cs);
+                s_dte[par][lane] = exp2_f(last - cs) * into;
+                s_ecs[par][lane] = exp2_f(cs) * reads;
                 s_D[par][lane] = prm.has_D ? Dr : 0.f;
                 if (lane == 0) s_A[par] = Ahr;
             }
@@ -316,7 +340,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 ae[m] = pack_frag(v);
             }
             const SplitTile gt = tile_at(lp, 2 + par);
-            const float alpha = exp2_f(s_cs[par][T - 1]);
+            const float alpha = kSeq ? exp2_f(s_cs[par][T - 1]) * s_carry[par] : exp2_f(s_cs[par][T - 1]);
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
                 f32x4 d = zero4();
@@ -432,7 +456,8 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             // lane forms them from wave-uniform values)
             const float rd_tot = wave_sum(s_rd[par][lane]);
             const float4 sdu4 = *(const float4 *)&s_sdu[par][0];
-            const float tail = rd_tot + exp2_f(s_cs[par][T - 1]) * (sdu4.x + sdu4.y + sdu4.z + sdu4.w);
+            const float carry = kSeq ? s_carry[par] : 1.f;
+            const float tail = rd_tot + carry * exp2_f(s_cs[par][T - 1]) * (sdu4.x + sdu4.y + sdu4.z + sdu4.w);
             const float v = s_dcs[par][lane] + (lane == T - 1 ? tail : 0.f);
             const float da = wave_suffix_scan(v);
             if (W == 0) {
@@ -506,6 +531,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                     Xo[ks] = frag(xt, own, ks);
                 }
                 const float cs_own = cs_[own], q_own = q_[own];
+                const int sid_own = kSeq ? s_sid[par][own] : 0;
                 Frag DCT[2], DCS[2], WS[2];
                 float rows = 0.f, cols = 0.f;
                 {
@@ -523,9 +549,14 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                             const float4 qv = *(const float4 *)&q_[16 * j + 4 * kq];
                             const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
                             const float qa[4] = {qv.x, qv.y, qv.z, qv.w}, cva[4] = {cv.x, cv.y, cv.z, cv.w};
+                            int sva[4] = {0, 0, 0, 0};
+                            if (kSeq) {
+                                const int4 sv = *(const int4 *)&s_sid[par][16 * j + 4 * kq];
+                                sva[0] = sv.x, sva[1] = sv.y, sva[2] = sv.z, sva[3] = sv.w;
+                            }
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
-                                const bool in = j < W || 4 * kq + i <= r16;
+                                const bool in = (j < W || 4 * kq + i <= r16) && (!kSeq || sva[i] == sid_own);
                                 const float e = in ? exp2_f(cs_own - cva[i]) : 0.f;
                                 const float dwv = dw[i] * qa[i];
                                 rows += dwv * cb[i] * e;
@@ -553,9 +584,14 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                             }
                             const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
                             const float cva[4] = {cv.x, cv.y, cv.z, cv.w};
+                            int sva[4] = {0, 0, 0, 0};
+                            if (kSeq) {
+                                const int4 sv = *(const int4 *)&s_sid[par][16 * j + 4 * kq];
+                                sva[0] = sv.x, sva[1] = sv.y, sva[2] = sv.z, sva[3] = sv.w;
+                            }
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
-                                const bool in = j > W || r16 <= 4 * kq + i;
+                                const bool in = (j > W || r16 <= 4 * kq + i) && (!kSeq || sva[i] == sid_own);
                                 const float e = in ? exp2_f(cva[i] - cs_own) : 0.f;
                                 const float dwv = dw[i] * q_own, wsv = cb[i] * e;
                                 cols += dwv * wsv;
@@ -706,7 +742,9 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 // dSoff^T[n][p] = sum_t C[t][n] (gy exp(cs))[t][p], read transposed from LDS.
 // The recurrence is that of mamba_ascendc/csrc/ops/mamba2_ssd_state_passing_bwd
 // (state_passing_bwd/design.md:44-61) with the dS_off product fused in.
-template <bool kHasZ>
+// kSeq: packed sequences, exp(cs_t) only for tokens that read the entering
+// state and the carry only where the state is not cut (as in k_bwd_ws).
+template <bool kHasZ, bool kSeq = false>
 __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, const float *dfinal,
                                                                 float *dinit) {
     constexpr int T = 64, P = 64, N = 64;
@@ -736,6 +774,7 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
         float4 gr[kDepth][4], zr[kDepth][4], cr[kDepth][4];
         float dtr[kDepth];
+        int sidr[kDepth], sprv[kDepth]; // kSeq: id of token `lane`, id of the token before the chunk
         // unconditional loads (exact wait counts): rows past the sequence end
         // re-read its last row (zeroed when staged), steps past the first
         // chunk read through an empty-range resource (zeros, no traffic)
@@ -757,6 +796,12 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
                 cr[sl][j] = buf_load4(rc, row * rowGN4 + c4 * 4, 0);
             }
             dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * H + h];
+            if (kSeq) {
+                const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + t0;
+                sidr[sl] = si[min(lane, tv - 1)];
+                const int pv = si[t0 > 0 ? -1 : 0]; // read unconditionally, 0 before the first chunk
+                sprv[sl] = t0 > 0 ? pv : 0;
+            }
         };
         auto put = [&](SplitTile d, int row, float4 v) {
             half4 vh, vl;
@@ -770,8 +815,14 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
             float a = 0.f;
             if (lane < tv) a = Ah2 * discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
             const float cs = wave_inclusive_scan(a); // log2 units
-            if (w == 0 && lane == 0) s_alpha[s] = exp2_f(readlane_f(cs, T - 1));
-            const float ecs = exp2_f(cs);
+            float reads = 1.f, carry = 1.f;
+            if (kSeq) {
+                const int e_end = __shfl(sidr[sl], T - 1, kWave);
+                reads = sidr[sl] == sprv[sl] ? 1.f : 0.f;
+                carry = e_end == sprv[sl] ? 1.f : 0.f;
+            }
+            if (w == 0 && lane == 0) s_alpha[s] = exp2_f(readlane_f(cs, T - 1)) * carry;
+            const float ecs = exp2_f(cs) * reads;
             const SplitTile ge = GE(s), ct = CT(s);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {

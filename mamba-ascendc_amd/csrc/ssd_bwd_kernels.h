@@ -6,7 +6,9 @@
 // (or dout), decay_t = exp(cs_last - cs_t):
 //
 //   k_bwd_dstate      : dSoff_k[p][n] = sum_t gy_t[p] exp(cs_t) C_t[n] (and the
-//                       chunk log decay cs_last)
+//                       chunk log decay cs_last; with packed sequences the
+//                       forward's masks: exp(cs_t) only for tokens that read
+//                       the entering state, -inf where the state is cut)
 //   k_state_pass_bwd  : reverse recurrence over chunks, in place:
 //                         dU_k = g_{k+1};  g_k = dSoff_k + exp(cs_last_k) g_{k+1}
 //                       with g_K = dfinal_state and dinitial_states = g_0
@@ -31,6 +33,7 @@ struct BwdParams {
     float *log_decay;       // [B, H, K] chunk sum of A q (written by k_bwd_dstate)
     float *dstates;         // [B, H, K, P, N]: dSoff, then dU (not used by the
                             // reverse fused chunk kernel)
+    const int32_t *seq_idx; // [B, L] sequence id of every token (packed sequences), or NULL
     const float *dfinal;    // [B, H, P, N] or NULL (zero)
     float *dinit;           // [B, H, P, N] or NULL
     float *part_dA;         // [B, H, K]
@@ -80,8 +83,20 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dstate(BwdParams prm) {
 
     if (w == 0) {
         const float cs = bwd_prologue(prm, b, h, t0, tv, s_q, s_cs, s_dqdu);
-        s_e[lane] = __expf(cs);
-        if (lane == T - 1) prm.log_decay[((int64_t)b * prm.H + h) * prm.K + k] = cs;
+        float e = __expf(cs), ld = cs;
+        if (prm.seq_idx) {
+            // packed sequences: a token reads the entering state only if its id
+            // is that of the token before the chunk (0 before the first); the
+            // state carries over the chunk only if the chunk ends on that id
+            const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + t0;
+            const int sid = si[min(lane, tv - 1)];
+            const int prev = k > 0 ? si[-1] : 0;
+            const int last = __shfl(sid, T - 1, 64);
+            if (sid != prev) e = 0.f;
+            if (last != prev) ld = -INFINITY;
+        }
+        s_e[lane] = e;
+        if (lane == T - 1) prm.log_decay[((int64_t)b * prm.H + h) * prm.K + k] = ld;
     }
     __syncthreads();
 
