@@ -294,13 +294,32 @@ def feature_flags(rt, feats):
             | rt.HAS_INITIAL), feats["dt_limit"][0], feats["dt_limit"][1]
 
 
-def bench_fwd_features(torch, lib, rt, inp, shape, feats, steps, warmup):
-    """Inference forward through the C ABI with the given feature tensors:
-    median ms of `steps` calls (HIP events on the launch stream)."""
+def packed_ids(torch, shape, seed, lo=256, hi=2048):
+    """Packed-sequence ids [B, L] (int32, GPU): every row cut into sequences
+    of U[lo, hi) tokens, the last one shortened to fit."""
+    b, l = shape[0], shape[1]
+    gen = torch.Generator().manual_seed(seed + 2)
+    rows = []
+    for _ in range(b):
+        lengths = []
+        while sum(lengths) < l:
+            lengths.append(int(torch.randint(lo, hi, (1,), generator=gen)))
+        lengths[-1] -= sum(lengths) - l
+        rows.append(torch.cat([torch.full((n,), i, dtype=torch.int32) for i, n in enumerate(lengths)]))
+    return torch.stack(rows).cuda()
+
+
+def bench_fwd_features(torch, lib, rt, inp, shape, feats, steps, warmup, seq=None):
+    """Inference forward through the C ABI with the given feature tensors
+    (and packed-sequence ids `seq`): median ms of `steps` calls (HIP events on
+    the launch stream)."""
     x, dt, A, B, C = (inp[k] for k in ("x", "dt", "A", "B", "C"))
     b, l, h, p, n, chunk, g = shape
     shp = rt.Mamba2SsdShape(b, l, h, p, g, n, chunk)
     flags, lo, hi = feature_flags(rt, feats)
+    if seq is not None:
+        flags |= rt.HAS_SEQ_IDX
+    feats = feats or {"D": None, "z": None, "dt_bias": None, "initial_states": None}
     nb = ctypes.c_size_t(0)
     rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shp), flags, ctypes.byref(nb)), "ws", lib)
     P = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
@@ -310,6 +329,7 @@ def bench_fwd_features(torch, lib, rt, inp, shape, feats, steps, warmup):
     fargs = rt.Mamba2SsdFwdArgs(shp, flags, lo, hi, P(x), P(dt), P(A), P(B), P(C),
                                 P(feats["D"]), P(feats["z"]), P(feats["dt_bias"]),
                                 P(feats["initial_states"]), P(out), P(final), None, None)
+    fargs.seq_idx = P(seq)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for _ in range(warmup):
         rt.check(lib.mamba2_ssd_fwd(ctypes.byref(fargs), P(ws), ws.numel(), stream), "fwd", lib)
@@ -325,11 +345,11 @@ def bench_fwd_features(torch, lib, rt, inp, shape, feats, steps, warmup):
     return statistics.median(samples)
 
 
-def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup, feats=None):
+def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup, feats=None, seq=None):
     """Training forward (saving the chunk-start states) + M1 bwd through the C
     ABI with per-kernel events; upstream gradients of the loss mean(y^2) +
-    mean(final^2).  `feats`: optional full-feature tensors (full_features).
-    None if unsupported."""
+    mean(final^2).  `feats`: optional full-feature tensors (full_features);
+    `seq`: optional packed-sequence ids.  None if unsupported."""
     x, dt, A, B, C = (inp[k] for k in ("x", "dt", "A", "B", "C"))
     b, l, h, p, n, chunk, g = shape
     shp = rt.Mamba2SsdShape(b, l, h, p, g, n, chunk)
@@ -337,6 +357,8 @@ def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup, feats=N
         return None
     flags, lo, hi = feature_flags(rt, feats)
     flags |= rt.SAVED_STATES
+    if seq is not None:
+        flags |= rt.HAS_SEQ_IDX
     fb, bb = ctypes.c_size_t(0), ctypes.c_size_t(0)
     rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shp), flags, ctypes.byref(fb)), "ws", lib)
     rt.check(lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(shp), flags, ctypes.byref(bb)), "ws", lib)
@@ -361,6 +383,8 @@ def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup, feats=N
                                 P(grads["x"]), P(grads["dt"]), P(grads["A"]), P(grads["B"]),
                                 P(grads["C"]), P(fg["D"]), P(fg["z"]), P(fg["dt_bias"]),
                                 P(fg["initial_states"]))
+    fargs.seq_idx = P(seq)
+    bargs.seq_idx = P(seq)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     rt.check(lib.mamba2_ssd_fwd(ctypes.byref(fargs), P(ws), ws.numel(), stream), "fwd", lib)
     torch.mul(out, 2.0 / out.numel(), out=dout)
@@ -894,6 +918,32 @@ def main(argv=None):
             memory = autograd_memory(torch, api, inp, chunk)
             log(f"autograd memory: saved {memory['saved_bytes'] / 2**30:.3f} GiB beyond the inputs, "
                 f"peak {memory['peak_extra_bytes'] / 2**30:.3f} GiB above inputs + upstream grads")
+    packed = None
+    if not args.no_full and shape[3] == 64 and shape[4] in (64, 128):
+        # packed sequences (seq_idx) on the same shape: the cost of the masks
+        seq = packed_ids(torch, shape, seed)
+        nfs = max(10, args.steps // 2)
+        # the same call path without ids, timed back to back with the packed
+        # calls, so the pair shows the masks' cost under the same conditions
+        plain = bench_fwd_features(torch, lib, rt, inp, shape, None, nfs, 3)
+        packed = {"ids": "every row cut into sequences of U[256, 2048) tokens",
+                  "nseqs": int((seq[:, 1:] != seq[:, :-1]).sum().item()) + shape[0],
+                  "fwd_ms": round(bench_fwd_features(torch, lib, rt, inp, shape, None, nfs, 3, seq=seq), 5),
+                  "fwd_ms_without_ids": round(plain, 5)}
+        log(f"packed sequences ({packed['nseqs']}): forward median {packed['fwd_ms']:.4f} ms "
+            f"(same path without ids {plain:.4f} ms)")
+        if not args.no_bwd:
+            tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, nfs, 3, seq=seq)
+            if tr is not None:
+                fres, bres = tr[0], tr[1]
+                packed["fwd_train_ms"] = round(statistics.median(r[0] for r in fres), 5)
+                packed["bwd_ms"] = round(statistics.median(r[0] for r in bres), 5)
+                packed["fwd_bwd_ms"] = round(statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres)), 5)
+                packed["grads_finite"] = bool(tr[3])
+                log(f"packed sequences: training forward {packed['fwd_train_ms']:.4f} ms, bwd "
+                    f"{packed['bwd_ms']:.4f} ms, fwd+bwd {packed['fwd_bwd_ms']:.4f} ms")
+        del seq
+        torch.cuda.empty_cache()
     full = None
     if not args.no_full:
         # the reference's headline feature set on the same shape
@@ -982,6 +1032,7 @@ def main(argv=None):
         "decode_step": decode,
         "autograd_memory": memory,
         "full_features": full,
+        "packed_sequences": packed,
         "op": {
             "flops": flops,
             "bytes": nbytes,

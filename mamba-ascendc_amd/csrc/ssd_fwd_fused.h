@@ -112,6 +112,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     __shared__ __attribute__((aligned(16))) int s_sid[2][TS];
     __shared__ __attribute__((aligned(16))) float s_off[2][TS];
     __shared__ float s_carry[2];
+    __shared__ int s_mixed[2]; // kSeq: the chunk holds more than one id (C.B^T needs the id mask)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const bool producer = wave >= 4;
@@ -205,10 +206,14 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             // rows past the sequence end repeat its last token's id
             const int sid = sidr[sl], e_end = __shfl(sid, T - 1, kWave), e_prev = sprv[sl];
             if (sid != e_end || e_end < 0) dec = 0.f; // not part of the state leaving the chunk
+            const bool mixed = __ballot(sid != e_end) != 0;
             if (w == 0) {
                 s_sid[s][lane] = sid;
                 s_off[s][lane] = sid == e_prev ? 1.f : 0.f;
-                if (lane == 0) s_carry[s] = e_end == e_prev ? 1.f : 0.f;
+                if (lane == 0) {
+                    s_carry[s] = e_end == e_prev ? 1.f : 0.f;
+                    s_mixed[s] = mixed ? 1 : 0;
+                }
             }
         }
         const SplitTile t1 = T1(s), t2 = T2(s), t3 = T3(s);
@@ -379,7 +384,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 c_load(k + 2, slot_c);
                 const SplitTile t1 = T1(s), t4 = T4(s);
                 const float cs_own = s_cs[s][own];
-                const int sid_own = kSeq ? s_sid[s][own] : 0;
+
                 // W^T tiles: C_t . B_s exp2(cs_t - cs_s), s <= t, t = own
                 Frag WT[2];
                 {
@@ -394,9 +399,21 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int so = 16 * j + 4 * kq + i;
-                            const bool live = j <= W && so <= own && (!kSeq || s_sid[s][so] == sid_own);
-                            const float e = live ? exp2_f(cs_own - s_cs[s][so]) * s_q[s][so] : 0.f;
+                            const float e = (j <= W && so <= own) ? exp2_f(cs_own - s_cs[s][so]) * s_q[s][so] : 0.f;
                             wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
+                        }
+                    }
+                    // packed sequences: C_t . B_s only between equal ids, applied
+                    // only to chunks that hold a sequence boundary (wave-uniform)
+                    if (kSeq && s_mixed[s]) {
+                        const int sid_own = s_sid[s][own];
+    #pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int4 sv = *(const int4 *)&s_sid[s][16 * j + 4 * kq];
+                            const int sva[4] = {sv.x, sv.y, sv.z, sv.w};
+    #pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                if (sva[i] != sid_own) wv[j >> 1][(j & 1) * 4 + i] = 0.f;
                         }
                     }
                     WT[0] = pack_frag(wv[0]);
