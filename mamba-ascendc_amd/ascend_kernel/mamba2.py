@@ -512,8 +512,9 @@ def mamba2_ssd_fwd(
     the state at the end of every sequence [nseq,H,P,N], giving ``(out,
     varlen_states)`` or ``(out, final_state, varlen_states)``;
     ``return_final_states`` is that port's name for ``return_final_state``.
-    Both need headdim 64 with dstate 64 or 128; varlen states also a
-    chunk_size that is a multiple of 64.
+    Both need headdim 64 with dstate 64 or 128 (gradients: dstate 64); varlen
+    states also a chunk_size that is a multiple of 64 and are not
+    differentiable.
     """
     register_ops()
     if return_final_states is not None:
