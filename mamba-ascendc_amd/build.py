@@ -7,8 +7,10 @@ hipcc cross-compiles without a GPU, so this runs on CPU-only hosts too.
 from __future__ import annotations
 
 import os
+import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -21,7 +23,6 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # packed fp32 VALU ops stay off (code generation choice for this target)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # MFMA results go to ordinary VGPRs: no v_accvgpr_read/write shuffles
@@ -31,18 +32,52 @@ FLAGS = [
 ]
 
 
+# translation units (source, extra flags): the host code with the small
+# kernels, the fused-forward variants, and the backward variants with and
+# without the z gate; compiled in parallel, then linked into one library
+UNITS = [
+    ("mamba2_ssd.hip", []),
+    ("ssd_fwd_seg.hip", []),
+    ("ssd_bwd_ws.hip", ["-DSSD_BWD_Z=0"]),
+    ("ssd_bwd_ws.hip", ["-DSSD_BWD_Z=1"]),
+]
+
+_NOISE = "is not a recognized feature for this target"
+
+
+def _messages(res) -> str:
+    return "\n".join(l for l in (res.stdout + res.stderr).splitlines() if _NOISE not in l)
+
+
 def build(verbose: bool = False) -> str:
-    src = os.path.join(CSRC, "mamba2_ssd.hip")
-    tmp = OUT + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-o", tmp, src]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    msgs = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{msgs}")
-    if verbose and msgs.strip():
-        print(msgs, file=sys.stderr)
-    os.replace(tmp, OUT)
+    work = tempfile.mkdtemp(prefix="mamba2_ssd_build_")
+    try:
+        jobs, objs = [], []
+        for i, (src, extra) in enumerate(UNITS):
+            obj = os.path.join(work, f"u{i}.o")
+            cmd = [HIPCC, *FLAGS, *extra, "-c", "-o", obj, os.path.join(CSRC, src)]
+            jobs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                               text=True)))
+            objs.append(obj)
+        failed = []
+        for cmd, proc in jobs:
+            out, err = proc.communicate()
+            res = subprocess.CompletedProcess(cmd, proc.returncode, out, err)
+            msgs = _messages(res)
+            if res.returncode != 0:
+                failed.append(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{msgs}")
+            elif verbose and msgs.strip():
+                print(msgs, file=sys.stderr)
+        if failed:
+            raise RuntimeError("\n\n".join(failed))
+        tmp = OUT + ".tmp"
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-fPIC", "-shared", "-o", tmp, *objs]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed ({res.returncode}):\n{' '.join(cmd)}\n{_messages(res)}")
+        os.replace(tmp, OUT)
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
     return OUT
 
 

@@ -17,6 +17,7 @@
 #include "ssd_decode.h"
 #include "ssd_fwd_fused.h"
 #include "ssd_fwd_kernels.h"
+#include "ssd_launch.h"
 #include "ssd_varlen.h"
 
 namespace {
@@ -124,25 +125,6 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags) {
 }
 
 size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags) { return fwd_plan(s, flags).ws; }
-
-// k_fwd_seg full pass for the runtime feature set (save states, z gate, packed sequences)
-template <bool kSave, bool kGate, bool kSeq>
-void launch_seg(dim3 grid, hipStream_t st, const ssd::FwdParams &kp, const ssd::SegParams &sp) {
-    hipLaunchKernelGGL((ssd::k_fwd_seg<false, kSave, kGate, kSeq>), grid, dim3(ssd::kWsThreads), 0,
-                       st, kp, sp);
-}
-
-using SegLaunch = void (*)(dim3, hipStream_t, const ssd::FwdParams &, const ssd::SegParams &);
-
-SegLaunch seg_launcher(bool save, bool gate, bool seq) {
-    static const SegLaunch table[8] = {
-        launch_seg<false, false, false>, launch_seg<false, false, true>,
-        launch_seg<false, true, false>,  launch_seg<false, true, true>,
-        launch_seg<true, false, false>,  launch_seg<true, false, true>,
-        launch_seg<true, true, false>,   launch_seg<true, true, true>,
-    };
-    return table[(save ? 4 : 0) + (gate ? 2 : 0) + (seq ? 1 : 0)];
-}
 
 // Optional per-kernel event trace: events[0] is recorded before the first
 // kernel and events[i + 1] right after kernel i, all on the launch stream.
@@ -319,11 +301,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         if (pl.nseg > 1) {
             sp.seg_state = (float *)((char *)workspace + pl.seg_state);
             sp.seg_log_decay = (float *)((char *)workspace + pl.seg_decay);
-            if (seq)
-                hipLaunchKernelGGL((ssd::k_fwd_seg<true, false, false, true>), dim3(units),
-                                   dim3(ssd::kWsThreads), 0, st, kp, sp);
-            else
-                hipLaunchKernelGGL(ssd::k_fwd_seg<true>, dim3(units), dim3(ssd::kWsThreads), 0, st, kp, sp);
+            ssd::launch_fwd_seg(true, false, false, seq, dim3(units), st, kp, sp);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
             const int PN = (int)(s->headdim * s->dstate);
             const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
@@ -336,7 +314,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
             sp.write_final = 1;
         }
         kp.chunk_states = prm.chunk_states;
-        seg_launcher(kp.chunk_states != nullptr, kp.has_z != 0, seq)(dim3(units), st, kp, sp);
+        ssd::launch_fwd_seg(false, kp.chunk_states != nullptr, kp.has_z != 0, seq, dim3(units), st, kp, sp);
         if (int rc = launch_status(kp.chunk_states ? "k_fwd_seg_save" : "k_fwd_seg", tr, st)) return rc;
         if (pl.nsplit > 1) {
             const int64_t n4 = s->batch * s->seqlen * s->nheads * s->headdim / 4;
@@ -548,25 +526,7 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     const int64_t bg = (int64_t)B * s->ngroups;
     if (bwd_fused_rev(s)) {
         // one pass: reverse chunk order, state gradients carried in registers
-        const dim3 grid((unsigned)bg), block(ssd::kBwsThreads);
-        const int R = bp.R;
-#define SSD_LAUNCH_REV(Z, RR, Q) \
-    hipLaunchKernelGGL((ssd::k_bwd_ws<Z, RR, Q>), grid, block, 0, st, bp, 1, K)
-#define SSD_LAUNCH_REV_R(Z, Q)                \
-    do {                                      \
-        if (R == 1) SSD_LAUNCH_REV(Z, 1, Q);  \
-        else if (R == 2) SSD_LAUNCH_REV(Z, 2, Q); \
-        else SSD_LAUNCH_REV(Z, 4, Q);         \
-    } while (0)
-        if (bp.has_z) {
-            if (seq) SSD_LAUNCH_REV_R(true, true);
-            else SSD_LAUNCH_REV_R(true, false);
-        } else {
-            if (seq) SSD_LAUNCH_REV_R(false, true);
-            else SSD_LAUNCH_REV_R(false, false);
-        }
-#undef SSD_LAUNCH_REV_R
-#undef SSD_LAUNCH_REV
+        ssd::launch_bwd_ws(bp.has_z != 0, bp.R, seq, dim3((unsigned)bg), st, bp, 1, K);
         if (int rc = launch_status("k_bwd_ws_rev", tr, st)) return rc;
         hipLaunchKernelGGL(ssd::k_bwd_finalize_slots, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
                            bp.part_dbias, bp.part_dD, a->dA, a->ddt_bias, a->dD, B, H, K, 64,
@@ -576,22 +536,8 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     }
     // state gradients dU_k (and dinitial_states)
     if ((int64_t)B * H >= kMinRevStreams) {
-        const dim3 rgrid((unsigned)(B * H)), rblock(ssd::kWsThreads);
-        if (bp.has_z) {
-            if (seq)
-                hipLaunchKernelGGL((ssd::k_bwd_dstate_rev<true, true>), rgrid, rblock, 0, st, bp,
+        ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, dim3((unsigned)(B * H)), st, bp,
                                    a->dfinal_state, a->dinitial_states);
-            else
-                hipLaunchKernelGGL((ssd::k_bwd_dstate_rev<true, false>), rgrid, rblock, 0, st, bp,
-                                   a->dfinal_state, a->dinitial_states);
-        } else {
-            if (seq)
-                hipLaunchKernelGGL((ssd::k_bwd_dstate_rev<false, true>), rgrid, rblock, 0, st, bp,
-                                   a->dfinal_state, a->dinitial_states);
-            else
-                hipLaunchKernelGGL((ssd::k_bwd_dstate_rev<false, false>), rgrid, rblock, 0, st, bp,
-                                   a->dfinal_state, a->dinitial_states);
-        }
         if (int rc = launch_status("k_bwd_dstate_rev", tr, st)) return rc;
     } else {
         hipLaunchKernelGGL(ssd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);
@@ -605,18 +551,7 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     nseg = nseg < K ? nseg : K;
     const int M = (int)((K + nseg - 1) / nseg);
     nseg = (K + M - 1) / M;
-    const dim3 wgrid((unsigned)(bg * nseg)), wblock(ssd::kBwsThreads);
-    if (bp.has_z) {
-        if (seq)
-            hipLaunchKernelGGL((ssd::k_bwd_ws<true, 0, true>), wgrid, wblock, 0, st, bp, (int)nseg, M);
-        else
-            hipLaunchKernelGGL((ssd::k_bwd_ws<true, 0, false>), wgrid, wblock, 0, st, bp, (int)nseg, M);
-    } else {
-        if (seq)
-            hipLaunchKernelGGL((ssd::k_bwd_ws<false, 0, true>), wgrid, wblock, 0, st, bp, (int)nseg, M);
-        else
-            hipLaunchKernelGGL((ssd::k_bwd_ws<false, 0, false>), wgrid, wblock, 0, st, bp, (int)nseg, M);
-    }
+    ssd::launch_bwd_ws(bp.has_z != 0, 0, seq, dim3((unsigned)(bg * nseg)), st, bp, (int)nseg, M);
     if (int rc = launch_status("k_bwd_ws", tr, st)) return rc;
     hipLaunchKernelGGL(ssd::k_bwd_finalize_slots, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
                        bp.part_dbias, bp.part_dD, a->dA, a->ddt_bias, a->dD, B, H, K, 64,

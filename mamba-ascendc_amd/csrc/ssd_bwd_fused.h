@@ -917,6 +917,7 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
 // fixed-order reductions of the per-chunk partials, one workgroup per head:
 // dA from [B, H, K], ddt_bias and dD from [B, H, K, slots] (dD per channel:
 // [B, H, K, slots, P])
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(kThreads) void k_bwd_finalize_slots(
     const float *part_dA, const float *part_dbias, const float *part_dD, float *dA, float *ddt_bias,
     float *dD, int B, int H, int K, int P, int slots, int has_D, int d_per_channel) {
@@ -956,5 +957,6 @@ __global__ __launch_bounds__(kThreads) void k_bwd_finalize_slots(
         }
     }
 }
+#endif
 
 }  // namespace ssd

@@ -68,6 +68,7 @@ __device__ __forceinline__ float bwd_prologue(const BwdParams &p, int b, int h, 
 // --------------------------------------------------------------------------
 // dSoff_k = (gy * exp(cs))^T C, one workgroup per (k, h, b)
 // --------------------------------------------------------------------------
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(kThreads) void k_bwd_dstate(BwdParams prm) {
     constexpr int P = 64, N = 64, T = 64;
     __shared__ float s_q[T], s_cs[T], s_dqdu[T], s_e[T];
@@ -131,10 +132,12 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dstate(BwdParams prm) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) out[(16 * w + 4 * kq + r) * N + 16 * nb + r16] = acc[nb][r];
 }
+#endif
 
 // --------------------------------------------------------------------------
 // reverse state passing (elementwise over P*N, serial over chunks, in place)
 // --------------------------------------------------------------------------
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(kThreads) void k_state_pass_bwd(float *ds, const float *log_decay,
                                                              const float *dfinal, float *dinit,
                                                              int K, int PN) {
@@ -169,6 +172,7 @@ __global__ __launch_bounds__(kThreads) void k_state_pass_bwd(float *ds, const fl
     }
     if (dinit) *(float4 *)(dinit + bh * PN + idx) = g;
 }
+#endif
 
 // --------------------------------------------------------------------------
 // workgroup sum (256 threads) in a fixed order

@@ -36,6 +36,7 @@ struct SsuParams {
     int softplus, has_D, d_per_channel, has_z;
 };
 
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(256) void k_ssu(SsuParams prm) {
     const int bh = blockIdx.y, b = bh / prm.H, h = bh % prm.H;
     const int tid = threadIdx.x, lpr = prm.lpr;
@@ -99,5 +100,6 @@ __global__ __launch_bounds__(256) void k_ssu(SsuParams prm) {
         }
     }
 }
+#endif
 
 }  // namespace ssd

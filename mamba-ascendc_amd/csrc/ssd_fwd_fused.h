@@ -533,6 +533,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
 
 // nsplit = 2 epilogue, elementwise over [B, L, H, P] in float4s: out holds
 // y_a, y_half y_b; out = (y_a + y_b + D x) (* silu z), pre_gate = y + D x.
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(kThreads) void k_fwd_combine(FwdParams prm, const float *y_half,
                                                           int64_t n4) {
     constexpr int P = 64;
@@ -562,5 +563,6 @@ __global__ __launch_bounds__(kThreads) void k_fwd_combine(FwdParams prm, const f
         *(float4 *)(prm.out + e) = v;
     }
 }
+#endif
 
 }  // namespace ssd

@@ -157,6 +157,7 @@ __global__ __launch_bounds__(kThreads) void k_chunk_state(FwdParams prm) {
 constexpr int kStateDepth = 8;  // batch prefetch of k_state_pass_bwd
 constexpr int kStateRing = 16;  // chunks in flight per thread in k_state_pass
 
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_states,
                                                          const float *log_decay,
                                                          const float *init, float *states_start,
@@ -218,10 +219,12 @@ __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_stat
     }
     if (final_state) *(float4 *)(final_state + bh * PN + idx) = s;
 }
+#endif
 
 // --------------------------------------------------------------------------
 // generic token recurrence (any headdim / dstate <= 256); one wave per (b,h,p)
 // --------------------------------------------------------------------------
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(64) void k_generic_fwd(FwdParams prm, int P, int N) {
     const int pc = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x;
@@ -268,5 +271,6 @@ __global__ __launch_bounds__(64) void k_generic_fwd(FwdParams prm, int P, int N)
         }
     }
 }
+#endif
 
 }  // namespace ssd

@@ -1,0 +1,35 @@
+// Variants of the fused forward k_fwd_seg and their launcher (declared in
+// ssd_launch.h); the library's host code is in mamba2_ssd.hip.
+#define SSD_KERNEL_TEMPLATES_ONLY
+#include "ssd_fwd_fused.h"
+#include "ssd_launch.h"
+
+namespace ssd {
+namespace {
+
+template <bool kStateOnly, bool kSave, bool kGate, bool kSeq>
+void run(dim3 grid, hipStream_t st, const FwdParams &kp, const SegParams &sp) {
+    hipLaunchKernelGGL((k_fwd_seg<kStateOnly, kSave, kGate, kSeq>), grid, dim3(kWsThreads), 0, st,
+                       kp, sp);
+}
+
+using Run = void (*)(dim3, hipStream_t, const FwdParams &, const SegParams &);
+
+}  // namespace
+
+void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
+                    const FwdParams &kp, const SegParams &sp) {
+    if (state_only) {
+        (seq ? run<true, false, false, true> : run<true, false, false, false>)(grid, st, kp, sp);
+        return;
+    }
+    static const Run full[8] = {
+        run<false, false, false, false>, run<false, false, false, true>,
+        run<false, false, true, false>,  run<false, false, true, true>,
+        run<false, true, false, false>,  run<false, true, false, true>,
+        run<false, true, true, false>,   run<false, true, true, true>,
+    };
+    full[(save ? 4 : 0) + (gate ? 2 : 0) + (seq ? 1 : 0)](grid, st, kp, sp);
+}
+
+}  // namespace ssd

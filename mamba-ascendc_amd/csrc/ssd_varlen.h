@@ -24,6 +24,7 @@ namespace ssd {
 
 constexpr int kVarlenThreads = 256;
 
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(kVarlenThreads) void k_varlen_states(FwdParams prm, const int32_t *cu,
                                                                    const float *chunk_states,
                                                                    float *out, int CS, int P,
@@ -101,5 +102,6 @@ __global__ __launch_bounds__(kVarlenThreads) void k_varlen_states(FwdParams prm,
         }
     }
 }
+#endif
 
 }  // namespace ssd
