@@ -64,6 +64,9 @@ template <bool kHasZ, int kRevR = 0, bool kSeq = false>
 __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg, int M) {
     static_assert(kRevR == 0 || kRevR == 1 || kRevR == 2 || kRevR == 4, "heads per group");
     constexpr bool kRev = kRevR > 0;
+    // reverse pass with the z gate: z and pre_gate are loaded after the first
+    // barrier of a step instead of half a step ahead (register pressure)
+    constexpr bool kLateZ = kHasZ && kRev;
     constexpr int T = 64, P = 64, N = 64;
     constexpr int TS = kSeq ? T : 1;
     // x and gy tiles double buffered by step parity (the epilogue of step n
@@ -113,24 +116,33 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         int sidr = 0, sprv = 0; // kSeq: id of token `lane`, id of the token before the chunk
         const float *dtb = prm.dt_bias ? prm.dt_bias : prm.A; // read unconditionally
         const float *Dp = prm.has_D ? prm.D : prm.A;
+        // z and pre_gate of step n (the z gate)
+        auto load_zp = [&](int n) __attribute__((always_inline)) {
+            n = min(n, NS - 1);
+            const int k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
+            const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
+            const auto rz = buf_rsrc(prm.z + xo);
+            const auto rp = buf_rsrc(prm.pre_gate + xo);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int lo = min(rt + 16 * j, tv - 1) * rowHP4 + c4 * 4;
+                zr[j] = buf_load4(rz, lo, 0);
+                pr[j] = buf_load4(rp, lo, 0);
+            }
+        };
         auto load_xg = [&](int n) __attribute__((always_inline)) {
             n = min(n, NS - 1);
             const int k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
             const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
             const auto rx = buf_rsrc(prm.x + xo);
             const auto rd = buf_rsrc(has_dout ? prm.dout + xo : prm.x + xo);
-            const auto rz = buf_rsrc(kHasZ ? prm.z + xo : prm.x + xo);
-            const auto rp = buf_rsrc(kHasZ ? prm.pre_gate + xo : prm.x + xo);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int lo = min(rt + 16 * j, tv - 1) * rowHP4 + c4 * 4;
                 xr[j] = buf_load4(rx, lo, 0);
                 gr[j] = buf_load4(rd, lo, 0);
-                if (kHasZ) {
-                    zr[j] = buf_load4(rz, lo, 0);
-                    pr[j] = buf_load4(rp, lo, 0);
-                }
             }
+            if (kHasZ && !kLateZ) load_zp(n);
             dtr = prm.dt[((int64_t)b * prm.L + (int64_t)k * T + min(lane, tv - 1)) * H + h];
             if (kSeq) {
                 const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + (int64_t)k * T;
@@ -278,7 +290,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             }
         };
         auto stage_bc = [&](int n) __attribute__((always_inline)) {
-            const int tv = tvalid(chunk_of(n));
+            const int tv = tvalid(chunk_of(min(n, NS - 1)));
             _Float16 *lp = opaque_lds(lds);
             const SplitTile bt = tile_at(lp, 6), ct = tile_at(lp, 7);
 #pragma unroll
@@ -355,6 +367,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         };
 
         load_xg(0);
+        if (kLateZ) load_zp(0);
         load_bc(0);
         load_su(0);
         stage_xg(0);
@@ -390,9 +403,20 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 load_xg(n + 1);
                 if constexpr ((pos + 1) % kRevR == 0) load_bc(n + 1);
                 lds_barrier();
-                if (n + 1 < NS) {
-                    stage_xg(n + 1);
+                if constexpr (kLateZ) {
+                    // the z gate: B, C staged first and z, pre_gate loaded only
+                    // now (covered by the consumers' phase B), so their
+                    // registers are not live beside the carries and the
+                    // other step's loads; both unconditional (past the end
+                    // they only restage tiles no consumer reads)
                     if constexpr ((pos + 1) % kRevR == 0) stage_bc(n + 1);
+                    load_zp(n + 1);
+                    if (n + 1 < NS) stage_xg(n + 1);
+                } else {
+                    if (n + 1 < NS) {
+                        stage_xg(n + 1);
+                        if constexpr ((pos + 1) % kRevR == 0) stage_bc(n + 1);
+                    }
                 }
                 lds_barrier();
             };
