@@ -128,6 +128,10 @@ def fwd_kernel_model(name: str, shape) -> dict:
     r = h // g
     units = b * h * k
     f4 = 4
+    if name.endswith("_seq"):
+        # packed sequences: the same tensors plus the [B, L] ids, shared by
+        # every head (a few bytes per unit, not counted)
+        name = name[: -len("_seq")]
     if name == "k_chunk_state":
         per = f4 * (T * p + T + T * n / r + p * n + 1)
         fl = 2 * T * p * n
@@ -681,23 +685,26 @@ def _short(name: str) -> str:
 def model_key(short: str) -> str:
     """Kernel-model / trace name of a (templated) kernel.
 
-    k_fwd_seg<state only, save states, z gate>: <true, ...> is k_fwd_seg_state,
-    <false, true, ...> k_fwd_seg_save, <false, false, ...> k_fwd_seg, with a
-    "_gate" suffix for the z-gated form.  k_bwd_ws<has z, heads per group>:
-    a group size above 0 is the reverse fused k_bwd_ws_rev ("_z" with z).
-    The others drop their template arguments."""
+    k_fwd_seg<state only, save states, z gate, packed sequences>: <true, ...>
+    is k_fwd_seg_state, <false, true, ...> k_fwd_seg_save, <false, false, ...>
+    k_fwd_seg, with a "_gate" suffix for the z-gated form and "_seq" for
+    packed sequences.  k_bwd_ws<has z, heads per group, packed sequences>: a
+    group size above 0 is the reverse fused k_bwd_ws_rev ("_z" with z, "_seq"
+    with packed sequences).  The others drop their template arguments."""
     if short.startswith("k_fwd_seg<"):
         args = [a.strip() for a in short[len("k_fwd_seg<"):-1].split(",")]
+        seq = "_seq" if len(args) > 3 and args[3] == "true" else ""
         if args[0] == "true":
-            return "k_fwd_seg_state"
+            return "k_fwd_seg_state" + seq
         key = "k_fwd_seg_save" if len(args) > 1 and args[1] == "true" else "k_fwd_seg"
-        return key + "_gate" if len(args) > 2 and args[2] == "true" else key
+        return (key + "_gate" if len(args) > 2 and args[2] == "true" else key) + seq
     base = short.split("<")[0]
     if base == "k_bwd_ws":
         args = [a.strip() for a in short[len("k_bwd_ws<"):-1].split(",")]
+        seq = "_seq" if len(args) > 2 and args[2] == "true" else ""
         if len(args) > 1 and args[1] != "0":
-            return "k_bwd_ws_rev_z" if args[0] == "true" else "k_bwd_ws_rev"
-        return "k_bwd_ws"
+            return ("k_bwd_ws_rev_z" if args[0] == "true" else "k_bwd_ws_rev") + seq
+        return "k_bwd_ws" + seq
     return base if base == "k_bwd_dstate_rev" else short
 
 
