@@ -185,11 +185,28 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
 /* dt [B, H], A [H], dt_bias [H] (the tied head-dim case, Mamba-2 decoding);
  * without it dt [B, H, P], A [H, P, N], dt_bias [H, P] */
 #define MAMBA2_SSU_TIED (1u << 16)
+/* the element strides in Mamba2SsuArgs.strides are set (else every input has the
+ * contiguous layout of its shape) */
+#define MAMBA2_SSU_STRIDES (1u << 17)
+
+/* Element strides of the decode inputs (MAMBA2_SSU_STRIDES); any may be 0 (a
+ * broadcast).  The innermost dimension of x, z (over P) and of B, C (over N) is
+ * contiguous; B and C rows stay 16-byte aligned. */
+typedef struct Mamba2SsuStrides {
+    int64_t x_b, x_h;            /* x [B, H, P] */
+    int64_t z_b, z_h;            /* z [B, H, P] */
+    int64_t bc_b, bc_g;          /* B and C [B, G, N] (the same strides for both) */
+    int64_t dt_b, dt_h, dt_p;    /* dt [B, H] (TIED: dt_p unused) or [B, H, P] */
+    int64_t A_h, A_p, A_n;       /* A [H] (TIED: A_p, A_n unused) or [H, P, N] */
+    int64_t bias_h, bias_p;      /* dt_bias [H] (TIED) or [H, P] */
+    int64_t D_h, D_p;            /* D [H] or [H, P] (D_PER_CHANNEL) */
+} Mamba2SsuStrides;
 
 typedef struct Mamba2SsuArgs {
     int64_t batch, nheads, headdim, dstate, ngroups;
-    uint32_t flags;     /* MAMBA2_SSU_TIED, MAMBA2_SSD_DT_SOFTPLUS, _HAS_D,
-                           _D_PER_CHANNEL (D [H, P], else [H]), _HAS_Z, _HAS_DT_BIAS */
+    uint32_t flags;     /* MAMBA2_SSU_TIED, MAMBA2_SSU_STRIDES, MAMBA2_SSD_DT_SOFTPLUS,
+                           _HAS_D, _D_PER_CHANNEL (D [H, P], else [H]), _HAS_Z,
+                           _HAS_DT_BIAS */
     float *state;       /* slots of [H, P, N] (contiguous within a slot), updated in place */
     int64_t state_slots;       /* number of slots (state batch) */
     int64_t state_slot_stride; /* floats between consecutive slots (>= H * P * N) */
@@ -204,12 +221,13 @@ typedef struct Mamba2SsuArgs {
     const float *z;     /* [B, H, P] or NULL */
     const float *dt_bias; /* [H] (TIED) or [H, P], or NULL */
     float *out;         /* [B, H, P] */
+    Mamba2SsuStrides strides; /* read iff MAMBA2_SSU_STRIDES (member added in ABI 4) */
 } Mamba2SsuArgs;
 
 /* One decode step: for each sequence b and head h, S = exp(A q) S + q x B^T
  * on its state slot and out = S C (+ D x) (* silu z), q = softplus?(dt + dt_bias).
- * dstate must be a multiple of 4 and at most 256; every pointer 16-byte aligned.
- * No workspace; enqueued on `stream`. */
+ * dstate must be a multiple of 4 and at most 256; state, B, C (and an untied A)
+ * 16-byte aligned.  No workspace; enqueued on `stream`. */
 int mamba2_selective_state_update(const Mamba2SsuArgs *args, void *stream);
 
 /* Thread-local message of the last failing call on this thread ("" if none). */

@@ -29,6 +29,7 @@ SAVED_STATES = 1 << 6
 HAS_SEQ_IDX = 1 << 7
 VARLEN_STATES = 1 << 8
 SSU_TIED = 1 << 16
+SSU_STRIDES = 1 << 17
 
 STATUS_NAMES = {
     0: "OK",
@@ -87,6 +88,12 @@ class Mamba2SsdBwdArgs(ctypes.Structure):
     ]
 
 
+class Mamba2SsuStrides(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in
+                ("x_b", "x_h", "z_b", "z_h", "bc_b", "bc_g", "dt_b", "dt_h", "dt_p",
+                 "A_h", "A_p", "A_n", "bias_h", "bias_p", "D_h", "D_p")]
+
+
 class Mamba2SsuArgs(ctypes.Structure):
     _fields_ = [
         ("batch", ctypes.c_int64), ("nheads", ctypes.c_int64), ("headdim", ctypes.c_int64),
@@ -97,6 +104,7 @@ class Mamba2SsuArgs(ctypes.Structure):
         ("x", _c_fp), ("dt", _c_fp), ("A", _c_fp), ("B", _c_fp), ("C", _c_fp),
         ("D", _c_fp), ("z", _c_fp), ("dt_bias", _c_fp),
         ("out", _c_fp),
+        ("strides", Mamba2SsuStrides),
     ]
 
 

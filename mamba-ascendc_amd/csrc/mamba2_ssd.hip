@@ -607,8 +607,9 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
 
 int mamba2_selective_state_update(const Mamba2SsuArgs *a, void *stream) {
     if (!a) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "args is NULL");
-    constexpr uint32_t kKnown = MAMBA2_SSU_TIED | MAMBA2_SSD_DT_SOFTPLUS | MAMBA2_SSD_HAS_D |
-                                MAMBA2_SSD_D_PER_CHANNEL | MAMBA2_SSD_HAS_Z | MAMBA2_SSD_HAS_DT_BIAS;
+    constexpr uint32_t kKnown = MAMBA2_SSU_TIED | MAMBA2_SSU_STRIDES | MAMBA2_SSD_DT_SOFTPLUS |
+                                MAMBA2_SSD_HAS_D | MAMBA2_SSD_D_PER_CHANNEL | MAMBA2_SSD_HAS_Z |
+                                MAMBA2_SSD_HAS_DT_BIAS;
     const uint32_t f = a->flags;
     if (f & ~kKnown) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "unknown flag bits 0x%x", f & ~kKnown);
     if (a->batch <= 0 || a->nheads <= 0 || a->headdim <= 0 || a->dstate <= 0 || a->ngroups <= 0)
@@ -667,6 +668,35 @@ int mamba2_selective_state_update(const Mamba2SsuArgs *a, void *stream) {
     prm.has_D = (f & MAMBA2_SSD_HAS_D) != 0;
     prm.d_per_channel = (f & MAMBA2_SSD_D_PER_CHANNEL) != 0;
     prm.has_z = (f & MAMBA2_SSD_HAS_Z) != 0;
+    const int64_t H = a->nheads, P = a->headdim, N = a->dstate, G = a->ngroups;
+    if (f & MAMBA2_SSU_STRIDES) {
+        const Mamba2SsuStrides &st = a->strides;
+        prm.x_b = st.x_b, prm.x_h = st.x_h, prm.z_b = st.z_b, prm.z_h = st.z_h;
+        prm.bc_b = st.bc_b, prm.bc_g = st.bc_g;
+        prm.dt_b = st.dt_b, prm.dt_h = st.dt_h, prm.dt_p = st.dt_p;
+        prm.A_h = st.A_h, prm.A_p = st.A_p, prm.A_n = st.A_n;
+        prm.bias_h = st.bias_h, prm.bias_p = st.bias_p, prm.D_h = st.D_h, prm.D_p = st.D_p;
+    } else {
+        // the contiguous layouts of the shapes
+        prm.x_b = prm.z_b = H * P, prm.x_h = prm.z_h = P;
+        prm.bc_b = G * N, prm.bc_g = N;
+        if (prm.tied) {
+            prm.dt_b = H, prm.dt_h = 1, prm.dt_p = 0;
+            prm.A_h = 1, prm.A_p = 0, prm.A_n = 0;
+            prm.bias_h = 1, prm.bias_p = 0;
+        } else {
+            prm.dt_b = H * P, prm.dt_h = P, prm.dt_p = 1;
+            prm.A_h = P * N, prm.A_p = N, prm.A_n = 1;
+            prm.bias_h = P, prm.bias_p = 1;
+        }
+        prm.D_h = prm.d_per_channel ? P : 1, prm.D_p = prm.d_per_channel ? 1 : 0;
+    }
+    // the 16-byte loads of B, C rows and of a contiguous untied A row
+    if (prm.bc_b % 4 || prm.bc_g % 4)
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "B and C strides must be multiples of 4 elements");
+    if (!prm.tied && prm.A_n == 1 && (prm.A_h % 4 || prm.A_p % 4))
+        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                    "an untied A with unit dstate stride needs head and dim strides that are multiples of 4");
     // one workgroup per (b, h) walks all rows; with few (b, h) pairs the rows
     // are split over up to 8 workgroups so the grid still has ~2k of them
     const int rows = 256 / lpr;

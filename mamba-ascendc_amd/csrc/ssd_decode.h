@@ -34,6 +34,9 @@ struct SsuParams {
     int lpr;                   // lanes per state row: N / 4 rounded up to a power of two
     int tied;                  // dt [B, H], A [H], dt_bias [H]; else [B, H, P], [H, P, N], [H, P]
     int softplus, has_D, d_per_channel, has_z;
+    // element strides (broadcast dimensions have stride 0)
+    int64_t x_b, x_h, z_b, z_h, bc_b, bc_g, dt_b, dt_h, dt_p, A_h, A_p, A_n, bias_h, bias_p,
+        D_h, D_p;
 };
 
 #ifndef SSD_KERNEL_TEMPLATES_ONLY
@@ -48,55 +51,76 @@ __global__ __launch_bounds__(256) void k_ssu(SsuParams prm) {
     // per (b, h): the group's B and C columns of this lane, the head's scalars
     float4 bv = make_float4(0.f, 0.f, 0.f, 0.f), cv = bv;
     if (cols && !pad) {
-        const int64_t bo = ((int64_t)b * prm.G + h / prm.R) * prm.N + n0;
+        const int64_t bo = b * prm.bc_b + (h / prm.R) * prm.bc_g + n0;
         bv = *(const float4 *)(prm.B + bo);
         cv = *(const float4 *)(prm.C + bo);
     }
-    const float dt_h = prm.tied ? prm.dt[(int64_t)b * prm.H + h] : 0.f;
-    const float bias_h = prm.tied && prm.dt_bias ? prm.dt_bias[h] : 0.f;
-    const float A_h = prm.tied ? prm.A[h] : 0.f;
-    // workgroup x covers rows x * rows + i * gridDim.x * rows
-    for (int p0 = blockIdx.x * rows; p0 < prm.P; p0 += gridDim.x * rows) {
-        const int p = p0 + tid / lpr;
-        const bool active = p < prm.P;                // whole rows are in or out
-        const int64_t xo = ((int64_t)b * prm.H + h) * prm.P + p;
-        if (pad) {
-            // no state update, zero output (one lane per row)
-            if (active && n0 == 0) prm.out[xo] = 0.f;
-            continue;
-        }
-        float q = 0.f, x = 0.f;
-        if (active) {
-            x = prm.x[xo];
-            const float u = prm.tied ? dt_h + bias_h
-                                     : prm.dt[xo] + (prm.dt_bias ? prm.dt_bias[h * prm.P + p] : 0.f);
-            q = prm.softplus ? softplus_f(u) : u;
-        }
-        float part = 0.f;
-        if (active && cols) {
-            float *sp = prm.state + slot * prm.state_bstride + ((int64_t)h * prm.P + p) * prm.N + n0;
-            const float4 s = *(const float4 *)sp;
-            float4 dA;
-            if (prm.tied) {
-                const float a = __expf(A_h * q);
-                dA = make_float4(a, a, a, a);
-            } else {
-                const float4 av = *(const float4 *)(prm.A + ((int64_t)h * prm.P + p) * prm.N + n0);
-                dA = make_float4(__expf(av.x * q), __expf(av.y * q), __expf(av.z * q), __expf(av.w * q));
+    const float dt_h = prm.tied ? prm.dt[b * prm.dt_b + h * prm.dt_h] : 0.f;
+    const float bias_h = prm.tied && prm.dt_bias ? prm.dt_bias[h * prm.bias_h] : 0.f;
+    const float A_h = prm.tied ? prm.A[h * prm.A_h] : 0.f;
+    // workgroup x covers rows x * rows + i * gridDim.x * rows, kBatch passes
+    // at a time: every state, x and dt load of the batch is issued before the
+    // math, so each thread keeps kBatch rows in flight
+    constexpr int kBatch = 4;
+    const int stride = gridDim.x * rows;
+    for (int p0 = blockIdx.x * rows; p0 < prm.P; p0 += kBatch * stride) {
+        float4 sv[kBatch];
+        float xv[kBatch], uv[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int p = p0 + i * stride + tid / lpr;
+            sv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[i] = uv[i] = 0.f;
+            if (p < prm.P && !pad) {
+                xv[i] = prm.x[b * prm.x_b + h * prm.x_h + p];
+                uv[i] = prm.tied ? dt_h + bias_h
+                                 : prm.dt[b * prm.dt_b + h * prm.dt_h + p * prm.dt_p] +
+                                       (prm.dt_bias ? prm.dt_bias[h * prm.bias_h + p * prm.bias_p] : 0.f);
+                if (cols)
+                    sv[i] = *(const float4 *)(prm.state + slot * prm.state_bstride +
+                                              ((int64_t)h * prm.P + p) * prm.N + n0);
             }
-            const float qx = q * x;
-            const float4 ns = make_float4(s.x * dA.x + qx * bv.x, s.y * dA.y + qx * bv.y,
-                                          s.z * dA.z + qx * bv.z, s.w * dA.w + qx * bv.w);
-            *(float4 *)sp = ns;
-            part = ns.x * cv.x + ns.y * cv.y + ns.z * cv.z + ns.w * cv.w;
         }
-        // sum over the lpr lanes of the row (aligned groups of a power of two)
-        for (int o = lpr >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-        if (active && n0 == 0) {
-            float y = part;
-            if (prm.has_D) y += x * prm.D[prm.d_per_channel ? h * prm.P + p : h];
-            if (prm.has_z) y *= silu_f(prm.z[xo]);
-            prm.out[xo] = y;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int p = p0 + i * stride + tid / lpr;
+            const bool active = p < prm.P;            // whole rows are in or out
+            const int64_t xo = ((int64_t)b * prm.H + h) * prm.P + p; // out is contiguous
+            if (pad) {
+                // no state update, zero output (one lane per row)
+                if (active && n0 == 0) prm.out[xo] = 0.f;
+                continue;
+            }
+            const float q = active ? (prm.softplus ? softplus_f(uv[i]) : uv[i]) : 0.f;
+            const float x = xv[i];
+            float part = 0.f;
+            if (active && cols) {
+                float *sp = prm.state + slot * prm.state_bstride + ((int64_t)h * prm.P + p) * prm.N + n0;
+                const float4 s4 = sv[i];
+                float4 dA;
+                if (prm.tied) {
+                    const float a = __expf(A_h * q);
+                    dA = make_float4(a, a, a, a);
+                } else {
+                    const float *ap = prm.A + h * prm.A_h + p * prm.A_p + n0 * prm.A_n;
+                    const float4 av = prm.A_n == 1 ? *(const float4 *)ap
+                                                   : make_float4(ap[0], ap[prm.A_n], ap[2 * prm.A_n], ap[3 * prm.A_n]);
+                    dA = make_float4(__expf(av.x * q), __expf(av.y * q), __expf(av.z * q), __expf(av.w * q));
+                }
+                const float qx = q * x;
+                const float4 ns = make_float4(s4.x * dA.x + qx * bv.x, s4.y * dA.y + qx * bv.y,
+                                              s4.z * dA.z + qx * bv.z, s4.w * dA.w + qx * bv.w);
+                *(float4 *)sp = ns;
+                part = ns.x * cv.x + ns.y * cv.y + ns.z * cv.z + ns.w * cv.w;
+            }
+            // sum over the lpr lanes of the row (aligned groups of a power of two)
+            for (int o = lpr >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+            if (active && n0 == 0) {
+                float y = part;
+                if (prm.has_D) y += x * prm.D[h * prm.D_h + (prm.d_per_channel ? p * prm.D_p : 0)];
+                if (prm.has_z) y *= silu_f(prm.z[b * prm.z_b + h * prm.z_h + p]);
+                prm.out[xo] = y;
+            }
         }
     }
 }

@@ -211,6 +211,16 @@ def test_decode_step_rejects_bad_arguments():
     assert lib.mamba2_selective_state_update(ctypes.byref(args(state_slots=1)), None) == -1
     # misaligned state
     assert lib.mamba2_selective_state_update(ctypes.byref(args(state=ctypes.c_void_p(0x1004))), None) == -1
+    # explicit strides: B / C rows must stay 16-byte aligned
+    bad = args(flags=rt.SSU_TIED | rt.SSU_STRIDES)
+    bad.strides.bc_b, bad.strides.bc_g = 6, 128
+    assert lib.mamba2_selective_state_update(ctypes.byref(bad), None) == -1
+    assert "multiples of 4" in rt.last_error(lib)
+    # an untied A read by rows of four needs head / dim strides that keep them aligned
+    bad = args(flags=rt.SSU_STRIDES)
+    bad.strides.bc_b, bad.strides.bc_g = 256, 128
+    bad.strides.A_h, bad.strides.A_p, bad.strides.A_n = 64 * 130, 130, 1
+    assert lib.mamba2_selective_state_update(ctypes.byref(bad), None) == -1
 
 
 def test_decode_step_python_shape_errors():

@@ -152,3 +152,79 @@ def test_decode_loop_equals_chunked_forward():
     sa, sl = parity_metrics(state.cpu(), want_final.cpu())
     _say(f"decode loop vs chunked forward: out relL2 {rl:.3e}, final relL2 {sl:.3e}")
     assert rl <= 5e-5 and sl <= 5e-5, (rl, sl)
+
+
+def test_decode_strided_views_match_contiguous():
+    """Serving-style inputs: x, B, C views into one projection output (batch
+    stride = its width), z a slice of another, dt / A / D / dt_bias broadcast
+    with stride 0.  The kernel reads them in place; the result equals the call
+    on contiguous copies and the oracle."""
+    _need_gpu()
+    from ascend_kernel import selective_state_update
+
+    b, h, p, n, g = 6, 8, 64, 128, 2
+    gen = torch.Generator().manual_seed(21)
+    width = h * p + 2 * g * n + 12                       # an extra 12 columns (e.g. dt)
+    xbc = torch.randn(b, width, generator=gen).cuda()
+    zx = torch.randn(b, 2 * h * p, generator=gen).cuda()
+    x = xbc[:, : h * p].view(b, h, p)
+    Bm = xbc[:, h * p: h * p + g * n].view(b, g, n)
+    Cm = xbc[:, h * p + g * n: h * p + 2 * g * n].view(b, g, n)
+    z = zx[:, h * p:].view(b, h, p)
+    dt_h = torch.rand(b, h, generator=gen).cuda()
+    A_h = -torch.rand(h, generator=gen).cuda()
+    D_h = torch.randn(h, generator=gen).cuda()
+    bias_h = (torch.randn(h, generator=gen) * 0.1).cuda()
+    dt = dt_h[..., None].expand(b, h, p)
+    A = A_h[:, None, None].expand(h, p, n)
+    D = D_h[:, None].expand(h, p)
+    bias = bias_h[:, None].expand(h, p)
+    state0 = torch.randn(b, h, p, n, generator=gen).cuda()
+    assert x.stride(0) == width and Bm.stride(0) == width and dt.stride(-1) == 0
+
+    s1, s2 = state0.clone(), state0.clone()
+    got = selective_state_update(s1, x, dt, A, Bm, Cm, D=D, z=z, dt_bias=bias, dt_softplus=True)
+    want = selective_state_update(s2, x.contiguous(), dt.contiguous(), A.contiguous(), Bm.contiguous(),
+                                  Cm.contiguous(), D=D.contiguous(), z=z.contiguous(),
+                                  dt_bias=bias.contiguous(), dt_softplus=True)
+    torch.cuda.synchronize()
+    assert torch.allclose(got, want, rtol=1e-6, atol=1e-6)
+    assert torch.allclose(s1, s2, rtol=1e-6, atol=1e-6)
+    ref_state = state0.double().cpu()
+    ref = selective_state_update_ref(ref_state, x.double().cpu(), dt.double().cpu(), A.double().cpu(),
+                                     Bm.double().cpu(), Cm.double().cpu(), D=D.double().cpu(),
+                                     z=z.double().cpu(), dt_bias=bias.double().cpu(), dt_softplus=True)
+    _, rl = parity_metrics(got.cpu(), ref)
+    _, sl = parity_metrics(s1.cpu(), ref_state)
+    assert rl <= 1e-5 and sl <= 1e-5, (rl, sl)
+
+
+def test_decode_c_abi_default_layout():
+    """The C ABI without MAMBA2_SSU_STRIDES reads every input in the
+    contiguous layout of its shape (tied form: dt [B, H], A [H], D [H])."""
+    _need_gpu()
+    import ctypes
+
+    from ascend_kernel import _runtime as rt
+    from ascend_kernel import selective_state_update
+
+    b, h, p, n, g = 3, 4, 64, 64, 2
+    gen = torch.Generator().manual_seed(22)
+    r = lambda *s: torch.randn(*s, generator=gen).cuda()  # noqa: E731
+    x, Bm, Cm, z = r(b, h, p), r(b, g, n), r(b, g, n), r(b, h, p)
+    dt_h, A_h, D_h = torch.rand(b, h, generator=gen).cuda(), -torch.rand(h, generator=gen).cuda(), r(h)
+    state0 = r(b, h, p, n)
+    s1, s2 = state0.clone(), state0.clone()
+    out = torch.empty(b, h, p, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    flags = rt.SSU_TIED | rt.DT_SOFTPLUS | rt.HAS_D | rt.HAS_Z
+    args = rt.Mamba2SsuArgs(b, h, p, n, g, flags, P(s1), b, h * p * n, None,
+                            P(x), P(dt_h), P(A_h), P(Bm), P(Cm), P(D_h), P(z), None, P(out))
+    lib = rt.load_library()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rt.check(lib.mamba2_selective_state_update(ctypes.byref(args), stream), "ssu", lib)
+    want = selective_state_update(s2, x, dt_h[..., None].expand(b, h, p), A_h[:, None, None].expand(h, p, n),
+                                  Bm, Cm, D=D_h[:, None].expand(h, p), z=z, dt_softplus=True)
+    torch.cuda.synchronize()
+    assert torch.allclose(out, want, rtol=1e-6, atol=1e-6)
+    assert torch.allclose(s1, s2, rtol=1e-6, atol=1e-6)
