@@ -293,3 +293,20 @@ def test_varlen_states_under_autograd():
     torch.cuda.synchronize()
     for k in res[0]:
         assert torch.equal(res[0][k], res[1][k]), k
+
+
+def test_varlen_states_empty_sequences():
+    """An empty sequence (equal consecutive cu_seqlens) has the zero state; the
+    others match the oracle."""
+    _need_gpu()
+    inp = make_inputs([1, 150, 2, 64, 64, 64, 1], seed=360)
+    lengths = [40, 0, 110]
+    ids = torch.cat([torch.zeros(40), torch.full((110,), 2)]).to(torch.int32)[None]
+    cu = torch.tensor([0, 40, 40, 150], dtype=torch.int32)
+    _, _, got_v = _run(inp, 64, ids, cu_seqlens=cu.cuda(), return_varlen_states=True)
+    _, _, states = _ref(inp, 64, ids, return_chunk_states=True)
+    want_v = chunk_state_varlen_ref(inp["x"], inp["dt"], inp["A"], inp["B"], 64,
+                                    torch.tensor([0, 40, 150]), states, dt_softplus=True)
+    assert torch.equal(got_v[1], torch.zeros_like(got_v[1]))
+    _check("varlen states", torch.stack([got_v[0], got_v[2]]), want_v)
+    assert got_v.shape[0] == len(lengths)
