@@ -100,7 +100,7 @@ def _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
 
 
 def _packed_shape_ok(x, B) -> bool:
-    return x.shape[-1] == 64 and B.shape[-1] in (64, 128)
+    return x.shape[-1] % 64 == 0 and B.shape[-1] in (64, 128)
 
 
 def _check_seq_idx(x, seq_idx, chunk_size, B) -> Optional[torch.Tensor]:
@@ -114,7 +114,8 @@ def _check_seq_idx(x, seq_idx, chunk_size, B) -> Optional[torch.Tensor]:
     if seq_idx.device != x.device:
         raise RuntimeError("mamba2_ssd_fwd: seq_idx must be on x's device")
     if not _packed_shape_ok(x, B):
-        raise NotImplementedError("mamba2_ssd_fwd: seq_idx needs headdim 64 with dstate 64 or 128")
+        raise NotImplementedError("mamba2_ssd_fwd: seq_idx needs a headdim that is a multiple of 64 "
+                                  "with dstate 64 or 128")
     return seq_idx.to(torch.int32).contiguous()
 
 
@@ -128,7 +129,7 @@ def _check_cu_seqlens(x, cu_seqlens, chunk_size, B) -> torch.Tensor:
         raise RuntimeError("mamba2_ssd_fwd: cu_seqlens must be on x's device")
     if x.shape[0] != 1:
         raise RuntimeError("mamba2_ssd_fwd: varlen states need batch 1")
-    if not _packed_shape_ok(x, B) or int(chunk_size) % 64:
+    if x.shape[-1] != 64 or B.shape[-1] not in (64, 128) or int(chunk_size) % 64:
         raise NotImplementedError("mamba2_ssd_fwd: varlen states need headdim 64, dstate 64 or "
                                   "128 and a chunk_size that is a multiple of 64")
     return cu_seqlens.to(torch.int32).contiguous()

@@ -89,6 +89,25 @@ bool fused_shape(const Mamba2SsdShape *s) {
     return s->headdim == 64 && (s->dstate == 64 || s->dstate == 128);
 }
 
+// A head of dim 64 m (m > 1) with dstate 64 or 128 runs the fused kernels as m
+// heads of dim 64: the public layouts of x, z, out, D [H, P] and the initial
+// and final states are the same memory read as [.., H m, 64, ..]; dt, A,
+// dt_bias and a per-head D are read for head h / m.  (Saved chunk states and
+// varlen states keep headdim 64: their layout would differ.)
+int head_split(const Mamba2SsdShape *s) {
+    return s->headdim > 64 && s->headdim % 64 == 0 && (s->dstate == 64 || s->dstate == 128)
+               ? (int)(s->headdim / 64)
+               : 1;
+}
+
+Mamba2SsdShape fused_view(const Mamba2SsdShape *s) {
+    Mamba2SsdShape v = *s;
+    const int m = head_split(s);
+    v.nheads *= m;
+    v.headdim /= m;
+    return v;
+}
+
 FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags) {
     FwdPlan pl;
     if (s->seqlen == 0) return pl;
@@ -124,7 +143,10 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags) {
     return pl;
 }
 
-size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags) { return fwd_plan(s, flags).ws; }
+size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags) {
+    const Mamba2SsdShape v = fused_view(s);
+    return fwd_plan(&v, flags).ws;
+}
 
 // Optional per-kernel event trace: events[0] is recorded before the first
 // kernel and events[i + 1] right after kernel i, all on the launch stream.
@@ -196,11 +218,15 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     if (bool(f & MAMBA2_SSD_SAVED_STATES) != (a->chunk_states != nullptr))
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
                     "chunk_states pointer and SAVED_STATES flag disagree");
-    if ((f & (MAMBA2_SSD_SAVED_STATES | MAMBA2_SSD_HAS_SEQ_IDX | MAMBA2_SSD_VARLEN_STATES)) &&
-        !fused_shape(s))
+    if ((f & (MAMBA2_SSD_SAVED_STATES | MAMBA2_SSD_VARLEN_STATES)) && !fused_shape(s))
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
-                    "SAVED_STATES, HAS_SEQ_IDX and VARLEN_STATES need headdim 64 with dstate 64 "
-                    "or 128 (got %lld, %lld)",
+                    "SAVED_STATES and VARLEN_STATES need headdim 64 with dstate 64 or 128 "
+                    "(got %lld, %lld)",
+                    (long long)s->headdim, (long long)s->dstate);
+    if ((f & MAMBA2_SSD_HAS_SEQ_IDX) && !fused_shape(s) && head_split(s) == 1)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
+                    "HAS_SEQ_IDX needs a headdim that is a multiple of 64 with dstate 64 or 128 "
+                    "(got %lld, %lld)",
                     (long long)s->headdim, (long long)s->dstate);
     if (bool(f & MAMBA2_SSD_HAS_SEQ_IDX) != (a->seq_idx != nullptr))
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "seq_idx pointer and HAS_SEQ_IDX flag disagree");
@@ -249,6 +275,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     prm.G = (int)s->ngroups;
     prm.R = (int)(s->nheads / s->ngroups);
     prm.K = (int)nchunks(s);
+    prm.hdiv = 1;
     prm.softplus = (f & MAMBA2_SSD_DT_SOFTPLUS) != 0;
     prm.has_D = (f & MAMBA2_SSD_HAS_D) != 0;
     prm.d_per_channel = (f & MAMBA2_SSD_D_PER_CHANNEL) != 0;
@@ -279,7 +306,15 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         }
         return ok();
     }
-    const FwdPlan pl = fwd_plan(s, f);
+    // the fused kernels' view of the shape (heads of dim 64)
+    const Mamba2SsdShape vs = fused_view(s);
+    const int m = head_split(s);
+    const FwdPlan pl = fwd_plan(&vs, f);
+    if (pl.fused && m > 1) {
+        prm.H = (int)vs.nheads;
+        prm.R = (int)(vs.nheads / vs.ngroups);
+        prm.hdiv = m;
+    }
     if (varlen && !prm.chunk_states) prm.chunk_states = (float *)((char *)workspace + pl.states);
     const bool seq = prm.seq_idx != nullptr;
     if (pl.fused) {
@@ -287,7 +322,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         sp.nseg = pl.nseg;
         sp.M = pl.M;
         sp.nsplit = pl.nsplit;
-        const unsigned units = (unsigned)(s->batch * s->nheads * pl.nseg * pl.nsplit);
+        const unsigned units = (unsigned)(vs.batch * vs.nheads * pl.nseg * pl.nsplit);
         // with two state halves the halves' sum, D x, pre_gate and the z gate
         // are applied by k_fwd_combine
         ssd::FwdParams kp = prm;
@@ -303,7 +338,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
             sp.seg_log_decay = (float *)((char *)workspace + pl.seg_decay);
             ssd::launch_fwd_seg(true, false, false, seq, dim3(units), st, kp, sp);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
-            const int PN = (int)(s->headdim * s->dstate);
+            const int PN = (int)(vs.headdim * vs.dstate);
             const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
             hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, sp.seg_state,
                                sp.seg_log_decay, prm.init, sp.seg_state, prm.final_state, pl.nseg, PN);

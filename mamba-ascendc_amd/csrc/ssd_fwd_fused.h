@@ -152,8 +152,9 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     float dtr[kDepth];
     int sidr[kDepth], sprv[kDepth]; // kSeq: id of token `lane`, id of the token before the chunk
     const int rowHP4 = (int)(rowHP * 4), rowGN4 = (int)(rowGN * 4); // token strides, bytes
-    const float Ah2 = prm.A[h] * kLog2e;                                 // A in log2 units
-    const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
+    const int hr = h / prm.hdiv, Hr = H / prm.hdiv;                      // the real head
+    const float Ah2 = prm.A[hr] * kLog2e;                                // A in log2 units
+    const float bias = prm.dt_bias ? prm.dt_bias[hr] : 0.f;
     // Loads are issued unconditionally, so the wait counts the compiler
     // derives are exact: rows past the sequence end re-read its last row
     // (their q is 0, so they add nothing), and chunks past the segment read
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             xr[sl][j] = buf_load4(rx, row * rowHP4 + c4 * 4, 0);
             br[sl][j] = buf_load4(rb, row * rowGN4 + c4 * 4, 0);
         }
-        dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * H + h];
+        dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * Hr + hr];
         if (kSeq) {
             const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + t0;
             sidr[sl] = si[min(lane, tv - 1)];
@@ -341,7 +342,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 c_load(kbeg + 1, C1{});
                 z_load(kbeg);
                 if (W == 0) {
-                    const float dv = prm.has_D ? prm.D[prm.d_per_channel ? h * P + lane : h] : 0.f;
+                    const float dv = prm.has_D ? prm.D[prm.d_per_channel ? h * P + lane : hr] : 0.f;
                     s_Dv[lane] = dv;
                 }
             }
@@ -546,7 +547,8 @@ __global__ __launch_bounds__(kThreads) void k_fwd_combine(FwdParams prm, const f
             const int p = (int)(e % P), h = (int)((e / P) % prm.H);
             const float4 xv = *(const float4 *)(prm.x + e);
             const float4 d = prm.d_per_channel ? *(const float4 *)(prm.D + h * P + p)
-                                               : make_float4(prm.D[h], prm.D[h], prm.D[h], prm.D[h]);
+                                               : make_float4(prm.D[h / prm.hdiv], prm.D[h / prm.hdiv],
+                                                             prm.D[h / prm.hdiv], prm.D[h / prm.hdiv]);
             v.x += d.x * xv.x;
             v.y += d.y * xv.y;
             v.z += d.z * xv.z;

@@ -33,6 +33,9 @@ struct FwdParams {
     const int32_t *seq_idx; // [B, L] sequence id of every token (packed sequences), or NULL
     int64_t L;
     int H, G, R, K;         // heads, groups, heads per group, chunks
+    int hdiv;               // the fused kernels see a head of dim 64 m as m heads of dim 64
+                            // (H, R counted that way); dt, A, dt_bias and a per-head D are
+                            // indexed by h / hdiv, dt's token stride is H / hdiv
     int softplus, has_D, d_per_channel, has_z;
     float lo, hi;
 };

@@ -63,6 +63,10 @@ CASES = [
     ([1, 1, 2, 64, 64, 64, 1], ("init",), True, (0.0, math.inf)),       # single token
     ([3, 130, 6, 64, 64, 32, 3], ("bias",), False, (0.05, 0.8)),        # clamp, no softplus
     ([1, 300, 4, 64, 128, 256, 4], ("D2", "z", "bias", "init"), True, (0.1, 1.5)),
+    # headdim 64 m: m heads of dim 64 in the fused kernels (per-head dt, A, D shared)
+    ([2, 300, 4, 128, 64, 64, 2], ("D", "z", "bias", "init"), True, (0.0, math.inf)),
+    ([1, 200, 2, 128, 128, 128, 1], ("D2", "z", "init"), True, (0.0, math.inf)),
+    ([1, 700, 2, 192, 64, 64, 1], ("D", "bias"), False, (0.05, 0.9)),  # segments
     # generic token-recurrence path (headdim/dstate outside the MFMA kernels)
     ([2, 70, 4, 32, 16, 16, 2], ("D", "z", "init"), True, (0.0, math.inf)),
     ([1, 33, 3, 20, 200, 8, 1], ("bias",), True, (0.0, math.inf)),

@@ -93,6 +93,7 @@ PACKED = [
     ([2, 700, 8, 64, 64, 256, 2], ("D", "bias", "init"), 2),
     ([1, 1000, 4, 64, 128, 128, 1], ("z", "init"), 3),
     ([3, 333, 4, 64, 128, 64, 4], ("D2", "bias"), 4),
+    ([2, 300, 4, 128, 64, 64, 2], ("D", "z", "init"), 5),   # headdim 128 (two heads of 64)
 ]
 
 
