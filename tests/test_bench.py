@@ -1,0 +1,46 @@
+"""CPU checks of bench.py: the one-GPU contract, the kernel models the roofline
+line uses, and the mapping of traced kernel names onto them."""
+
+import math
+
+import bench
+
+
+def test_more_than_one_gpu_exits_with_a_message(capsys):
+    assert bench.main(["--gpus", "2"]) == 2
+    assert "exactly one GPU" in capsys.readouterr().err
+
+
+def test_forward_model_matches_the_documented_bytes():
+    """C3: 4 (2 T P + T + 2 T N / R) bytes per (b, h, chunk) unit, 131072
+    units (41.2 KB and 5.402 GB); the flops are the op-level formula's."""
+    shape = bench.CONFIGS[3]
+    m = bench.fwd_kernel_model("k_fwd_seg", shape)
+    T, P, N, R = 64, 64, 64, 4
+    assert m["units"] == 8 * 256 * 64
+    assert m["bytes_per_unit"] == 4 * (2 * T * P + T + 2 * T * N / R)
+    assert math.isclose(m["bytes"] / 1e9, 5.402, rel_tol=1e-3)
+    flops, _ = bench.op_work(shape)
+    assert math.isclose(m["flops"], flops, rel_tol=1e-12)
+    # the training forward adds the state entering each chunk
+    save = bench.fwd_kernel_model("k_fwd_seg_save", shape)
+    assert save["bytes"] - m["bytes"] == 4 * P * N * m["units"]
+    # packed sequences move the same tensors
+    assert bench.fwd_kernel_model("k_fwd_seg_seq", shape)["bytes"] == m["bytes"]
+
+
+def test_traced_names_map_to_distinct_models():
+    key = bench.model_key
+    assert key("k_fwd_seg<false, false, false, false>") == "k_fwd_seg"
+    assert key("k_fwd_seg<false, true, false, false>") == "k_fwd_seg_save"
+    assert key("k_fwd_seg<false, false, true, false>") == "k_fwd_seg_gate"
+    assert key("k_fwd_seg<false, true, true, true>") == "k_fwd_seg_save_gate_seq"
+    assert key("k_fwd_seg<true, false, false, true>") == "k_fwd_seg_state_seq"
+    assert key("k_bwd_ws<false, 4, false>") == "k_bwd_ws_rev"
+    assert key("k_bwd_ws<true, 2, false>") == "k_bwd_ws_rev_z"
+    assert key("k_bwd_ws<false, 4, true>") == "k_bwd_ws_rev_seq"
+    assert key("k_bwd_ws<true, 0, false>") == "k_bwd_ws"
+    assert key("k_state_pass") == "k_state_pass"
+    shape = bench.CONFIGS[3]
+    for name in ("k_fwd_seg_gate", "k_fwd_seg_save_gate", "k_bwd_ws_rev", "k_bwd_ws_rev_z"):
+        assert not math.isnan(bench.fwd_kernel_model(name, shape)["bytes"]), name
