@@ -73,13 +73,16 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     // still reads them while step n + 1 runs); S, dU, B, C single
     __shared__ __attribute__((aligned(16))) _Float16 lds[16 * kTile];
     // per-token (and per-channel D) values of a step, double buffered by step parity
-    __shared__ __attribute__((aligned(16))) float s_q[2][T], s_cs[2][T], s_dqdu[2][T], s_dte[2][T],
+    // The per-token arrays are aligned above the tile array so the LDS layout
+    // places them first, below 64 KB: their lane addresses then share one
+    // base register with 16-bit immediate offsets instead of one register each.
+    __shared__ __attribute__((aligned(32))) float s_q[2][T], s_cs[2][T], s_dqdu[2][T], s_dte[2][T],
         s_ecs[2][T], s_D[2][P];
-    __shared__ float s_dcs[2][T], s_rd[2][T], s_A[2];
-    __shared__ __attribute__((aligned(16))) float s_sdu[2][4];
-    __shared__ __attribute__((aligned(16))) float s_da[4][T]; // epilogue: da of a step, per consumer wave
-    __shared__ __attribute__((aligned(16))) int s_sid[2][TS];   // kSeq: token ids, by step parity
-    __shared__ float s_carry[2];                                 // kSeq: 1 where the state carries over
+    __shared__ __attribute__((aligned(32))) float s_dcs[2][T], s_rd[2][T], s_A[2];
+    __shared__ __attribute__((aligned(32))) float s_sdu[2][4];
+    __shared__ __attribute__((aligned(32))) float s_da[4][T]; // epilogue: da of a step, per consumer wave
+    __shared__ __attribute__((aligned(32))) int s_sid[2][TS];   // kSeq: token ids, by step parity
+    __shared__ __attribute__((aligned(32))) float s_carry[2];   // kSeq: 1 where the state carries over
 
     auto Xt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, par); };
     auto Gt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, 2 + par); };
