@@ -64,6 +64,14 @@ int check_shape(const Mamba2SsdShape *s, uint32_t flags) {
                     (long long)s->nheads, (long long)s->ngroups);
     if (s->batch > 65535 || s->nheads > 65535)
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "batch and nheads must be <= 65535");
+    // the chunk kernels address a chunk's 64 token rows with 32-bit byte
+    // offsets from the chunk start
+    if (s->nheads * s->headdim > (int64_t)0x7fffffff / (4 * ssd::kChunk) ||
+        s->ngroups * s->dstate > (int64_t)0x7fffffff / (4 * ssd::kChunk))
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
+                    "token rows too wide: nheads*headdim=%lld and ngroups*dstate=%lld must be <= %lld",
+                    (long long)(s->nheads * s->headdim), (long long)(s->ngroups * s->dstate),
+                    (long long)((int64_t)0x7fffffff / (4 * ssd::kChunk)));
     return MAMBA2_SSD_OK;
 }
 

@@ -63,6 +63,10 @@ def _shape(**kw):
         (dict(), rt.D_PER_CHANNEL, -1),
         (dict(), 1 << 12, -1),
         (dict(batch=70000), 0, -2),
+        # 64 token rows of H*P (or G*N) floats must stay within 32-bit byte offsets
+        (dict(nheads=65535, ngroups=65535, headdim=128), 0, 0),
+        (dict(nheads=65535, ngroups=65535, headdim=192), 0, -2),
+        (dict(nheads=65535, ngroups=65535, dstate=192), 0, -2),
     ],
 )
 def test_workspace_size_validation(kw, flags, code):

@@ -239,6 +239,7 @@ BWD = [
     ([2, 130, 256, 64, 64, 64, 32], ("z", "init"), "mixed"),                 # reverse dstate pass
     ([2, 200, 256, 64, 64, 64, 128], ("D2", "z", "bias", "init"), "mixed"),  # fused reverse, R = 2
     ([4, 130, 256, 64, 64, 128, 64], ("D", "init"), "packed"),               # fused reverse, R = 4
+    ([4, 140, 256, 64, 64, 64, 64], ("z", "bias"), "mixed"),                 # fused reverse, R = 4, z
     ([1, 150, 256, 64, 64, 64, 256], ("z", "bias", "init"), "mixed"),        # fused reverse, R = 1
 ]
 
