@@ -72,17 +72,26 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     // x and gy tiles double buffered by step parity (the epilogue of step n
     // still reads them while step n + 1 runs); S, dU, B, C single
     __shared__ __attribute__((aligned(16))) _Float16 lds[16 * kTile];
-    // per-token (and per-channel D) values of a step, double buffered by step parity
     // The per-token arrays are aligned above the tile array so the LDS layout
     // places them first, below 64 KB: their lane addresses then share one
     // base register with 16-bit immediate offsets instead of one register each.
-    __shared__ __attribute__((aligned(32))) float s_q[2][T], s_cs[2][T], s_dqdu[2][T], s_dte[2][T],
-        s_ecs[2][T], s_D[2][P];
-    __shared__ __attribute__((aligned(32))) float s_dcs[2][T], s_rd[2][T], s_A[2];
+    // Per-token (and per-channel D) values of a step written by the dt
+    // prologue, double buffered by step parity; one struct, so the writing
+    // wave addresses every member from one base (see the prologue).
+    struct StepTok {
+        float q[2][T], cs[2][T], dqdu[2][T], dte[2][T], ecs[2][T], D[2][P];
+        int sid[2][TS];  // kSeq: token ids
+        float carry[2];  // kSeq: 1 where the state carries over
+        float A[2];
+    };
+    __shared__ __attribute__((aligned(32))) StepTok s_tok;
+    auto &s_q = s_tok.q, &s_cs = s_tok.cs, &s_dqdu = s_tok.dqdu, &s_dte = s_tok.dte, &s_ecs = s_tok.ecs,
+         &s_D = s_tok.D;
+    auto &s_sid = s_tok.sid;
+    auto &s_carry = s_tok.carry, &s_A = s_tok.A;
+    __shared__ __attribute__((aligned(32))) float s_dcs[2][T], s_rd[2][T];
     __shared__ __attribute__((aligned(32))) float s_sdu[2][4];
     __shared__ __attribute__((aligned(32))) float s_da[4][T]; // epilogue: da of a step, per consumer wave
-    __shared__ __attribute__((aligned(32))) int s_sid[2][TS];   // kSeq: token ids, by step parity
-    __shared__ __attribute__((aligned(32))) float s_carry[2];   // kSeq: 1 where the state carries over
 
     auto Xt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, par); };
     auto Gt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, 2 + par); };
@@ -276,20 +285,24 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 const float cs = wave_inclusive_scan(a); // log2 units
                 const float last = readlane_f(cs, T - 1);
                 float into = 1.f, reads = 1.f;
+                // every member from one base the optimizer cannot split into
+                // per-array registers (those were held across the step loop
+                // and spilled, and each reload waited for the prefetches)
+                StepTok *tk = opaque_lds_t(&s_tok);
                 if (kSeq) {
                     const int e_end = __shfl(sidr, T - 1, kWave); // rows past the end repeat the last id
                     into = (sidr == e_end && e_end >= 0) ? 1.f : 0.f;
                     reads = sidr == sprv ? 1.f : 0.f;
-                    s_sid[par][lane] = sidr;
-                    if (lane == 0) s_carry[par] = e_end == sprv ? 1.f : 0.f;
+                    tk->sid[par][lane] = sidr;
+                    if (lane == 0) tk->carry[par] = e_end == sprv ? 1.f : 0.f;
                 }
-                s_q[par][lane] = q;
-                s_cs[par][lane] = cs;
-                s_dqdu[par][lane] = dq;
-                s_dte[par][lane] = exp2_f(last - cs) * into;
-                s_ecs[par][lane] = exp2_f(cs) * reads;
-                s_D[par][lane] = prm.has_D ? Dr : 0.f;
-                if (lane == 0) s_A[par] = Ahr;
+                tk->q[par][lane] = q;
+                tk->cs[par][lane] = cs;
+                tk->dqdu[par][lane] = dq;
+                tk->dte[par][lane] = exp2_f(last - cs) * into;
+                tk->ecs[par][lane] = exp2_f(cs) * reads;
+                tk->D[par][lane] = prm.has_D ? Dr : 0.f;
+                if (lane == 0) tk->A[par] = Ahr;
             }
         };
         auto stage_bc = [&](int n) __attribute__((always_inline)) {

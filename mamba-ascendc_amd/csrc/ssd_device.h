@@ -317,6 +317,15 @@ __device__ __forceinline__ _Float16 *opaque_lds(_Float16 *p) {
     return (_Float16 *)(lptr)(uintptr_t)a;
 }
 
+// The same for any LDS object (a struct of small arrays, say).
+template <class X>
+__device__ __forceinline__ X *opaque_lds_t(X *p) {
+    typedef __attribute__((address_space(3))) X *lptr;
+    uint32_t a = (uint32_t)(uintptr_t)(lptr)p;
+    asm volatile("" : "+s"(a));
+    return (X *)(lptr)(uintptr_t)a;
+}
+
 __device__ __forceinline__ half8 cat8(half4 a, half4 b) {
     return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
