@@ -339,3 +339,47 @@ def test_validation_messages(mutate, match, monkeypatch):
     with pytest.raises(RuntimeError, match=match):
         api._validate_fwd("mamba2_ssd_fwd", t["x"], t["dt"], t["A"], t["B"], t["C"], 64,
                           None, None, None, None, 0.0, math.inf)
+
+
+def test_header_constants_match_the_python_side():
+    """Flag bits, ABI version and status codes of include/mamba2_ssd.h are the
+    values the ctypes layer passes and decodes."""
+    text = open(HEADER).read()
+    flags = re.findall(r"#define (MAMBA2_\w+) \(1u << (\d+)\)", text)
+    assert len(flags) >= 11
+    for name, bit in flags:
+        short = name.replace("MAMBA2_SSD_", "").replace("MAMBA2_", "")
+        assert getattr(rt, short) == 1 << int(bit), name
+    assert rt.ABI_VERSION == int(re.search(r"#define MAMBA2_SSD_ABI_VERSION (\d+)", text).group(1))
+    codes = re.findall(r"#define MAMBA2_SSD_(OK|ERR_\w+) \(?(-?\d+)\)?", text)
+    assert len(codes) == len(rt.STATUS_NAMES)
+    for name, value in codes:
+        assert rt.STATUS_NAMES[int(value)] == name.replace("ERR_", ""), name
+
+
+def test_struct_layouts_match_ctypes(tmp_path):
+    """sizeof and every member offset of the header's argument structs, as a C
+    compiler lays them out, equal the ctypes declarations."""
+    import shutil
+
+    if shutil.which("gcc") is None:
+        pytest.skip("needs gcc")
+    classes = [rt.Mamba2SsdShape, rt.Mamba2SsdFwdArgs, rt.Mamba2SsdBwdArgs, rt.Mamba2SsuStrides,
+               rt.Mamba2SsuArgs]
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "mamba2_ssd.h"', "int main(void) {"]
+    for cls in classes:
+        n = cls.__name__
+        lines.append(f'  printf("{n} %zu\\n", sizeof({n}));')
+        for field in cls._fields_:
+            lines.append(f'  printf("{n}.{field[0]} %zu\\n", offsetof({n}, {field[0]}));')
+    lines += ["  return 0;", "}"]
+    src, exe = tmp_path / "layout.c", tmp_path / "layout"
+    src.write_text("\n".join(lines) + "\n")
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.dirname(HEADER), "-o", str(exe), str(src)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                 check=True).stdout.splitlines())
+    for cls in classes:
+        n = cls.__name__
+        assert int(got[n]) == ctypes.sizeof(cls), n
+        for field in cls._fields_:
+            assert int(got[f"{n}.{field[0]}"]) == getattr(cls, field[0]).offset, (n, field[0])
