@@ -854,7 +854,8 @@ def main(argv=None):
 
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for --gpus {args.gpus}): the SSD hot path "
-              "is a single-device operator here; see DESIGN.md for how it would shard.",
+              "is a single-device operator here (it would shard over (batch, group) streams, "
+              "which share nothing in the forward).",
               file=sys.stderr)
         return 2
 
