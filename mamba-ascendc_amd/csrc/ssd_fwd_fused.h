@@ -105,14 +105,24 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     // T2(s), T3(s) = tiles 2 s, 2 s + 1
     constexpr int kTiles = kStateOnly ? 4 : 8;
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * kTiles * kTile];
-    __shared__ __attribute__((aligned(16))) float s_cs[2][T], s_q[2][T];
+    // Per-token values of a chunk written by the producers' dt prologue, by
+    // chunk parity; one struct, so the writing wave addresses every member
+    // from one base (see the prologue).
+    struct ChunkTok {
+        float cs[2][T], q[2][T];
+        // kSeq: token ids, 1 where the token reads the entering state
+        int sid[2][TS];
+        float off[2][TS];
+        float carry[2]; // kSeq: 1 where the state carries over the chunk
+        int mixed[2];   // kSeq: the chunk holds more than one id (C.B^T needs the id mask)
+    };
+    __shared__ __attribute__((aligned(16))) ChunkTok s_tok;
+    auto &s_cs = s_tok.cs, &s_q = s_tok.q;
+    auto &s_sid = s_tok.sid;
+    auto &s_off = s_tok.off;
+    auto &s_carry = s_tok.carry;
+    auto &s_mixed = s_tok.mixed;
     __shared__ __attribute__((aligned(16))) float s_Dv[P]; // D per channel (a scalar D repeated)
-    // kSeq, by chunk parity: token ids, 1 where the token reads the entering
-    // state, 1 where the state carries over the chunk
-    __shared__ __attribute__((aligned(16))) int s_sid[2][TS];
-    __shared__ __attribute__((aligned(16))) float s_off[2][TS];
-    __shared__ float s_carry[2];
-    __shared__ int s_mixed[2]; // kSeq: the chunk holds more than one id (C.B^T needs the id mask)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const bool producer = wave >= 4;
@@ -198,9 +208,12 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         }
         const float cs = wave_inclusive_scan(a);
         const float cs_last = readlane_f(cs, T - 1);
+        // every member from one base the optimizer cannot split into
+        // per-array address registers
+        ChunkTok *tk = opaque_lds_t(&s_tok);
         if (w == 0) {
-            s_cs[s][lane] = cs;
-            s_q[s][lane] = q;
+            tk->cs[s][lane] = cs;
+            tk->q[s][lane] = q;
         }
         float dec = exp2_f(cs_last - cs);
         if (kSeq) {
@@ -209,11 +222,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             if (sid != e_end || e_end < 0) dec = 0.f; // not part of the state leaving the chunk
             const bool mixed = __ballot(sid != e_end) != 0;
             if (w == 0) {
-                s_sid[s][lane] = sid;
-                s_off[s][lane] = sid == e_prev ? 1.f : 0.f;
+                tk->sid[s][lane] = sid;
+                tk->off[s][lane] = sid == e_prev ? 1.f : 0.f;
                 if (lane == 0) {
-                    s_carry[s] = e_end == e_prev ? 1.f : 0.f;
-                    s_mixed[s] = mixed ? 1 : 0;
+                    tk->carry[s] = e_end == e_prev ? 1.f : 0.f;
+                    tk->mixed[s] = mixed ? 1 : 0;
                 }
             }
         }
