@@ -276,7 +276,100 @@ def bench_forward(torch, lib, rt, api, hip, inp, shape, steps, warmup):
     run_traced(torch, lib, rt, hip, call, warmup)
     res, names, wall = run_traced(torch, lib, rt, hip, call, steps)
     ok = bool(torch.isfinite(out).all()) and bool(torch.isfinite(final).all())
-    return res, names, wall, ok, ws.numel()
+    return res, names, wall, ok, ws.numel(), out, final
+
+
+PARITY_MAXABS, PARITY_RELL2 = 2e-2, 5e-3  # the contract: max-abs and relative-L2 vs the fp32 oracle
+
+
+def parity_slices(torch, inp, out, final, shape, slices):
+    """Same-run parity gate: the CPU oracle on slices (batch, head0, head1) of the
+    timed inputs against the same slices of the GPU output.  Heads share nothing
+    but their group's B and C, so a slice of heads of one group is an
+    independent problem."""
+    from oracle.ssd_reference import parity_metrics, ssd_chunk_scan_ref
+
+    b, l, h, p, n, chunk, g = shape
+    r = h // g
+    rows, worst = [], [0.0, 0.0, 0.0, 0.0]
+    for bi, h0, h1 in slices:
+        gi = h0 // r
+        assert (h1 - 1) // r == gi, "a parity slice stays within one group"
+        sub = {"x": inp["x"][bi:bi + 1, :, h0:h1], "dt": inp["dt"][bi:bi + 1, :, h0:h1],
+               "A": inp["A"][h0:h1], "B": inp["B"][bi:bi + 1, :, gi:gi + 1],
+               "C": inp["C"][bi:bi + 1, :, gi:gi + 1]}
+        sub = {k: v.contiguous().cpu() for k, v in sub.items()}
+        with torch.no_grad():
+            ref, ref_fin = ssd_chunk_scan_ref(sub["x"], sub["dt"], sub["A"], sub["B"], sub["C"], chunk,
+                                              dt_softplus=True, return_final_state=True)
+        m = parity_metrics(out[bi:bi + 1, :, h0:h1].cpu(), ref) + \
+            parity_metrics(final[bi:bi + 1, h0:h1].cpu(), ref_fin)
+        worst = [max(a, c) for a, c in zip(worst, m)]
+        rows.append(f"batch {bi} heads {h0}..{h1 - 1}")
+    ok = (worst[0] <= PARITY_MAXABS and worst[1] <= PARITY_RELL2 and worst[2] <= PARITY_MAXABS
+          and worst[3] <= PARITY_RELL2)
+    return {"slices": rows, "out_maxabs": worst[0], "out_relL2": worst[1],
+            "final_maxabs": worst[2], "final_relL2": worst[3],
+            "bound": {"maxabs": PARITY_MAXABS, "relL2": PARITY_RELL2}, "pass": bool(ok),
+            "oracle": "oracle/ssd_reference.py fp32 on the CPU, same inputs"}
+
+
+# parity slices (batch, head0, head1) per BASELINE config: the first and the
+# last heads of the problem
+PARITY_SLICES = {
+    1: [(0, 0, 2)],
+    2: [(0, 0, 4), (3, 12, 16)],
+    3: [(0, 0, 4), (7, 252, 256)],
+    4: [(0, 0, 4), (3, 12, 16)],
+    5: [(0, 0, 2), (0, 30, 32)],
+}
+
+
+def summarize_kernels(res, names, shape):
+    kern = {}
+    for i, name in enumerate(names):
+        durs = [r[1][i] for r in res]
+        model = fwd_kernel_model(name, shape)
+        avg = statistics.fmean(durs)
+        kern[name] = {"avg_ms": round(avg, 6), "median_ms": round(statistics.median(durs), 6)}
+        if model["bytes"] == model["bytes"]:
+            kern[name]["GB_s"] = round(model["bytes"] / (avg * 1e-3) / 1e9, 1)
+    return kern
+
+
+def bench_config(torch, lib, rt, api, hip, cfg, steps, warmup):
+    """One BASELINE config besides the headline: the forward (dt_softplus, final
+    state) timed with the reference protocol, its per-kernel durations, the
+    op-level algorithmic GB/s and HBM fraction, and a same-run parity slice; for
+    config 4 (the M1 backward config) also the training forward + backward."""
+    shape = CONFIGS[cfg]
+    seed = 20260806 + (cfg - 1)
+    inp = make_gpu_inputs(torch, shape, seed)
+    torch.cuda.synchronize()
+    res, names, _wall, finite, ws_bytes, out, final = bench_forward(
+        torch, lib, rt, api, hip, inp, shape, steps, warmup)
+    fwd_ms = statistics.median(r[0] for r in res)
+    flops, nbytes = op_work(shape)
+    row = {"shape": shape, "seed": seed, "fwd_ms": round(fwd_ms, 5),
+           "fwd_kernels": summarize_kernels(res, names, shape),
+           "op_GB_s": round(nbytes / (fwd_ms * 1e-3) / 1e9, 1),
+           "op_TFLOP_s": round(flops / (fwd_ms * 1e-3) / 1e12, 2),
+           "hbm_roofline_frac": round(nbytes / (fwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "op_bytes": nbytes, "workspace_bytes": ws_bytes, "finite": finite,
+           "parity": parity_slices(torch, inp, out, final, shape, PARITY_SLICES[cfg])}
+    del out, final
+    if shape[3] == 64 and shape[4] == 64:
+        tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup)
+        if tr is not None:
+            fres, bres, bnames, bfinite = tr[:4]
+            row["fwd_train_ms"] = round(statistics.median(r[0] for r in fres), 5)
+            row["bwd_ms"] = round(statistics.median(r[0] for r in bres), 5)
+            row["fwd_bwd_ms"] = round(statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres)), 5)
+            row["bwd_kernels"] = summarize_kernels(bres, bnames, shape)
+            row["grads_finite"] = bool(bfinite)
+    del inp
+    torch.cuda.empty_cache()
+    return row
 
 
 def full_features(torch, shape, seed):
@@ -831,6 +924,8 @@ def main(argv=None):
     ap.add_argument("--config", type=int, default=HEADLINE, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--no-bwd", action="store_true", help="skip the fwd+bwd timing")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="time only --config, not the other BASELINE configs")
     ap.add_argument("--no-full", action="store_true",
                     help="skip the full-feature (D, z, dt_bias, initial states, dt_limit) timings")
     ap.add_argument("--copy-calib", action="store_true",
@@ -880,8 +975,8 @@ def main(argv=None):
     inp = make_gpu_inputs(torch, shape, seed)
     torch.cuda.synchronize()
     log("inputs ready; forward warmup + timed steps")
-    res, names, wall_ms, finite, ws_bytes = bench_forward(torch, lib, rt, api, hip, inp, shape,
-                                                          args.steps, args.warmup)
+    res, names, wall_ms, finite, ws_bytes, out, final = bench_forward(
+        torch, lib, rt, api, hip, inp, shape, args.steps, args.warmup)
     step_ms = [r[0] for r in res]
     fwd_ms = statistics.median(step_ms)
     kern = {}
@@ -900,6 +995,11 @@ def main(argv=None):
         log(f"  {name:<16} avg {avg:8.4f} ms  {kern[name]['GB_s']:8.1f} GB/s  "
             f"{kern[name]['TFLOP_s']:7.2f} TFLOP/s")
     log(f"forward median {fwd_ms:.4f} ms (wall {wall_ms / args.steps:.4f} ms/step), finite={finite}")
+    parity = parity_slices(torch, inp, out, final, shape, PARITY_SLICES[args.config])
+    log(f"same-run parity vs the CPU oracle on {parity['slices']}: out maxabs {parity['out_maxabs']:.3e} "
+        f"relL2 {parity['out_relL2']:.3e}, final maxabs {parity['final_maxabs']:.3e} relL2 "
+        f"{parity['final_relL2']:.3e} -> {'pass' if parity['pass'] else 'FAIL'}")
+    del out, final
 
     api_ms = bench_api(torch, api, inp, chunk, max(5, args.steps // 3), 3)
     log(f"public API forward median {api_ms:.4f} ms per call (runs of 5 consecutive calls)")
@@ -1009,6 +1109,19 @@ def main(argv=None):
     }
     del inp
     torch.cuda.empty_cache()
+    others = {}
+    if not args.no_configs:
+        # the other BASELINE configs, each with its own inputs and parity slice
+        for cfg in sorted(CONFIGS):
+            if cfg == args.config:
+                continue
+            row = bench_config(torch, lib, rt, api, hip, cfg, args.steps, args.warmup)
+            others[f"C{cfg}"] = row
+            log(f"config C{cfg} {row['shape']}: forward {row['fwd_ms']:.4f} ms, {row['op_GB_s']:.0f} GB/s "
+                f"({100 * row['hbm_roofline_frac']:.1f} % of 8 TB/s), parity "
+                f"{'pass' if row['parity']['pass'] else 'FAIL'} (out relL2 {row['parity']['out_relL2']:.2e})"
+                + (f"; training fwd {row['fwd_train_ms']:.4f} + bwd {row['bwd_ms']:.4f} ms"
+                   if "bwd_ms" in row else ""))
     copy_gbs = copy_bandwidth(torch)
     log(f"device copy (1 GiB, read + write) {copy_gbs:.0f} GB/s: the dominant kernel streams at "
         f"{d['GB_s'] / copy_gbs:.2f} of it")
@@ -1073,6 +1186,8 @@ def main(argv=None):
         "workspace_bytes": ws_bytes,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "parity": parity,
+        "configs": others,
         "finite": finite,
         "device": dev.name,
     }

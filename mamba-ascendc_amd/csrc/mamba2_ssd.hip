@@ -638,8 +638,16 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
     const int64_t PN = headdim * dstate;
     if (PN % 4)
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "headdim*dstate must be a multiple of 4");
-    if (batch * nheads > 65535 || PN > (int64_t)1 << 30 || nchunks_ > (int64_t)1 << 30)
-        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "problem too large for one launch");
+    // k_state_pass addresses its ring of kStateRing chunks and the log decays
+    // with 32-bit byte offsets: 16 chunks of PN floats and (K + 2 * 16) floats
+    if (batch * nheads > 65535)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "batch * nheads must be <= 65535");
+    if (PN * 4 * ssd::kStateRing > (int64_t)0x7fffffff ||
+        (nchunks_ + 2 * ssd::kStateRing) * 4 > (int64_t)0x7fffffff)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
+                    "headdim*dstate=%lld must be <= %lld and nchunks=%lld <= %lld",
+                    (long long)PN, (long long)(0x7fffffff / (4 * ssd::kStateRing)),
+                    (long long)nchunks_, (long long)(0x7fffffff / 4 - 2 * ssd::kStateRing));
     const dim3 grid((unsigned)((PN / 4 + ssd::kThreads - 1) / ssd::kThreads), (unsigned)(batch * nheads));
     hipLaunchKernelGGL(ssd::k_state_pass, grid, dim3(ssd::kThreads), 0, (hipStream_t)stream,
                        chunk_states, chunk_log_decay, initial_states, states_start, final_state,

@@ -92,13 +92,17 @@ __device__ __forceinline__ float exp2_f(float v) { return __builtin_amdgcn_exp2f
 __device__ __forceinline__ float rcp_f(float v) { return __builtin_amdgcn_rcpf(v); }
 
 // torch.nn.functional.softplus with beta = 1, threshold = 20, as
-// max(u, 0) + ln(1 + e^-|u|) with hardware exp2/log2: a handful of
-// instructions instead of the libm expf/log1pf chains.  Where e^-|u| < 2^-24
-// the log term rounds to 0 (absolute error below 6e-8).
+// max(u, 0) + ln(1 + e) with e = e^-|u|, using hardware exp2/log2: a handful
+// of instructions instead of the libm expf/log1pf chains.  ln(1 + e) is
+// evaluated as log1p: with w = fl(1 + e), ln(w) * e / (w - 1) (w - 1 is exact)
+// cancels the rounding of w, and where w rounds to 1 the term is e itself, so
+// a very negative u keeps its relative accuracy (softplus(-20) = 2.06e-9, not 0).
 __device__ __forceinline__ float softplus_f(float u) {
     if (u > 20.f) return u;
     const float e = exp2_f(-fabsf(u) * kLog2e);
-    return fmaxf(u, 0.f) + kLn2 * __builtin_amdgcn_logf(1.f + e);
+    const float w = 1.f + e;
+    const float l = w == 1.f ? e : kLn2 * __builtin_amdgcn_logf(w) * (e * rcp_f(w - 1.f));
+    return fmaxf(u, 0.f) + l;
 }
 
 __device__ __forceinline__ float sigmoid_f(float v) { return rcp_f(1.f + exp2_f(-v * kLog2e)); }

@@ -127,8 +127,29 @@ def test_backward_deterministic(shape):
         assert torch.equal(a[k], c[k]), k
 
 
+def _cos(a, b):
+    return torch.nn.functional.cosine_similarity(a.double().flatten(), b.double().flatten(), dim=0).item()
+
+
+def _oracle_loss_grads(inp, dtype):
+    """Gradients of mean(y^2) + mean(final^2) by autograd of the oracle in `dtype`."""
+    lv = {k: v.to(dtype).clone().requires_grad_(True) for k, v in inp.items()}
+    ro, rf = ssd_chunk_scan_ref(lv["x"], lv["dt"], lv["A"], lv["B"], lv["C"], 64, dt_softplus=True,
+                                return_final_state=True, compute_dtype=dtype)
+    (ro.pow(2).mean() + rf.pow(2).mean()).backward()
+    return {k: v.grad for k, v in lv.items()}
+
+
+# rel-L2 of the GPU gradients against the float64 oracle at config 4 (the
+# bound of the small float64 cases)
+C4_REL_VS_FP64 = 2e-4
+
+
 def test_backward_baseline_config4():
-    """BASELINE M1 config [4,2048,16,64,64,64,4], loss mean(y^2) + mean(final^2)."""
+    """BASELINE M1 config [4,2048,16,64,64,64,4], loss mean(y^2) + mean(final^2):
+    the GPU gradients against autograd of the oracle in float32 (the contract)
+    and in float64 (the tight bound, which also shows how far the fp32 oracle is
+    from exact arithmetic)."""
     _need_gpu()
     import ascend_kernel
 
@@ -141,17 +162,62 @@ def test_backward_baseline_config4():
                                             return_final_state=True)
     (out.pow(2).mean() + fin.pow(2).mean()).backward()
     torch.cuda.synchronize()
-    ref_leaves = {k: v.clone().requires_grad_(True) for k, v in inp.items()}
-    ro, rf = ssd_chunk_scan_ref(ref_leaves["x"], ref_leaves["dt"], ref_leaves["A"], ref_leaves["B"],
-                                ref_leaves["C"], 64, dt_softplus=True, return_final_state=True)
-    (ro.pow(2).mean() + rf.pow(2).mean()).backward()
+    g32 = _oracle_loss_grads(inp, torch.float32)
+    g64 = _oracle_loss_grads(inp, torch.float64)
     for k in inp:
-        got, want = leaves[k].grad.cpu(), ref_leaves[k].grad
-        ma, rl = parity_metrics(got, want)
-        cos = torch.nn.functional.cosine_similarity(got.double().flatten(), want.double().flatten(), dim=0).item()
-        _say(f"  d{k:<3} maxabs {ma:.3e} relL2 {rl:.3e} cos {cos:.9f}")
+        got = leaves[k].grad.cpu()
+        ma, rl = parity_metrics(got, g32[k])
+        ma64, rl64 = parity_metrics(got, g64[k])
+        _, rl_oracle = parity_metrics(g32[k], g64[k])
+        cos = _cos(got, g64[k])
+        _say(f"  d{k:<3} vs fp32 oracle: maxabs {ma:.3e} relL2 {rl:.3e} | vs fp64: maxabs "
+             f"{ma64:.3e} relL2 {rl64:.3e} cos {cos:.9f} | fp32 oracle vs fp64: relL2 {rl_oracle:.3e}")
         assert rl <= 5e-3 and ma <= 2e-2, (k, ma, rl)
+        assert rl64 <= C4_REL_VS_FP64 and ma64 <= 2e-2, (k, ma64, rl64)
         assert cos >= 0.999, (k, cos)
+
+
+def test_backward_baseline_config3_slices():
+    """BASELINE config 3 [8,4096,256,64,64,64,64] trained at full size through
+    autograd (the reverse fused backward: 512 (batch, group) streams, 64 chunks
+    each, 4 heads per group), loss mean(y^2) + mean(final^2).  (batch, group)
+    units share nothing but dA, so dx, ddt, dB and dC of a slice depend only on
+    that slice's inputs and upstream gradients: the oracle runs on batches 0
+    and 7, groups 0..3, with the GPU's own upstream gradients."""
+    _need_gpu()
+    import ascend_kernel
+
+    shape = [8, 4096, 256, 64, 64, 64, 64]
+    _say(f"config 3 backward {shape}")
+    inp = make_inputs(shape, seed=bench_seed(2))
+    leaves = {k: v.cuda().requires_grad_(True) for k, v in inp.items()}
+    out, fin = ascend_kernel.mamba2_ssd_fwd(leaves["x"], leaves["dt"], leaves["A"], leaves["B"],
+                                            leaves["C"], 64, dt_softplus=True,
+                                            return_final_state=True)
+    gy = (out * (2.0 / out.numel())).detach()
+    gf = (fin * (2.0 / fin.numel())).detach()
+    torch.autograd.backward((out, fin), (gy, gf))
+    torch.cuda.synchronize()
+    for k in ("x", "dt", "B", "C"):
+        assert bool(torch.isfinite(leaves[k].grad).all()), k
+    r, groups = 4, 4
+    for bi in (0, 7):
+        hs = slice(0, groups * r)
+        sub = {"x": inp["x"][bi:bi + 1, :, hs], "dt": inp["dt"][bi:bi + 1, :, hs], "A": inp["A"][hs],
+               "B": inp["B"][bi:bi + 1, :, :groups], "C": inp["C"][bi:bi + 1, :, :groups]}
+        lv = {k: v.contiguous().clone().requires_grad_(True) for k, v in sub.items()}
+        ro, rf = ssd_chunk_scan_ref(lv["x"], lv["dt"], lv["A"], lv["B"], lv["C"], 64,
+                                    dt_softplus=True, return_final_state=True)
+        torch.autograd.backward((ro, rf), (gy[bi:bi + 1, :, hs].cpu(), gf[bi:bi + 1, hs].cpu()))
+        got = {"x": leaves["x"].grad[bi:bi + 1, :, hs], "dt": leaves["dt"].grad[bi:bi + 1, :, hs],
+               "B": leaves["B"].grad[bi:bi + 1, :, :groups], "C": leaves["C"].grad[bi:bi + 1, :, :groups]}
+        for k, g in got.items():
+            g = g.cpu()
+            ma, rl = parity_metrics(g, lv[k].grad)
+            cos = _cos(g, lv[k].grad)
+            _say(f"  batch {bi} d{k:<3} maxabs {ma:.3e} (max |want| {lv[k].grad.abs().max():.3e}) "
+                 f"relL2 {rl:.3e} cos {cos:.9f}")
+            assert rl <= 5e-3 and ma <= 2e-2 and cos >= 0.999, (bi, k, ma, rl, cos)
 
 
 def test_forward_chunk_states_are_prefix_final_states():

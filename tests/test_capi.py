@@ -187,6 +187,16 @@ def test_state_passing_rejects_bad_arguments():
     assert lib.mamba2_ssd_state_passing(None, fake, None, fake, None, 1, 1, 1, 64, 64, None) == -1
     assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 1, 1, 0, 64, 64, None) == -1
     assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 1, 1, 1, 3, 3, None) == -2
+    # limits of the kernel's 32-bit offsets: 16 chunks of P*N floats, and the
+    # log decays of K + 32 chunks, must stay below 2^31 bytes
+    biggest_pn = 0x7FFFFFFF // (4 * 16)
+    assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 1, 1, 1, biggest_pn + 1, 1,
+                                        None) == -2
+    assert "headdim*dstate" in rt.last_error(lib)
+    assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 1, 1, 0x7FFFFFFF // 4 - 31,
+                                        64, 64, None) == -2
+    assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 256, 256, 1, 64, 64,
+                                        None) == -2
 
 
 def test_decode_step_rejects_bad_arguments():

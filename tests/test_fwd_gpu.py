@@ -145,29 +145,64 @@ def _slice_groups(inp, g0, g1, r):
     return out
 
 
-@pytest.mark.parametrize("cfg_index,shape,batches,groups", [
-    (1, [4, 2048, 16, 64, 128, 128, 4], 4, 4),   # config 2: whole problem
-    (2, [8, 4096, 256, 64, 64, 64, 64], 1, 4),   # config 3: batch 0, groups 0..3 (16 heads)
-    (4, [1, 16384, 32, 64, 128, 256, 1], 1, 1),  # config 5: whole problem
+def _fwd_capi_nan_filled(dev, shape):
+    """Forward through the C ABI into output buffers filled with NaN, so that
+    an element the kernels never write stays NaN."""
+    import ctypes
+
+    from ascend_kernel import _runtime as rt
+
+    lib = rt.load_library()
+    b, l, h, p, n, chunk, g = shape
+    shp = rt.Mamba2SsdShape(b, l, h, p, g, n, chunk)
+    flags = rt.DT_SOFTPLUS
+    nb = ctypes.c_size_t(0)
+    rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shp), flags, ctypes.byref(nb)), "ws", lib)
+    out = torch.full_like(dev["x"], math.nan)
+    fin = torch.full((b, h, p, n), math.nan, device=dev["x"].device)
+    ws = torch.empty(max(1, nb.value), dtype=torch.uint8, device=dev["x"].device)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    args = rt.Mamba2SsdFwdArgs(shp, flags, 0.0, math.inf, P(dev["x"]), P(dev["dt"]), P(dev["A"]),
+                               P(dev["B"]), P(dev["C"]), None, None, None, None, P(out), P(fin))
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rt.check(lib.mamba2_ssd_fwd(ctypes.byref(args), P(ws), ws.numel(), stream), "fwd", lib)
+    torch.cuda.synchronize()
+    return out, fin
+
+
+@pytest.mark.parametrize("cfg_index,shape,slices", [
+    # config 2: the whole problem
+    (1, [4, 2048, 16, 64, 128, 128, 4], [(0, 4, 0, 4)]),
+    # config 3: (batch, group) slices at the low end, the middle and the far
+    # end of the 2 GiB output (x spans exactly 2^31 bytes there)
+    (2, [8, 4096, 256, 64, 64, 64, 64], [(0, 1, 0, 4), (3, 4, 30, 34), (7, 8, 60, 64)]),
+    # config 5: the whole problem
+    (4, [1, 16384, 32, 64, 128, 256, 1], [(0, 1, 0, 1)]),
 ])
-def test_forward_parity_baseline_configs(cfg_index, shape, batches, groups):
-    """Full-size BASELINE configs: GPU on the whole problem, oracle on independent units."""
+def test_forward_parity_baseline_configs(cfg_index, shape, slices):
+    """Full-size BASELINE configs: GPU on the whole problem, oracle on
+    independent (batch, group) units; every output element must be written."""
     _need_gpu()
     _say(f"config {cfg_index + 1} {shape}")
     inp = make_inputs(shape, seed=bench_seed(cfg_index))
-    out, fin = _run_gpu(inp, shape[5])
+    dev = {k: v.cuda() for k, v in inp.items()}
+    out, fin = _fwd_capi_nan_filled(dev, shape)
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(fin).all())
+    del dev
     r = shape[2] // shape[6]
-    sub = _slice_groups({k: v[:batches] for k, v in inp.items() if k != "A"} | {"A": inp["A"]}, 0, groups, r)
     torch.set_num_threads(max(1, torch.get_num_threads()))
-    ref, ref_fin = _run_ref(sub, shape[5])
-    o = out[:batches, :, : groups * r]
-    f = fin[:batches, : groups * r]
-    ma, rl = parity_metrics(o, ref)
-    fma, frl = parity_metrics(f, ref_fin)
-    _say(f"  out maxabs {ma:.3e} rel {rl:.3e} | final maxabs {fma:.3e} rel {frl:.3e}")
-    assert ma <= MAXABS and rl <= RELL2
-    assert fma <= MAXABS and frl <= RELL2
-    assert torch.isfinite(out).all()
+    for b0, b1, g0, g1 in slices:
+        sub = _slice_groups({k: v[b0:b1] for k, v in inp.items() if k != "A"} | {"A": inp["A"]},
+                            g0, g1, r)
+        ref, ref_fin = _run_ref(sub, shape[5])
+        o = out[b0:b1, :, g0 * r:g1 * r].cpu()
+        f = fin[b0:b1, g0 * r:g1 * r].cpu()
+        ma, rl = parity_metrics(o, ref)
+        fma, frl = parity_metrics(f, ref_fin)
+        _say(f"  batches {b0}..{b1 - 1} groups {g0}..{g1 - 1}: out maxabs {ma:.3e} rel {rl:.3e} "
+             f"| final maxabs {fma:.3e} rel {frl:.3e}")
+        assert ma <= MAXABS and rl <= RELL2
+        assert fma <= MAXABS and frl <= RELL2
 
 
 def test_split_rounding_ties():
