@@ -64,7 +64,7 @@ extern "C" {
 /* packed sequences: seq_idx [B, L] gives every token's sequence id (the
  * seq_idx argument of the reference's Triton port,
  * mamba_triton_ascend/mamba2/ops/triton/ssd_combined.py:359-409);
- * forward: headdim 64 with dstate 64 or 128; backward: with SAVED_STATES */
+ * forward: headdim 64 with dstate 64 or 128; backward: headdim = dstate = 64 */
 #define MAMBA2_SSD_HAS_SEQ_IDX (1u << 7)
 /* forward: also write the state at the end of every sequence of a batch-1
  * input split by cu_seqlens (ssd_combined.py:406-409, chunk_state_varlen);
@@ -129,8 +129,7 @@ typedef struct Mamba2SsdBwdArgs {
     float *dx, *ddt, *dA, *dB, *dC;
     float *dD, *dz, *ddt_bias, *dinitial_states; /* required iff the feature is flagged */
     /* member below added in ABI 4 */
-    const int32_t *seq_idx;    /* [B, L] iff HAS_SEQ_IDX (the forward's ids; needs
-                                  SAVED_STATES from that forward), else NULL */
+    const int32_t *seq_idx;    /* [B, L] iff HAS_SEQ_IDX (the forward's ids), else NULL */
 } Mamba2SsdBwdArgs;
 
 /* Bytes of device workspace mamba2_ssd_fwd needs for this shape/flags

@@ -9,7 +9,8 @@ package loads the HIP library (no GPU work) and registers the
 """
 
 from ._runtime import LIBRARY_PATH, load_library
-from .mamba2 import mamba2_ssd_fwd, mamba_chunk_scan_combined, register_ops
+from .mamba2 import (TrainingPolicy, get_training_policy, mamba2_ssd_fwd, mamba_chunk_scan_combined,
+                     register_ops, set_training_policy, training_policy)
 from .modules import SsdCore
 from .selective_state_update import selective_state_update
 
@@ -17,4 +18,5 @@ load_library()
 register_ops()
 
 __all__ = ["mamba2_ssd_fwd", "mamba_chunk_scan_combined", "selective_state_update", "SsdCore",
+           "TrainingPolicy", "get_training_policy", "set_training_policy", "training_policy",
            "load_library", "LIBRARY_PATH"]

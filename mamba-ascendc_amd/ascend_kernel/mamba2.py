@@ -21,9 +21,12 @@ path: CPU tensors are rejected.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import dataclasses
 import math
-from typing import Optional, Tuple, Union
+import threading
+from typing import Iterator, Optional, Tuple, Union
 
 import torch
 
@@ -327,8 +330,6 @@ def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bia
         if tuple(chunk_states.shape) != want:
             raise RuntimeError(f"{op}: chunk_states must have shape [B,H,ceil(L/64),P,N] = {list(want)}")
     if seq_idx is not None:
-        if chunk_states is None:
-            raise RuntimeError(f"{op}: seq_idx needs the packed forward's chunk_states")
         seq_idx = _check_seq_idx(x, seq_idx, chunk_size, B)
     grads = _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
                      chunk_size, dt_softplus, dt_limit_min, dt_limit_max,
@@ -393,6 +394,57 @@ def register_ops() -> None:
     _OPS_DEFINED = True
 
 
+# ----------------------------------------------------------------------------- training policy
+
+@dataclasses.dataclass(frozen=True)
+class TrainingPolicy:
+    """What the training forward keeps for the M1 backward.
+
+    ``save_chunk_states``: keep the state entering every 64-token chunk
+    (B*H*ceil(L/64)*P*N fp32, 2 GiB at [8,4096,256,64,64]) from the forward to
+    the backward (True, the default: the training forward writes them in the
+    same pass, about +0.3 ms at that size), or let the backward recompute them
+    with one extra streaming pass over x, dt and B (False: that memory is not
+    held between the passes).  This is the reference's save/recompute switch for
+    ``states_start`` (mamba_ascendc/python/ascend_kernel/ascend_kernel/mamba2.py:
+    1682-1697, ``MAMBA_ASCENDC_SAVE_STATES_START``), as an object instead of an
+    environment variable.  The gradients do not depend on the choice.
+    """
+
+    save_chunk_states: bool = True
+
+
+_policy_lock = threading.Lock()
+_policy = TrainingPolicy()
+
+
+def get_training_policy() -> TrainingPolicy:
+    """The policy new training calls use."""
+    return _policy
+
+
+def set_training_policy(policy: TrainingPolicy) -> TrainingPolicy:
+    """Make ``policy`` the default for new training calls; returns the old one."""
+    global _policy
+    if not isinstance(policy, TrainingPolicy):
+        raise TypeError("set_training_policy expects a TrainingPolicy")
+    with _policy_lock:
+        old, _policy = _policy, policy
+    return old
+
+
+@contextlib.contextmanager
+def training_policy(**fields) -> Iterator[TrainingPolicy]:
+    """``with training_policy(save_chunk_states=False): ...`` -- the policy with
+    the given fields changed, for the calls inside the block."""
+    new = dataclasses.replace(_policy, **fields)
+    old = set_training_policy(new)
+    try:
+        yield new
+    finally:
+        set_training_policy(old)
+
+
 # ----------------------------------------------------------------------------- autograd
 
 def _requires_grad(*values) -> bool:
@@ -416,26 +468,30 @@ def _can_use_native_bwd_m1(x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_st
 
 
 class _Mamba2SsdAutogradM1(torch.autograd.Function):
-    """Autograd contract of mamba2.py:1661-1838: saves the inputs, the
-    chunk-start states (and pre_gate with z), recomputes the other forward
-    intermediates in backward, returns 13 gradients (plus None for the
-    packed-sequence arguments ``seq_idx`` / ``cu_seqlens``, the Triton port's
-    extension, ssd_combined.py:612-637).  The third output, the varlen
-    states, is not differentiable (that port's backward rejects it)."""
+    """Autograd contract of mamba2.py:1661-1838: saves the inputs (and
+    pre_gate with z), and the chunk-start states unless the training policy
+    says to recompute them, recomputes the other forward intermediates in
+    backward, returns 13 gradients (plus None for the packed-sequence arguments
+    ``seq_idx`` / ``cu_seqlens``, the Triton port's extension,
+    ssd_combined.py:612-637, and for ``save_states``).  The third output, the
+    varlen states, is not differentiable (that port's backward rejects it)."""
 
     @staticmethod
     def forward(ctx, x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus,
-                dt_limit_min, dt_limit_max, initial_states, seq_idx=None, cu_seqlens=None):
+                dt_limit_min, dt_limit_max, initial_states, seq_idx=None, cu_seqlens=None,
+                save_states=True):
         _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
                       initial_states, dt_limit_min, dt_limit_max)
         # the pre-gate output y + D x is saved when z is present (dz needs it),
-        # as the reference's Train forward does (mamba2.py:1682-1770)
-        # and so are the chunk-start states (the reference's training forward
-        # returns states_start for its backward, mamba2.py:228,322,408-418)
+        # as the reference's Train forward does (mamba2.py:1682-1770), and the
+        # chunk-start states when the policy keeps them (the reference's
+        # training forward returns states_start for its backward,
+        # mamba2.py:228,322,408-418); varlen states are read from them
         out, final_state, pre_gate, states, varlen = _fwd_raw(
             x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
             float(dt_limit_min), float(dt_limit_max), want_final=True,
-            want_pre_gate=z is not None, want_states=True, seq_idx=seq_idx, cu_seqlens=cu_seqlens)
+            want_pre_gate=z is not None, want_states=bool(save_states), seq_idx=seq_idx,
+            cu_seqlens=cu_seqlens)
         empty = x.new_empty(0)
         ctx.save_for_backward(
             x, dt, A, B, C,
@@ -444,11 +500,11 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
             dt_bias if dt_bias is not None else empty,
             initial_states if initial_states is not None else empty,
             pre_gate if pre_gate is not None else empty,
-            states,
+            states if states is not None else empty,
             seq_idx if seq_idx is not None else empty,
         )
         ctx.has = (D is not None, z is not None, dt_bias is not None, initial_states is not None,
-                   seq_idx is not None)
+                   seq_idx is not None, states is not None)
         ctx.chunk_size = int(chunk_size)
         ctx.dt_softplus = bool(dt_softplus)
         ctx.dt_limit = (float(dt_limit_min), float(dt_limit_max))
@@ -460,20 +516,21 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, dfinal_state, _dvarlen):
         x, dt, A, B, C, D, z, dt_bias, initial_states, pre_gate, states, seq_idx = ctx.saved_tensors
-        has_D, has_z, has_bias, has_init, has_seq = ctx.has
+        has_D, has_z, has_bias, has_init, has_seq, has_states = ctx.has
         if dout is None:
             dout = torch.zeros_like(x)
         grads = torch.ops.mamba_ascend.mamba2_ssd_bwd_m1(
             x, dt, A, B, C, dout.contiguous(),
             None if dfinal_state is None else dfinal_state.contiguous(),
             D if has_D else None, z if has_z else None, dt_bias if has_bias else None,
-            initial_states if has_init else None, pre_gate if has_z else None, states,
+            initial_states if has_init else None, pre_gate if has_z else None,
+            states if has_states else None,
             ctx.chunk_size, ctx.dt_softplus, ctx.dt_limit[0], ctx.dt_limit[1],
             seq_idx if has_seq else None)
         dx, ddt, dA, dB, dC, dD, dz, ddt_bias, dinit = grads
         return (dx, ddt, dA, dB, dC, None,
                 dD if has_D else None, dz if has_z else None, ddt_bias if has_bias else None,
-                None, None, None, dinit if has_init else None, None, None)
+                None, None, None, dinit if has_init else None, None, None, None)
 
 
 # ----------------------------------------------------------------------------- public API
@@ -497,6 +554,7 @@ def mamba2_ssd_fwd(
     cu_seqlens: Optional[torch.Tensor] = None,
     return_varlen_states: bool = False,
     return_final_states: Optional[bool] = None,
+    save_chunk_states: Optional[bool] = None,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, ...]]:
     """Mamba-2 SSD forward (chunked selective scan) on MI355X.
 
@@ -516,6 +574,11 @@ def mamba2_ssd_fwd(
     Both need headdim 64 with dstate 64 or 128 (gradients: dstate 64); varlen
     states also a chunk_size that is a multiple of 64 and are not
     differentiable.
+
+    ``save_chunk_states`` (keyword-only, training calls): keep the chunk-start
+    states for the backward (True) or recompute them there (False); None takes
+    the current ``TrainingPolicy`` (``set_training_policy`` /
+    ``training_policy``).
     """
     register_ops()
     if return_final_states is not None:
@@ -531,9 +594,10 @@ def mamba2_ssd_fwd(
                 "mamba2_ssd_fwd backward requires contiguous FP32 GPU tensors with "
                 "headdim == dstate == 64"
             )
+        save = _policy.save_chunk_states if save_chunk_states is None else bool(save_chunk_states)
         out, final_state, varlen = _Mamba2SsdAutogradM1.apply(
             x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus, lo, hi, initial_states,
-            seq32, cu32)
+            seq32, cu32, save)
         if cu32 is not None:
             return (out, final_state, varlen) if return_final_state else (out, varlen)
     else:

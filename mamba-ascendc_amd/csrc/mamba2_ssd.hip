@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/mamba2_ssd.h"
 #include "ssd_bwd_fused.h"
@@ -398,12 +399,15 @@ bool bwd_fused_rev(const Mamba2SsdShape *s) {
     return (R == 1 || R == 2 || R == 4) && s->batch * s->ngroups >= kMinFusedStreams;
 }
 
-// Backward workspace: states [B,H,K,P,N] (unless SAVED_STATES) | log decay [B,H,K]
-// | dstates [B,H,K,P,N] (unless the reverse fused path runs)
-// | dA partials [B,H,K] | ddt_bias partials [B,H,K,slots] | dD partials
-// [B,H,K,slots,P] (slots = one per consumer wave of the chunk kernel).
+// Backward workspace: states [B,H,K,P,N] and, for the recompute of long
+// sequences with few streams, the forward plan's segment states and log decays
+// (both unless SAVED_STATES) | log decay [B,H,K] | dstates [B,H,K,P,N] (unless
+// the reverse fused path runs) | dA partials [B,H,K] | ddt_bias partials
+// [B,H,K,slots] | dD partials [B,H,K,slots,P] (slots = one per consumer wave
+// of the chunk kernel).
 struct BwdLayout {
-    size_t states, log_decay, dstates, part_dA, part_db, part_dD, total;
+    size_t states, seg_state, seg_decay, log_decay, dstates, part_dA, part_db, part_dD, total;
+    FwdPlan recompute; // plan of the state recompute (when the states are not passed in)
 };
 
 BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
@@ -412,7 +416,17 @@ BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
     BwdLayout l{};
     size_t off = 0;
     l.states = off; // absent when the forward's chunk states are passed in
-    if (!(flags & MAMBA2_SSD_SAVED_STATES)) off += align256(bhk * pn * sizeof(float));
+    if (!(flags & MAMBA2_SSD_SAVED_STATES)) {
+        off += align256(bhk * pn * sizeof(float));
+        l.recompute = fwd_plan(s, 0);
+        if (l.recompute.nseg > 1) {
+            const size_t units = (size_t)s->batch * s->nheads * l.recompute.nseg;
+            l.seg_state = off;
+            off += align256(units * pn * sizeof(float));
+            l.seg_decay = off;
+            off += align256(units * sizeof(float));
+        }
+    }
     l.log_decay = off;
     off += align256(bhk * sizeof(float));
     l.dstates = off;
@@ -475,9 +489,6 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
                     "chunk_states pointer and SAVED_STATES flag disagree");
     if (bool(f & MAMBA2_SSD_HAS_SEQ_IDX) != (a->seq_idx != nullptr))
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "seq_idx pointer and HAS_SEQ_IDX flag disagree");
-    if ((f & MAMBA2_SSD_HAS_SEQ_IDX) && !(f & MAMBA2_SSD_SAVED_STATES))
-        return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
-                    "HAS_SEQ_IDX needs SAVED_STATES (the chunk states of the packed forward)");
     if (f & MAMBA2_SSD_VARLEN_STATES)
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "VARLEN_STATES is a forward-only flag");
     if (!bwd_supported(s))
@@ -513,6 +524,7 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     fp.G = (int)s->ngroups;
     fp.R = (int)(s->nheads / s->ngroups);
     fp.K = K;
+    fp.hdiv = 1; // heads are not split here (headdim 64)
     fp.softplus = (f & MAMBA2_SSD_DT_SOFTPLUS) != 0;
     fp.lo = a->dt_limit_min;
     fp.hi = a->dt_limit_max;
@@ -559,12 +571,33 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     const dim3 state_grid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * H);
     if (int rc = record(tr, st, nullptr)) return rc;
     if (!saved) {
-        // forward recompute of the chunk-start states
-        hipLaunchKernelGGL((ssd::k_chunk_state<64, 64>), chunk_grid, dim3(ssd::kThreads), 0, st, fp);
-        if (int rc = launch_status("k_chunk_state", tr, st)) return rc;
-        hipLaunchKernelGGL(ssd::k_state_pass, state_grid, dim3(ssd::kThreads), 0, st, fp.states,
-                           fp.chunk_log_decay, fp.init, fp.states, (float *)nullptr, K, PN);
-        if (int rc = launch_status("k_state_pass", tr, st)) return rc;
+        // recompute of the chunk-start states by the fused forward's state
+        // pass (x, dt and B streamed once, the states written once); with
+        // segments, their contributions and the segment recurrence first
+        ssd::FwdParams kp = fp;
+        kp.seq_idx = a->seq_idx;
+        ssd::FwdParams sp_prm = fp;
+        sp_prm.chunk_states = fp.states;
+        sp_prm.seq_idx = a->seq_idx;
+        ssd::SegParams sp{};
+        sp.nseg = lay.recompute.nseg;
+        sp.M = lay.recompute.M;
+        sp.nsplit = 1;
+        const unsigned units = (unsigned)(B * H * sp.nseg);
+        const bool seq = a->seq_idx != nullptr;
+        if (sp.nseg > 1) {
+            sp.seg_state = (float *)(ws + lay.seg_state);
+            sp.seg_log_decay = (float *)(ws + lay.seg_decay);
+            ssd::launch_fwd_seg(true, false, false, seq, dim3(units), st, kp, sp);
+            if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
+            hipLaunchKernelGGL(ssd::k_state_pass, dim3((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * H),
+                               dim3(ssd::kThreads), 0, st, sp.seg_state, sp.seg_log_decay, fp.init,
+                               sp.seg_state, (float *)nullptr, sp.nseg, PN);
+            if (int rc = launch_status("k_state_pass", tr, st)) return rc;
+            sp.seg_in = sp.seg_state;
+        }
+        ssd::launch_fwd_seg(true, true, false, seq, dim3(units), st, sp_prm, sp);
+        if (int rc = launch_status("k_fwd_seg_state_save", tr, st)) return rc;
     }
     const int64_t bg = (int64_t)B * s->ngroups;
     if (bwd_fused_rev(s)) {
@@ -583,7 +616,7 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
                                    a->dfinal_state, a->dinitial_states);
         if (int rc = launch_status("k_bwd_dstate_rev", tr, st)) return rc;
     } else {
-        hipLaunchKernelGGL(ssd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);
+        hipLaunchKernelGGL(ssd::bwd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);
         if (int rc = launch_status("k_bwd_dstate", tr, st)) return rc;
         hipLaunchKernelGGL(ssd::k_state_pass_bwd, state_grid, dim3(ssd::kThreads), 0, st, bp.dstates,
                            fp.chunk_log_decay, a->dfinal_state, a->dinitial_states, K, PN);

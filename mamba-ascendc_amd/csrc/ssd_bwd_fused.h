@@ -39,6 +39,7 @@
 
 #include <type_traits>
 
+#include "ssd_bf16.h"
 #include "ssd_bwd_kernels.h"
 #include "ssd_fwd_fused.h"
 
@@ -46,6 +47,10 @@ namespace ssd {
 
 constexpr int kBwsThreads = 512;  // 4 consumer + 4 producer waves
 constexpr int kBwsSlots = 4;      // partial sums per (b, h, k): one per consumer wave
+
+// The chunk kernels below use split-bf16 operands (ssd_bf16.h): the upstream
+// gradient of a mean-reduced loss is far below fp16's range.
+namespace bwd {
 
 // kRevR = 0: steps in chunk order, the state gradients dU_k read from
 // prm.dstates.  kRevR = R (1, 2 or 4 heads per group, one run per stream):
@@ -71,7 +76,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     constexpr int TS = kSeq ? T : 1;
     // x and gy tiles double buffered by step parity (the epilogue of step n
     // still reads them while step n + 1 runs); S, dU, B, C single
-    __shared__ __attribute__((aligned(16))) _Float16 lds[16 * kTile];
+    __shared__ __attribute__((aligned(16))) __bf16 lds[16 * kTile];
     // The per-token arrays are aligned above the tile array so the LDS layout
     // places them first, below 64 KB: their lane addresses then share one
     // base register with 16-bit immediate offsets instead of one register each.
@@ -219,15 +224,12 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             }
         };
         auto put = [&](SplitTile d, int row, float4 v) __attribute__((always_inline)) {
-            half4 vh, vl;
-            split4(v, vh, vl);
-            *(half4 *)&d.hi[row * kTS + c4] = vh;
-            *(half4 *)&d.lo[row * kTS + c4] = vl;
+            store_split4(d, row * kTS + c4, v);
         };
         auto stage_xg = [&](int n) __attribute__((always_inline)) {
             const int par = n & 1, k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
             const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
-            _Float16 *lp = opaque_lds(lds);
+            __bf16 *lp = opaque_lds_t(lds);
             const SplitTile xt = tile_at(lp, par), gt = tile_at(lp, 2 + par);
             const auto rdz = buf_rsrc(kHasZ ? prm.dz + xo : prm.x + xo);
             float4 dD4 = z4; // sum over this lane's rows of x gy, columns c4 .. c4 + 3
@@ -307,7 +309,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         };
         auto stage_bc = [&](int n) __attribute__((always_inline)) {
             const int tv = tvalid(chunk_of(min(n, NS - 1)));
-            _Float16 *lp = opaque_lds(lds);
+            __bf16 *lp = opaque_lds_t(lds);
             const SplitTile bt = tile_at(lp, 6), ct = tile_at(lp, 7);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -332,15 +334,12 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         // dSoff^T[n][p] = sum_t (exp2(cs_t) C_t[n]) gy_t[p] from the C and gy
         // tiles the consumers read in the same phase
         auto put_acc = [&](SplitTile d, int pb, f32x4 v) __attribute__((always_inline)) {
-            half4 vh, vl;
-            split4(make_float4(v[0], v[1], v[2], v[3]), vh, vl);
-            *(half4 *)&d.hi[(16 * pb + r16) * kTS + 16 * pw + 4 * kq] = vh;
-            *(half4 *)&d.lo[(16 * pb + r16) * kTS + 16 * pw + 4 * kq] = vl;
+            store_split4(d, (16 * pb + r16) * kTS + 16 * pw + 4 * kq, make_float4(v[0], v[1], v[2], v[3]));
         };
         auto stage_su_rev = [&](int n, auto slot_c) __attribute__((always_inline)) {
             constexpr int rr = decltype(slot_c)::value;
             const int par = n & 1;
-            _Float16 *lp = opaque_lds(lds);
+            __bf16 *lp = opaque_lds_t(lds);
             const SplitTile st_ = tile_at(lp, 4), ut = tile_at(lp, 5), ct = tile_at(lp, 7);
             float sdu = 0.f;
 #pragma unroll
@@ -507,7 +506,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             const float Ah = s_A[par];
             const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
             f32x4 xa[4], ga[4], Dv[4];
-            _Float16 *le = opaque_lds(lds);
+            __bf16 *le = opaque_lds_t(lds);
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
                 xa[pb] = tile_row4(tile_at(le, par), own, 16 * pb + cq);
@@ -553,7 +552,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         for (int n = 0; n < NS; ++n) {
             const int k = chunk_of(n), r = n % R, par = n & 1;
             if (n > 0) epilogue(n - 1);
-            _Float16 *la = opaque_lds(lds);
+            __bf16 *la = opaque_lds_t(lds);
             const SplitTile xt = tile_at(la, par), gt = tile_at(la, 2 + par);
             const SplitTile Bt = tile_at(la, 6), Ct = tile_at(la, 7);
 
@@ -680,7 +679,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             lds_barrier(); // S, dU staged; B, C of the next chunk may now be staged
 
             // ---------------- phase B: S, dU (x, gy of this step are still in LDS)
-            _Float16 *lb = opaque_lds(lds);
+            __bf16 *lb = opaque_lds_t(lds);
             const SplitTile xb = tile_at(lb, par), gb = tile_at(lb, 2 + par);
             const SplitTile St = tile_at(lb, 4), Ut = tile_at(lb, 5);
             const float q_o = s_q[par][own], dte_o = s_dte[par][own], ecs_o = s_ecs[par][own];
@@ -788,7 +787,7 @@ template <bool kHasZ, bool kSeq = false>
 __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, const float *dfinal,
                                                                 float *dinit) {
     constexpr int T = 64, P = 64, N = 64;
-    __shared__ __attribute__((aligned(16))) _Float16 lds[8 * kTile]; // GE(s), CT(s), s = 0, 1
+    __shared__ __attribute__((aligned(16))) __bf16 lds[8 * kTile]; // GE(s), CT(s), s = 0, 1
     __shared__ float s_alpha[2];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -843,12 +842,7 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
                 sprv[sl] = t0 > 0 ? pv : 0;
             }
         };
-        auto put = [&](SplitTile d, int row, float4 v) {
-            half4 vh, vl;
-            split4(v, vh, vl);
-            *(half4 *)&d.hi[row * kTS + c4] = vh;
-            *(half4 *)&d.lo[row * kTS + c4] = vl;
-        };
+        auto put = [&](SplitTile d, int row, float4 v) { store_split4(d, row * kTS + c4, v); };
         auto p_stage = [&](int i, int s, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
             const int tv = i < K ? tvalid(K - 1 - i) : 0; // nothing valid past the first chunk
@@ -953,6 +947,8 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
                 make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
     }
 }
+
+}  // namespace bwd
 
 // fixed-order reductions of the per-chunk partials, one workgroup per head:
 // dA from [B, H, K], ddt_bias and dD from [B, H, K, slots] (dD per channel:

@@ -22,6 +22,7 @@
 // and layouts are this file's own.
 #pragma once
 
+#include "ssd_bf16.h"
 #include "ssd_fwd_kernels.h"
 
 namespace ssd {
@@ -66,13 +67,15 @@ __device__ __forceinline__ float bwd_prologue(const BwdParams &p, int b, int h, 
 
 
 // --------------------------------------------------------------------------
-// dSoff_k = (gy * exp(cs))^T C, one workgroup per (k, h, b)
+// dSoff_k = (gy * exp(cs))^T C, one workgroup per (k, h, b); split-bf16
+// operands (ssd_bf16.h)
 // --------------------------------------------------------------------------
 #ifndef SSD_KERNEL_TEMPLATES_ONLY
+namespace bwd {
 __global__ __launch_bounds__(kThreads) void k_bwd_dstate(BwdParams prm) {
     constexpr int P = 64, N = 64, T = 64;
     __shared__ float s_q[T], s_cs[T], s_dqdu[T], s_e[T];
-    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * kTile];
+    __shared__ __attribute__((aligned(16))) __bf16 lds[4 * kTile];
 
     const int k = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -132,6 +135,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dstate(BwdParams prm) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) out[(16 * w + 4 * kq + r) * N + 16 * nb + r16] = acc[nb][r];
 }
+}  // namespace bwd
 #endif
 
 // --------------------------------------------------------------------------

@@ -20,12 +20,12 @@ constexpr bool kZ = SSD_BWD_Z != 0;
 
 template <int kR, bool kSeq>
 void run_ws(dim3 grid, hipStream_t st, const BwdParams &bp, int nseg, int M) {
-    hipLaunchKernelGGL((k_bwd_ws<kZ, kR, kSeq>), grid, dim3(kBwsThreads), 0, st, bp, nseg, M);
+    hipLaunchKernelGGL((bwd::k_bwd_ws<kZ, kR, kSeq>), grid, dim3(kBwsThreads), 0, st, bp, nseg, M);
 }
 
 template <bool kSeq>
 void run_rev(dim3 grid, hipStream_t st, const BwdParams &bp, const float *dfinal, float *dinit) {
-    hipLaunchKernelGGL((k_bwd_dstate_rev<kZ, kSeq>), grid, dim3(kWsThreads), 0, st, bp, dfinal, dinit);
+    hipLaunchKernelGGL((bwd::k_bwd_dstate_rev<kZ, kSeq>), grid, dim3(kWsThreads), 0, st, bp, dfinal, dinit);
 }
 
 }  // namespace

@@ -93,7 +93,10 @@ __device__ __forceinline__ int xcd_unit(int id, int total, int R) {
 
 constexpr int kWsThreads = 512; // 4 producer + 4 consumer waves
 
-// kSave: also write the state entering every chunk to prm.chunk_states.
+// kSave: also write the state entering every chunk to prm.chunk_states; with
+// kStateOnly, a state pass that starts each segment from its entering state
+// (sp.seg_in, or the initial states) and writes only those chunk states (the
+// backward's recompute of the states it was not given).
 // kGate: the z gate (prm.has_z), whose z rows the consumers prefetch a chunk ahead.
 // kSeq: packed sequences (prm.seq_idx).
 template <bool kStateOnly, bool kSave = false, bool kGate = false, bool kSeq = false>
@@ -334,7 +337,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
 
         {
             const float *s0 = nullptr;
-            if (!kStateOnly) {
+            if (!kStateOnly || kSave) {
                 if (sp.seg_in)
                     s0 = sp.seg_in + (((int64_t)b * H + h) * sp.nseg + sg) * PNS + n0;
                 else if (prm.init)
@@ -521,7 +524,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         }
 
         float *dst = nullptr;
-        if (kStateOnly) {
+        if (kStateOnly && !kSave) {
             const int64_t si = ((int64_t)b * H + h) * sp.nseg + sg;
             dst = sp.seg_state + si * PNS + n0;
             // natural units; -inf (a factor of 0) where the state was cut

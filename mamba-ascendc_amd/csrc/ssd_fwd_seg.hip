@@ -20,7 +20,10 @@ using Run = void (*)(dim3, hipStream_t, const FwdParams &, const SegParams &);
 void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
                     const FwdParams &kp, const SegParams &sp) {
     if (state_only) {
-        (seq ? run<true, false, false, true> : run<true, false, false, false>)(grid, st, kp, sp);
+        if (save)
+            (seq ? run<true, true, false, true> : run<true, true, false, false>)(grid, st, kp, sp);
+        else
+            (seq ? run<true, false, false, true> : run<true, false, false, false>)(grid, st, kp, sp);
         return;
     }
     static const Run full[8] = {

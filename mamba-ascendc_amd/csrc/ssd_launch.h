@@ -12,7 +12,7 @@ namespace ssd {
 
 struct SegParams;
 
-// k_fwd_seg<state_only, save, gate, seq> (state_only excludes save and gate)
+// k_fwd_seg<state_only, save, gate, seq> (state_only excludes gate)
 void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
                     const FwdParams &kp, const SegParams &sp);
 

@@ -3,11 +3,14 @@
 The oracle (oracle/ssd_reference.py, pinned in tests/test_oracle.py against an
 independent float64 adjoint recurrence and finite differences) is run with
 torch autograd on the same seeded inputs.  Small cases use float64 on the CPU
-and a tight relative-L2 bound (the split-fp16 MFMA scheme keeps about 22 bits
-per operand); the BASELINE M1 configuration [4,2048,16,64,64,64,4] uses the
-fp32 oracle, the loss mean(y^2) + mean(final^2), and the contract bound
-rel-L2 <= 5e-3 on every gradient (the reference's own gate is NRMSE <= 8e-3,
-mamba_ascendc/tests/test_mamba2_ssd_bwd_m1.py:161-165).
+and a tight relative-L2 bound (the backward's split-bf16 MFMA operands keep
+about 17 bits over the whole fp32 exponent range); the BASELINE M1
+configuration [4,2048,16,64,64,64,4] is checked with the loss mean(y^2) +
+mean(final^2), whose upstream gradients are O(1 / numel), against the fp32
+oracle at the contract bound rel-L2 <= 5e-3 (the reference's own gate is
+NRMSE <= 8e-3, mamba_ascendc/tests/test_mamba2_ssd_bwd_m1.py:161-165) and
+against the float64 oracle at the bound of the small cases; config 3 the same
+way on independent slices.
 """
 
 import math
@@ -140,9 +143,11 @@ def _oracle_loss_grads(inp, dtype):
     return {k: v.grad for k, v in lv.items()}
 
 
-# rel-L2 of the GPU gradients against the float64 oracle at config 4 (the
-# bound of the small float64 cases)
-C4_REL_VS_FP64 = 2e-4
+# rel-L2 of the GPU gradients against the oracle at configs 4 and 3: the
+# split-bf16 backward measures 3e-6 .. 4.3e-6 on dx, ddt, dB, dC (5e-8 on dA)
+# at the BASELINE loss, and the same with the upstream gradients scaled by
+# 2^16 or 2^24 (scale-independent)
+TIGHT_REL = 5e-5
 
 
 def test_backward_baseline_config4():
@@ -173,7 +178,7 @@ def test_backward_baseline_config4():
         _say(f"  d{k:<3} vs fp32 oracle: maxabs {ma:.3e} relL2 {rl:.3e} | vs fp64: maxabs "
              f"{ma64:.3e} relL2 {rl64:.3e} cos {cos:.9f} | fp32 oracle vs fp64: relL2 {rl_oracle:.3e}")
         assert rl <= 5e-3 and ma <= 2e-2, (k, ma, rl)
-        assert rl64 <= C4_REL_VS_FP64 and ma64 <= 2e-2, (k, ma64, rl64)
+        assert rl64 <= TIGHT_REL and ma64 <= 2e-2, (k, ma64, rl64)
         assert cos >= 0.999, (k, cos)
 
 
@@ -218,6 +223,7 @@ def test_backward_baseline_config3_slices():
             _say(f"  batch {bi} d{k:<3} maxabs {ma:.3e} (max |want| {lv[k].grad.abs().max():.3e}) "
                  f"relL2 {rl:.3e} cos {cos:.9f}")
             assert rl <= 5e-3 and ma <= 2e-2 and cos >= 0.999, (bi, k, ma, rl, cos)
+            assert rl <= TIGHT_REL, (bi, k, rl)
 
 
 def test_forward_chunk_states_are_prefix_final_states():
@@ -305,3 +311,47 @@ def test_ssdcore_module_trains():
         _, rl = parity_metrics(leaves[k].grad.cpu(), ref[k].grad)
         _say(f"  SsdCore d{k:<8} relL2 {rl:.3e}")
         assert rl <= 2e-4, (k, rl)
+
+
+@pytest.mark.parametrize("shape,features,packed", [
+    ([2, 700, 8, 64, 64, 64, 2], ("D", "z", "bias", "init"), False),    # split path, segmented recompute
+    ([4, 330, 256, 64, 64, 64, 64], ("D2", "bias"), False),            # fused reverse, one segment
+    ([2, 400, 16, 64, 64, 128, 4], ("z", "init"), True),               # packed sequences
+], ids=["split-segments", "fused-reverse", "packed"])
+def test_training_policy_recompute_matches_saved(shape, features, packed):
+    """The save-vs-recompute policy (TrainingPolicy.save_chunk_states) changes
+    what autograd keeps between the passes, not the gradients: the backward
+    that recomputes the chunk-start states runs the forward's own state pass, so
+    the gradients are bitwise those of the backward that reads the saved ones."""
+    _need_gpu()
+    import ascend_kernel
+
+    b, l, h, p, n, chunk, g = shape
+    _say(f"training policy {shape} {features} packed={packed}")
+    inp = make_inputs(shape, seed=41, features=features)
+    gen = torch.Generator().manual_seed(8)
+    gy = torch.randn(b, l, h, p, generator=gen).cuda()
+    gf = torch.randn(b, h, p, n, generator=gen).cuda()
+    ids = None
+    if packed:
+        cuts = torch.sort(torch.randint(1, l, (b, 3), generator=gen), dim=1).values
+        ids = (torch.arange(l)[None, :, None] >= cuts[:, None, :]).sum(-1).to(torch.int32).cuda()
+
+    def grads(**kw):
+        leaves = {k: v.cuda().requires_grad_(True) for k, v in inp.items()}
+        out, fin = ascend_kernel.mamba2_ssd_fwd(
+            leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], chunk,
+            D=leaves.get("D"), z=leaves.get("z"), dt_bias=leaves.get("dt_bias"), dt_softplus=True,
+            initial_states=leaves.get("initial_states"), return_final_state=True, seq_idx=ids, **kw)
+        torch.autograd.backward((out, fin), (gy, gf))
+        torch.cuda.synchronize()
+        return {k: v.grad.cpu() for k, v in leaves.items()}
+
+    saved = grads(save_chunk_states=True)
+    recomputed = grads(save_chunk_states=False)
+    with ascend_kernel.training_policy(save_chunk_states=False):
+        by_policy = grads()
+    for k in inp:
+        assert torch.isfinite(saved[k]).all(), k
+        assert torch.equal(saved[k], recomputed[k]), k
+        assert torch.equal(saved[k], by_policy[k]), k

@@ -393,3 +393,30 @@ def test_struct_layouts_match_ctypes(tmp_path):
         assert int(got[n]) == ctypes.sizeof(cls), n
         for field in cls._fields_:
             assert int(got[f"{n}.{field[0]}"]) == getattr(cls, field[0]).offset, (n, field[0])
+
+
+def test_training_policy_object():
+    """TrainingPolicy: the default keeps the chunk states; set_training_policy
+    swaps the default and returns the old one; training_policy(...) changes it
+    for a block only; the public forward takes a per-call override."""
+    import inspect
+
+    import ascend_kernel
+
+    assert ascend_kernel.get_training_policy() == ascend_kernel.TrainingPolicy(save_chunk_states=True)
+    with ascend_kernel.training_policy(save_chunk_states=False) as pol:
+        assert pol.save_chunk_states is False
+        assert ascend_kernel.get_training_policy() is pol
+    assert ascend_kernel.get_training_policy().save_chunk_states is True
+    old = ascend_kernel.set_training_policy(ascend_kernel.TrainingPolicy(save_chunk_states=False))
+    try:
+        assert ascend_kernel.get_training_policy().save_chunk_states is False
+    finally:
+        ascend_kernel.set_training_policy(old)
+    with pytest.raises(TypeError):
+        ascend_kernel.set_training_policy(False)
+    with pytest.raises(TypeError):
+        with ascend_kernel.training_policy(no_such_field=True):
+            pass
+    sig = inspect.signature(ascend_kernel.mamba2_ssd_fwd)
+    assert sig.parameters["save_chunk_states"].kind is inspect.Parameter.KEYWORD_ONLY
