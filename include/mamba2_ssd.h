@@ -151,6 +151,25 @@ int mamba2_ssd_fwd_traced(const Mamba2SsdFwdArgs *args, void *workspace, size_t 
                           void *stream, void *const *events, int nevents, const char **names,
                           int *nkernels);
 
+/* Scratch size of mamba2_ssd_fwd_noalloc (40 MiB): enough for the segment
+ * states of every forward plan whose scratch is only those (headdim 64 m with
+ * dstate 64 or 128, any length). */
+#define MAMBA2_SSD_NOALLOC_SCRATCH_BYTES (40u << 20)
+
+/* Forward that allocates nothing and takes no workspace.  This entry point has
+ * no counterpart in the reference; it is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  Same arguments, results and kernels as mamba2_ssd_fwd;
+ * the scratch that call would take from its workspace (size given by
+ * mamba2_ssd_fwd_workspace_size) comes from a static device array of
+ * MAMBA2_SSD_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs
+ * on until the process ends (on the calling thread's current device, which
+ * must be the device of `stream`).  A forward that needs more scratch returns
+ * MAMBA2_SSD_ERR_WORKSPACE before any GPU work.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams, or two host
+ * threads, without ordering between them) race and must not be issued. */
+int mamba2_ssd_fwd_noalloc(const Mamba2SsdFwdArgs *args, void *stream);
+
 /* Bytes of device workspace mamba2_ssd_bwd_m1 needs for this shape/flags
  * (less with SAVED_STATES: the chunk states are not recomputed). */
 int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes);

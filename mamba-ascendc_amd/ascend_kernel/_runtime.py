@@ -31,6 +31,9 @@ VARLEN_STATES = 1 << 8
 SSU_TIED = 1 << 16
 SSU_STRIDES = 1 << 17
 
+# static device scratch of mamba2_ssd_fwd_noalloc (MAMBA2_SSD_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 40 << 20
+
 STATUS_NAMES = {
     0: "OK",
     -1: "INVALID_ARGUMENT",
@@ -124,6 +127,10 @@ EXPORTS = {
         [ctypes.POINTER(Mamba2SsdFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
          ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
          ctypes.POINTER(ctypes.c_int)],
+        ctypes.c_int,
+    ),
+    "mamba2_ssd_fwd_noalloc": (
+        [ctypes.POINTER(Mamba2SsdFwdArgs), ctypes.c_void_p],
         ctypes.c_int,
     ),
     "mamba2_ssd_bwd_m1_workspace_size": (

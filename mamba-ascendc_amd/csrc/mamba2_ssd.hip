@@ -794,6 +794,65 @@ int mamba2_selective_state_update(const Mamba2SsuArgs *a, void *stream) {
     return ok();
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward (mamba2_ssd_fwd_noalloc): the forward's scratch (the
+// segment states and log decays of long sequences with few streams, and the
+// other buffers fwd_plan lays out) comes from this file-scope device array
+// instead of a caller workspace.  Each GPU the library runs on holds its own
+// copy until the process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns for that device.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[MAMBA2_SSD_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the calling thread's current device, looked
+// up once per device with that device current.
+int scratch_for_current_device(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(MAMBA2_SSD_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "device %d: the allocation-free forward supports %d devices",
+                    dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(MAMBA2_SSD_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MAMBA2_SSD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mamba2_ssd_fwd_noalloc(const Mamba2SsdFwdArgs *a, void *stream) {
+    if (!a) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "args is NULL");
+    if (int rc = check_shape(&a->shape, a->flags)) return rc;
+    const size_t need = fwd_ws_bytes(&a->shape, a->flags);
+    if (need > (size_t)MAMBA2_SSD_NOALLOC_SCRATCH_BYTES)
+        return fail(MAMBA2_SSD_ERR_WORKSPACE,
+                    "this forward needs %zu bytes of scratch; mamba2_ssd_fwd_noalloc has %zu "
+                    "(use mamba2_ssd_fwd with a workspace)",
+                    need, (size_t)MAMBA2_SSD_NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    if (need)
+        if (int rc = scratch_for_current_device(&ws)) return rc;
+    return fwd_impl(a, ws, need ? (size_t)MAMBA2_SSD_NOALLOC_SCRATCH_BYTES : 0, stream, nullptr);
+}
+
 int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes) {
     if (int rc = check_shape(shape, flags)) return rc;
     if (!bytes) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "bytes is NULL");

@@ -395,6 +395,27 @@ def test_struct_layouts_match_ctypes(tmp_path):
             assert int(got[f"{n}.{field[0]}"]) == getattr(cls, field[0]).offset, (n, field[0])
 
 
+def test_noalloc_forward_limits_without_gpu():
+    """mamba2_ssd_fwd_noalloc: its scratch size is the header's, and a forward
+    whose scratch would exceed it is rejected with the workspace status before
+    any GPU work (here: varlen states without saved states, whose chunk states
+    of a 2^20-token sequence need 2 GiB)."""
+    text = open(HEADER).read()
+    m = re.search(r"#define MAMBA2_SSD_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == rt.NOALLOC_SCRATCH_BYTES
+    lib = rt.load_library()
+    assert lib.mamba2_ssd_fwd_noalloc(None, None) == -1
+    fake = ctypes.c_void_p(0x1000)
+    shape = _shape(batch=1, seqlen=1 << 20, nheads=8, ngroups=1)
+    need = ctypes.c_size_t(0)
+    assert lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shape), rt.VARLEN_STATES, ctypes.byref(need)) == 0
+    assert need.value > rt.NOALLOC_SCRATCH_BYTES
+    args = rt.Mamba2SsdFwdArgs(shape, rt.VARLEN_STATES, 0.0, math.inf, fake, fake, fake, fake, fake,
+                               None, None, None, None, fake, None, None, None, None, fake, 2, fake)
+    assert lib.mamba2_ssd_fwd_noalloc(ctypes.byref(args), None) == -3
+    assert "mamba2_ssd_fwd_noalloc" in rt.last_error(lib)
+
+
 def test_training_policy_object():
     """TrainingPolicy: the default keeps the chunk states; set_training_policy
     swaps the default and returns the old one; training_policy(...) changes it
