@@ -101,17 +101,25 @@ class HipEvents:
 # ----------------------------------------------------------------------------- work model
 
 def fwd_segments(shape):
-    """(nseg, nsplit) of the fused forward's plan (mamba2_ssd.hip fwd_plan):
-    dstate 128 runs as two state halves, and segments are added until there
-    are about 1024 (b, h, half) work units."""
+    """(nseg, nseg_pre, nsplit) of the fused forward's plan (mamba2_ssd.hip
+    fwd_plan): dstate 128 runs two workgroups per head; with fewer than 256
+    (b, h, half) streams the sequence is cut into segments (when that saves at
+    least 6 chunk steps), and the state-only pass runs on segments twice as
+    fine."""
     b, l, h, p, n, _chunk, g = shape
     k = math.ceil(l / EXEC_CHUNK)
     nsplit = n // 64
     streams = b * h * nsplit
-    nseg = 1 if streams >= 1024 else -(-1024 // streams)
+    nseg = 1 if streams >= 256 else -(-256 // streams)
     nseg = min(nseg, k)
-    m = -(-k // nseg)
-    return -(-k // m), nsplit
+    if k - math.ceil(k / nseg) < 6:
+        nseg = 1
+    if nseg == 1:
+        return 1, 1, nsplit
+    mt = math.ceil(k / nseg)
+    mult = min(2, mt)
+    mp = math.ceil(mt / mult)
+    return math.ceil(k / (mult * mp)), math.ceil(k / mp), nsplit
 
 
 def fwd_kernel_model(name: str, shape) -> dict:
@@ -137,29 +145,27 @@ def fwd_kernel_model(name: str, shape) -> dict:
         fl = 2 * T * p * n
     elif name == "k_state_pass":
         # between the fused forward's segments: segment states in and out
-        nseg, _ = fwd_segments(shape)
-        su = b * h * nseg
+        _, nseg_pre, _ = fwd_segments(shape)
+        su = b * h * nseg_pre
         per = f4 * (2 * p * n + 1)
         return {"bytes": su * per + b * h * p * n * f4, "flops": su * 2 * p * n, "units": su,
                 "bytes_per_unit": per}
-    elif name == "k_fwd_combine":
-        # dstate 128: the two halves' outputs in, the sum out
-        per = f4 * 3 * T * p
-        fl = T * p
-    elif name == "k_fwd_seg":
+    elif name in ("k_fwd_seg", "k_fwd_wide"):
         # fused: x, dt, B, C in, y out; the state stays on chip (segment
-        # entry/exit states are a few per stream and not counted)
+        # entry/exit states are a few per stream and not counted).  dstate
+        # 128 (k_fwd_wide) splits a head's channels over two workgroups,
+        # which share B and C through L2: the same bytes per (b, h, k)
         per = f4 * (2 * T * p + T + 2 * T * n / r)
         fl = 2 * (T * T * n / r + T * T * p + 2 * T * n * p)
-    elif name == "k_fwd_seg_save":
+    elif name in ("k_fwd_seg_save", "k_fwd_wide_save"):
         # training forward: as k_fwd_seg plus the state entering every chunk
         per = f4 * (2 * T * p + T + 2 * T * n / r + p * n)
         fl = 2 * (T * T * n / r + T * T * p + 2 * T * n * p)
-    elif name in ("k_fwd_seg_gate", "k_fwd_seg_save_gate"):
+    elif name in ("k_fwd_seg_gate", "k_fwd_seg_save_gate", "k_fwd_wide_gate", "k_fwd_wide_save_gate"):
         # z-gated forms: as k_fwd_seg / k_fwd_seg_save plus z in, and for
         # training the pre-gate output y + D x out (D, dt_bias and the
         # initial states are a few values per head or stream)
-        save = name == "k_fwd_seg_save_gate"
+        save = name.endswith("save_gate")
         per = f4 * ((4 if save else 3) * T * p + T + 2 * T * n / r + (p * n if save else 0))
         fl = 2 * (T * T * n / r + T * T * p + 2 * T * n * p)
     elif name == "k_fwd_seg_state":
@@ -358,6 +364,8 @@ def bench_config(torch, lib, rt, api, hip, cfg, steps, warmup):
            "op_bytes": nbytes, "workspace_bytes": ws_bytes, "finite": finite,
            "parity": parity_slices(torch, inp, out, final, shape, PARITY_SLICES[cfg])}
     del out, final
+    row["api_fwd_ms"] = round(bench_api(torch, api, inp, shape[5], max(5, steps // 3), 3), 5)
+    row["api_host_us"] = round(api_host_cost(torch, api, inp, shape[5]), 1)
     if shape[3] == 64 and shape[4] == 64:
         tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup)
         if tr is not None:
@@ -651,6 +659,26 @@ def bench_api(torch, api, inp, chunk, steps, warmup, run=5):
     return statistics.median(samples)
 
 
+def api_host_cost(torch, api, inp, chunk, calls=50):
+    """Host microseconds to issue one forward through the public Python API
+    (validation, workspace query through ctypes, output and workspace
+    allocation, the launch): wall time of `calls` calls queued back to back,
+    divided by `calls`.  When it is below the kernel time the host work hides
+    under the queued GPU work."""
+    def call():
+        return api.mamba2_ssd_fwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], chunk,
+                                  dt_softplus=True, return_final_state=True)
+    for _ in range(5):
+        call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        call()
+    host = (time.perf_counter() - t0) / calls
+    torch.cuda.synchronize()
+    return host * 1e6
+
+
 def bench_fwd_bwd(torch, api, inp, chunk, steps, warmup):
     """fwd + bwd through autograd; None if the backward is not available for
     this shape.  The upstream gradients are those of the loss
@@ -790,7 +818,7 @@ def cpu_baseline(torch, shape, seed, budget_s):
 def _short(name: str) -> str:
     """`ssd::k_chunk_scan<64, 64>(...)` -> `k_chunk_scan<64, 64>`."""
     base = name.split("(")[0].replace("void ", "").strip()
-    return base.replace("ssd::", "")
+    return base.replace("ssd::bwd::", "").replace("ssd::", "")
 
 
 def model_key(short: str) -> str:
@@ -802,6 +830,11 @@ def model_key(short: str) -> str:
     packed sequences.  k_bwd_ws<has z, heads per group, packed sequences>: a
     group size above 0 is the reverse fused k_bwd_ws_rev ("_z" with z, "_seq"
     with packed sequences).  The others drop their template arguments."""
+    if short.startswith("k_fwd_wide<"):
+        args = [a.strip() for a in short[len("k_fwd_wide<"):-1].split(",")]
+        key = "k_fwd_wide_save" if args[0] == "true" else "k_fwd_wide"
+        key = key + "_gate" if len(args) > 1 and args[1] == "true" else key
+        return key + ("_seq" if len(args) > 2 and args[2] == "true" else "")
     if short.startswith("k_fwd_seg<"):
         args = [a.strip() for a in short[len("k_fwd_seg<"):-1].split(",")]
         seq = "_seq" if len(args) > 3 and args[3] == "true" else ""
@@ -1117,7 +1150,9 @@ def main(argv=None):
                 continue
             row = bench_config(torch, lib, rt, api, hip, cfg, args.steps, args.warmup)
             others[f"C{cfg}"] = row
-            log(f"config C{cfg} {row['shape']}: forward {row['fwd_ms']:.4f} ms, {row['op_GB_s']:.0f} GB/s "
+            log(f"config C{cfg} {row['shape']}: forward {row['fwd_ms']:.4f} ms (public API "
+                f"{row['api_fwd_ms']:.4f} ms per call, {row['api_host_us']:.0f} us of host work per call), "
+                f"{row['op_GB_s']:.0f} GB/s "
                 f"({100 * row['hbm_roofline_frac']:.1f} % of 8 TB/s), parity "
                 f"{'pass' if row['parity']['pass'] else 'FAIL'} (out relL2 {row['parity']['out_relL2']:.2e})"
                 + (f"; training fwd {row['fwd_train_ms']:.4f} + bwd {row['bwd_ms']:.4f} ms"

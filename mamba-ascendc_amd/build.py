@@ -33,11 +33,13 @@ FLAGS = [
 
 
 # translation units (source, extra flags): the host code with the small
-# kernels, the fused-forward variants, and the backward variants with and
-# without the z gate; compiled in parallel, then linked into one library
+# kernels, the fused-forward variants (dstate 64 and dstate 128), and the
+# backward variants with and without the z gate; compiled in parallel, then
+# linked into one library
 UNITS = [
     ("mamba2_ssd.hip", []),
     ("ssd_fwd_seg.hip", []),
+    ("ssd_fwd_wide.hip", []),
     ("ssd_bwd_ws.hip", ["-DSSD_BWD_Z=0"]),
     ("ssd_bwd_ws.hip", ["-DSSD_BWD_Z=1"]),
 ]

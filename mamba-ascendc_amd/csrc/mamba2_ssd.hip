@@ -18,6 +18,7 @@
 #include "ssd_decode.h"
 #include "ssd_fwd_fused.h"
 #include "ssd_fwd_kernels.h"
+#include "ssd_fwd_wide.h"
 #include "ssd_launch.h"
 #include "ssd_varlen.h"
 
@@ -78,18 +79,34 @@ int check_shape(const Mamba2SsdShape *s, uint32_t flags) {
 
 int64_t nchunks(const Mamba2SsdShape *s) { return (s->seqlen + ssd::kChunk - 1) / ssd::kChunk; }
 
-// Forward plan.  headdim = 64 with dstate = 64 or 128 runs the fused
-// segment-serial kernel (dstate 128 as two 64-column state halves, one
-// workgroup each): segments are added only when there are fewer than
-// kMinStreams (b, h, half) streams, so that the grid still has about that
-// many workgroups.
-constexpr int64_t kMinStreams = 1024;
+// Forward plan.  headdim = 64 with dstate = 64 runs the fused segment-serial
+// kernel k_fwd_seg, dstate = 128 its wide form k_fwd_wide (two workgroups per
+// head, 32 channels each).  With fewer than kMinStreams (b, h, half) streams
+// the sequence is cut into segments so the full pass still has about that many
+// workgroups: one per CU (it holds a CU's LDS), in one round, so each pays its
+// pipeline fill once (C4 [4,2048,16,64,64]: 64 streams; 4 segments of 8 chunks
+// ran the full pass in 30 us, 16 segments of 2 chunks in 45 us).  The
+// state-only pass that gives each segment's entering state runs on kPreMult
+// times finer segments (it fits two workgroups per CU), and full segment s
+// starts at the boundary of pre-segment s * kPreMult.  A cut costs two
+// launches (the state-only pass and the segment recurrence, about 15 us
+// together), so it is made only where it saves at least kMinSavedChunks
+// chunk steps of about 3 us each.
+#ifndef SSD_MIN_STREAMS
+#define SSD_MIN_STREAMS 256
+#endif
+#ifndef SSD_PRE_MULT
+#define SSD_PRE_MULT 2
+#endif
+constexpr int64_t kMinStreams = SSD_MIN_STREAMS;
+constexpr int64_t kPreMult = SSD_PRE_MULT;
+constexpr int64_t kMinSavedChunks = 6;
 
 struct FwdPlan {
     bool fused = false;
-    int nseg = 1, M = 1, nsplit = 1;
+    int nseg = 1, M = 1, nsplit = 1;     // nsplit: workgroups per head (2 for dstate 128)
+    int nseg_pre = 1, M_pre = 1, mult = 1; // segments of the state-only pass (nseg > 1)
     size_t seg_state = 0, seg_decay = 0; // workspace offsets (fused, nseg > 1)
-    size_t y_half = 0;                   // workspace offset (fused, nsplit = 2)
     size_t states = 0;                   // chunk states for VARLEN_STATES without SAVED_STATES
     size_t ws = 0;
 };
@@ -128,20 +145,27 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags) {
         const int64_t wstreams = streams * pl.nsplit;
         int64_t nseg = wstreams >= kMinStreams ? 1 : (kMinStreams + wstreams - 1) / wstreams;
         nseg = nseg < K ? nseg : K;
-        const int64_t M = (K + nseg - 1) / nseg;
-        pl.M = (int)M;
-        pl.nseg = (int)((K + M - 1) / M);
+        if (K - (K + nseg - 1) / nseg < kMinSavedChunks) nseg = 1;
+        if (nseg > 1) {
+            // full segments of M = mult * M_pre chunks, pre-segments of M_pre
+            const int64_t Mt = (K + nseg - 1) / nseg;
+            const int64_t mult = kPreMult < Mt ? kPreMult : Mt;
+            const int64_t Mp = (Mt + mult - 1) / mult;
+            pl.mult = (int)mult;
+            pl.M_pre = (int)Mp;
+            pl.M = (int)(mult * Mp);
+            pl.nseg = (int)((K + pl.M - 1) / pl.M);
+            pl.nseg_pre = (int)((K + Mp - 1) / Mp);
+        } else {
+            pl.M = (int)K;
+        }
         size_t off = 0;
         if (pl.nseg > 1) {
-            const size_t units = (size_t)streams * pl.nseg;
+            const size_t units = (size_t)streams * pl.nseg_pre;
             pl.seg_state = off;
             off += align256(units * pn * sizeof(float));
             pl.seg_decay = off;
             off += align256(units * sizeof(float));
-        }
-        if (pl.nsplit > 1) {
-            pl.y_half = off;
-            off += align256((size_t)s->batch * s->seqlen * s->nheads * s->headdim * sizeof(float));
         }
         if ((flags & MAMBA2_SSD_VARLEN_STATES) && !(flags & MAMBA2_SSD_SAVED_STATES)) {
             pl.states = off;
@@ -332,41 +356,39 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         sp.M = pl.M;
         sp.nsplit = pl.nsplit;
         const unsigned units = (unsigned)(vs.batch * vs.nheads * pl.nseg * pl.nsplit);
-        // with two state halves the halves' sum, D x, pre_gate and the z gate
-        // are applied by k_fwd_combine
         ssd::FwdParams kp = prm;
-        if (pl.nsplit > 1) {
-            sp.y_half = (float *)((char *)workspace + pl.y_half);
-            kp.has_D = 0;
-            kp.has_z = 0;
-            kp.pre_gate = nullptr;
-        }
         if (int rc = record(tr, st, nullptr)) return rc;
         if (pl.nseg > 1) {
-            sp.seg_state = (float *)((char *)workspace + pl.seg_state);
-            sp.seg_log_decay = (float *)((char *)workspace + pl.seg_decay);
-            ssd::launch_fwd_seg(true, false, false, seq, dim3(units), st, kp, sp);
+            // each pre-segment's contribution, then the states at their boundaries
+            ssd::SegParams pre = sp;
+            pre.nseg = pl.nseg_pre;
+            pre.M = pl.M_pre;
+            pre.seg_state = (float *)((char *)workspace + pl.seg_state);
+            pre.seg_log_decay = (float *)((char *)workspace + pl.seg_decay);
+            const unsigned pre_units = (unsigned)(vs.batch * vs.nheads * pl.nseg_pre * pl.nsplit);
+            ssd::launch_fwd_seg(true, false, false, seq, dim3(pre_units), st, kp, pre);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
             const int PN = (int)(vs.headdim * vs.dstate);
             const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
-            hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, sp.seg_state,
-                               sp.seg_log_decay, prm.init, sp.seg_state, prm.final_state, pl.nseg, PN);
+            hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, pre.seg_state,
+                               pre.seg_log_decay, prm.init, pre.seg_state, prm.final_state, pl.nseg_pre, PN);
             if (int rc = launch_status("k_state_pass", tr, st)) return rc;
-            sp.seg_in = sp.seg_state;
+            sp.seg_in = pre.seg_state;
+            sp.seg_in_n = pl.nseg_pre;
+            sp.in_mult = pl.mult;
             sp.write_final = 0;
         } else {
             sp.write_final = 1;
         }
         kp.chunk_states = prm.chunk_states;
-        ssd::launch_fwd_seg(false, kp.chunk_states != nullptr, kp.has_z != 0, seq, dim3(units), st, kp, sp);
-        if (int rc = launch_status(kp.chunk_states ? "k_fwd_seg_save" : "k_fwd_seg", tr, st)) return rc;
         if (pl.nsplit > 1) {
-            const int64_t n4 = s->batch * s->seqlen * s->nheads * s->headdim / 4;
-            int64_t blocks = (n4 + ssd::kThreads - 1) / ssd::kThreads;
-            blocks = blocks < 4096 ? blocks : 4096;
-            hipLaunchKernelGGL(ssd::k_fwd_combine, dim3((unsigned)blocks), dim3(ssd::kThreads), 0, st,
-                               prm, (const float *)sp.y_half, n4);
-            if (int rc = launch_status("k_fwd_combine", tr, st)) return rc;
+            // dstate 128: two workgroups per head, 32 channels and all 128
+            // state columns each, writing out directly
+            ssd::launch_fwd_wide(kp.chunk_states != nullptr, kp.has_z != 0, seq, dim3(units), st, kp, sp);
+            if (int rc = launch_status(kp.chunk_states ? "k_fwd_wide_save" : "k_fwd_wide", tr, st)) return rc;
+        } else {
+            ssd::launch_fwd_seg(false, kp.chunk_states != nullptr, kp.has_z != 0, seq, dim3(units), st, kp, sp);
+            if (int rc = launch_status(kp.chunk_states ? "k_fwd_seg_save" : "k_fwd_seg", tr, st)) return rc;
         }
         if (varlen) {
             hipLaunchKernelGGL(ssd::k_varlen_states, dim3((unsigned)a->nseqs, prm.H),
@@ -420,7 +442,7 @@ BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
         off += align256(bhk * pn * sizeof(float));
         l.recompute = fwd_plan(s, 0);
         if (l.recompute.nseg > 1) {
-            const size_t units = (size_t)s->batch * s->nheads * l.recompute.nseg;
+            const size_t units = (size_t)s->batch * s->nheads * l.recompute.nseg_pre;
             l.seg_state = off;
             off += align256(units * pn * sizeof(float));
             l.seg_decay = off;
@@ -586,15 +608,20 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
         const unsigned units = (unsigned)(B * H * sp.nseg);
         const bool seq = a->seq_idx != nullptr;
         if (sp.nseg > 1) {
-            sp.seg_state = (float *)(ws + lay.seg_state);
-            sp.seg_log_decay = (float *)(ws + lay.seg_decay);
-            ssd::launch_fwd_seg(true, false, false, seq, dim3(units), st, kp, sp);
+            ssd::SegParams pre = sp;
+            pre.nseg = lay.recompute.nseg_pre;
+            pre.M = lay.recompute.M_pre;
+            pre.seg_state = (float *)(ws + lay.seg_state);
+            pre.seg_log_decay = (float *)(ws + lay.seg_decay);
+            ssd::launch_fwd_seg(true, false, false, seq, dim3((unsigned)(B * H * pre.nseg)), st, kp, pre);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
             hipLaunchKernelGGL(ssd::k_state_pass, dim3((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * H),
-                               dim3(ssd::kThreads), 0, st, sp.seg_state, sp.seg_log_decay, fp.init,
-                               sp.seg_state, (float *)nullptr, sp.nseg, PN);
+                               dim3(ssd::kThreads), 0, st, pre.seg_state, pre.seg_log_decay, fp.init,
+                               pre.seg_state, (float *)nullptr, pre.nseg, PN);
             if (int rc = launch_status("k_state_pass", tr, st)) return rc;
-            sp.seg_in = sp.seg_state;
+            sp.seg_in = pre.seg_state;
+            sp.seg_in_n = pre.nseg;
+            sp.in_mult = lay.recompute.mult;
         }
         ssd::launch_fwd_seg(true, true, false, seq, dim3(units), st, sp_prm, sp);
         if (int rc = launch_status("k_fwd_seg_state_save", tr, st)) return rc;

@@ -271,13 +271,18 @@ struct Frag {
     half8 h, l;
 };
 
-__device__ __forceinline__ Frag frag(SplitTile s, int row, int ks) {
+// Row `row`, k-step ks of a split tile with a row stride of kS halves (the
+// 64-wide tiles use kTS; wider or narrower tiles pass their own stride).
+template <int kS>
+__device__ __forceinline__ Frag frag_s(SplitTile s, int row, int ks) {
     const int kq = (threadIdx.x & 63) >> 4;
     Frag f;
-    f.h = *(const half8 *)&s.hi[row * kTS + ks * 32 + kq * 8];
-    f.l = *(const half8 *)&s.lo[row * kTS + ks * 32 + kq * 8];
+    f.h = *(const half8 *)&s.hi[row * kS + ks * 32 + kq * 8];
+    f.l = *(const half8 *)&s.lo[row * kS + ks * 32 + kq * 8];
     return f;
 }
+
+__device__ __forceinline__ Frag frag(SplitTile s, int row, int ks) { return frag_s<kTS>(s, row, ks); }
 
 __device__ __forceinline__ f32x4 mma3f(Frag a, Frag b, f32x4 c) { return mma3(a.h, a.l, b.h, b.l, c); }
 
@@ -301,12 +306,15 @@ __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 // ds_read_b64_tr_b16 on a split-tile array stored with the contraction index
 // along rows (tile[k][c]).  Each 16-lane group names rows k0..k0+3 (k0 may
 // differ between groups); lane l receives tile[k0 + e][c0 + l % 16], e = 0..3.
-__device__ __forceinline__ half4 tr4(const _Float16 *arr, int k0, int c0) {
+template <int kS>
+__device__ __forceinline__ half4 tr4_s(const _Float16 *arr, int k0, int c0) {
     const int m = threadIdx.x & 15;
     typedef short v4s __attribute__((ext_vector_type(4)));
-    auto p = (__attribute__((address_space(3))) v4s *)(arr + (k0 + (m >> 2)) * kTS + c0 + 4 * (m & 3));
+    auto p = (__attribute__((address_space(3))) v4s *)(arr + (k0 + (m >> 2)) * kS + c0 + 4 * (m & 3));
     return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
 }
+
+__device__ __forceinline__ half4 tr4(const _Float16 *arr, int k0, int c0) { return tr4_s<kTS>(arr, k0, c0); }
 
 // The LDS array base as a value the optimizer cannot see through.  Tiles
 // past the first 64 KB of LDS cannot use the 16-bit immediate offset of the
@@ -346,13 +354,16 @@ __device__ __forceinline__ Frag frag_tn(SplitTile s, int ks, int c0) {
 
 // The same in the k order of operands taken from MFMA outputs (perm32):
 // slots 0..3 are rows 32 m + 4 (l / 16) + 0..3, slots 4..7 rows 32 m + 16 + ...
-__device__ __forceinline__ Frag frag_tp(SplitTile s, int m, int c0) {
+template <int kS>
+__device__ __forceinline__ Frag frag_tp_s(SplitTile s, int m, int c0) {
     const int k0 = 32 * m + 4 * ((threadIdx.x & 63) >> 4);
     Frag f;
-    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 16, c0));
-    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 16, c0));
+    f.h = cat8(tr4_s<kS>(s.hi, k0, c0), tr4_s<kS>(s.hi, k0 + 16, c0));
+    f.l = cat8(tr4_s<kS>(s.lo, k0, c0), tr4_s<kS>(s.lo, k0 + 16, c0));
     return f;
 }
+
+__device__ __forceinline__ Frag frag_tp(SplitTile s, int m, int c0) { return frag_tp_s<kTS>(s, m, c0); }
 
 // fp32 hi + lo of four split values: one mixed-precision FMA each
 // (hi * 1 + lo with both fp16 operands widened, exact, rounded once to fp32),
@@ -380,8 +391,19 @@ __device__ __forceinline__ f32x4 tile_acc(SplitTile s, int row0, int c0) {
 }
 
 // fp32 values of tile[row][c0 .. c0 + 3] (one 8-byte read of each half).
-__device__ __forceinline__ f32x4 tile_row4(SplitTile s, int row, int c0) {
-    return join4(*(const half4 *)&s.hi[row * kTS + c0], *(const half4 *)&s.lo[row * kTS + c0]);
+template <int kS>
+__device__ __forceinline__ f32x4 tile_row4_s(SplitTile s, int row, int c0) {
+    return join4(*(const half4 *)&s.hi[row * kS + c0], *(const half4 *)&s.lo[row * kS + c0]);
+}
+
+__device__ __forceinline__ f32x4 tile_row4(SplitTile s, int row, int c0) { return tile_row4_s<kTS>(s, row, c0); }
+
+// tile[idx .. idx + 3] = v (both halves)
+__device__ __forceinline__ void store_split4(SplitTile d, int idx, float4 v) {
+    half4 vh, vl;
+    split4(v, vh, vl);
+    *(half4 *)&d.hi[idx] = vh;
+    *(half4 *)&d.lo[idx] = vl;
 }
 
 // Value of v in lane `lane` (which must be the same for the whole wave).

@@ -9,12 +9,10 @@
 //         (+ D x_t, * silu(z_t))
 //   S  <- exp(cs_last) S + sum_t decay_t q_t x_t (x) B_t
 //
-// dstate N = 128 runs as two independent 64-column halves of the state
-// (nsplit = 2): with W_a, W_b the decayed C.B^T of each half of the columns,
-//   y = (W_a + W_b)(q x) + exp(cs) (C_a . S_a + C_b . S_b) = y_a + y_b,
-// so one workgroup per half runs the N = 64 algorithm on its columns of B, C
-// and the state, writes y_a to out and y_b to sp.y_half, and
-// k_fwd_combine adds them (and applies D and z).
+// dstate N = 128: the full pass is k_fwd_wide (ssd_fwd_wide.h); the
+// state-only pass below runs two independent 64-column halves of the state
+// (nsplit = 2), one workgroup each, since a state contribution splits by
+// columns.
 //
 // Long sequences with few (b, h) streams are cut into segments so the grid
 // still fills the GPU: a state-only pass (kStateOnly) computes each
@@ -71,10 +69,12 @@ struct SegParams {
     int M;                 // chunks per segment (the last one may be shorter)
     float *seg_state;      // [B, H, nseg, P, N] segment contributions (state-only pass)
     float *seg_log_decay;  // [B, H, nseg]
-    const float *seg_in;   // [B, H, nseg, P, N] state entering each segment, or NULL
+    const float *seg_in;   // [B, H, seg_in_n, P, N] states at the segment-pass boundaries, or
+                           // NULL; segment sg starts from entry sg * in_mult
+    int seg_in_n, in_mult;
     int write_final;       // full pass writes final_state (single segment)
-    int nsplit;            // 64-column state halves per head: 1 (N = 64) or 2 (N = 128)
-    float *y_half;         // nsplit = 2: [B, L, H, P] output of the second half
+    int nsplit;            // 64-column state halves per head: 1 (N = 64) or 2 (N = 128,
+                           // state-only pass; the full pass of N = 128 is k_fwd_wide)
 };
 
 constexpr int kXcds = 8; // MI355X: workgroups go round-robin over 8 XCDs
@@ -137,10 +137,12 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     auto T3 = [&](int s) { return tile_at(lds, kStateOnly ? 2 * s + 1 : 3 * s + 2); };
     auto T4 = [&](int s) { return tile_at(lds, 6 + s); };
 
-    // unit = (((b * G + g) * nseg + sg) * nsplit + nh) * R + r
-    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, prm.R);
-    const int r = u % prm.R;
-    const int nh = (u / prm.R) % sp.nsplit;
+    // unit = (((b * G + g) * nseg + sg) * R + r) * nsplit + nh: the column
+    // halves of a head next to each other, so the second reads the head's x
+    // rows from the L2 the first filled
+    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, prm.R * sp.nsplit);
+    const int nh = u % sp.nsplit;
+    const int r = (u / sp.nsplit) % prm.R;
     const int sg = (u / (prm.R * sp.nsplit)) % sp.nseg;
     const int bg = u / (prm.R * sp.nsplit * sp.nseg);
     const int g = bg % prm.G, b = bg / prm.G;
@@ -339,7 +341,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             const float *s0 = nullptr;
             if (!kStateOnly || kSave) {
                 if (sp.seg_in)
-                    s0 = sp.seg_in + (((int64_t)b * H + h) * sp.nseg + sg) * PNS + n0;
+                    s0 = sp.seg_in + (((int64_t)b * H + h) * sp.seg_in_n + sg * sp.in_mult) * PNS + n0;
                 else if (prm.init)
                     s0 = prm.init + ((int64_t)b * H + h) * PNS + n0;
             }
@@ -484,7 +486,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                             v.z *= silu_f(zv.z);
                             v.w *= silu_f(zv.w);
                         }
-                        *(float4 *)((nh ? sp.y_half : prm.out) + row + p) = v;
+                        *(float4 *)(prm.out + row + p) = v;
                     }
                 }
                 z_load(k + 1);
@@ -548,39 +550,6 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     }
 }
 
-// nsplit = 2 epilogue, elementwise over [B, L, H, P] in float4s: out holds
-// y_a, y_half y_b; out = (y_a + y_b + D x) (* silu z), pre_gate = y + D x.
-#ifndef SSD_KERNEL_TEMPLATES_ONLY
-__global__ __launch_bounds__(kThreads) void k_fwd_combine(FwdParams prm, const float *y_half,
-                                                          int64_t n4) {
-    constexpr int P = 64;
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4;
-         i += (int64_t)gridDim.x * kThreads) {
-        const int64_t e = 4 * i;
-        const float4 a = *(const float4 *)(prm.out + e), c = *(const float4 *)(y_half + e);
-        float4 v = make_float4(a.x + c.x, a.y + c.y, a.z + c.z, a.w + c.w);
-        if (prm.has_D) {
-            const int p = (int)(e % P), h = (int)((e / P) % prm.H);
-            const float4 xv = *(const float4 *)(prm.x + e);
-            const float4 d = prm.d_per_channel ? *(const float4 *)(prm.D + h * P + p)
-                                               : make_float4(prm.D[h / prm.hdiv], prm.D[h / prm.hdiv],
-                                                             prm.D[h / prm.hdiv], prm.D[h / prm.hdiv]);
-            v.x += d.x * xv.x;
-            v.y += d.y * xv.y;
-            v.z += d.z * xv.z;
-            v.w += d.w * xv.w;
-        }
-        if (prm.pre_gate) *(float4 *)(prm.pre_gate + e) = v;
-        if (prm.has_z) {
-            const float4 zv = *(const float4 *)(prm.z + e);
-            v.x *= silu_f(zv.x);
-            v.y *= silu_f(zv.y);
-            v.z *= silu_f(zv.z);
-            v.w *= silu_f(zv.w);
-        }
-        *(float4 *)(prm.out + e) = v;
-    }
-}
-#endif
+
 
 }  // namespace ssd

@@ -1,0 +1,437 @@
+// Fused forward for dstate N = 128 (headdim 64): one workgroup per
+// (batch b, head h, channel half ph, segment), 32 channels of the head and all
+// 128 state columns.
+//
+// The two channel halves of a head are independent problems: the state rows
+// p, the output channels p and the x columns p of one half never meet the
+// other half's, while C . B^T (over all 128 columns) is the same for both, so
+// each workgroup forms it in full.  Each workgroup therefore writes its own
+// channels of `out` (with D x, pre_gate and the z gate) directly, reads its
+// half of every x row, and B and C come from HBM once per head group: the two
+// halves of a head, like the R heads of a group, run on consecutive workgroups
+// of one XCD (xcd_unit), so the second reader finds them in that XCD's L2.
+//
+// Per 64-token chunk, as in k_fwd_seg (q = discretised dt, cs = chunk-local
+// cumsum of A q in log2 units, decay_t = exp2(cs_last - cs_t)):
+//   y_t[p] = exp2(cs_t) C_t . S[p] + sum_{s <= t} (C_t . B_s) exp2(cs_t - cs_s) q_s x_s[p]
+//   S[p]  <- exp2(cs_last) S[p] + sum_t B_t (decay_t q_t x_t[p])
+// Tiles (split fp16, LDS, double buffered by chunk parity s):
+//   T1 = B [t][n], 64 x 128      (A operand of C.B^T, rows s; and, read
+//                                 transposed, the A operand of U^T)
+//   T2 = x [t][p], 64 x 32       (x^T operand of the W product, transposed
+//                                 reads; and the x of the D x term)
+//   T3 = decay q x [t][p], 64 x 32  (B operand of U^T, transposed reads)
+//   T4 = S [p][n], 32 x 128      (A operand of the C.S term)
+// and, in registers, C_t for the lane's own token row.  The state of wave W is
+// its two 16-column blocks n in {16 W.., 64 + 16 W..} for the 32 rows p, held
+// in the accumulator layout of U^T.
+//
+// Long sequences with few streams are cut into segments exactly as for
+// k_fwd_seg: the state-only pass of k_fwd_seg (two 64-column halves) gives each
+// segment's contribution in the same [B, H, nseg, P, N] layout, the segment
+// recurrence (k_state_pass) the state entering each segment, and this kernel
+// starts each segment from it (sp.seg_in).
+//
+// The math is that of mamba_ascendc/csrc/ops/mamba2_ssd_fwd/design.md:10-20 and
+// the chunked decomposition of mamba_torch/ssd_reference.py:113-189; the
+// fusion, blocking and layouts are this file's own.
+#pragma once
+
+#include <type_traits>
+
+#include "ssd_fwd_fused.h"
+
+namespace ssd {
+
+namespace wide {
+constexpr int kT = 64, kPC = 32, kNC = 128;
+constexpr int kS1 = kNC + 8;  // row stride (halves) of the 128-wide tiles T1, T4
+constexpr int kS2 = kPC + 8;  // row stride of the 32-wide tiles T2, T3
+constexpr int kA1 = kT * kS1, kA2 = kT * kS2, kA4 = kPC * kS1;  // halves per array
+// offsets (halves) of the arrays of buffer s: T1 hi, lo | T2 hi, lo | T3 hi, lo | T4 hi, lo
+constexpr int kBuf = 2 * (kA1 + 2 * kA2 + kA4);
+__device__ __forceinline__ SplitTile T1(_Float16 *b, int s) { return {b + s * kBuf, b + s * kBuf + kA1}; }
+__device__ __forceinline__ SplitTile T2(_Float16 *b, int s) {
+    return {b + s * kBuf + 2 * kA1, b + s * kBuf + 2 * kA1 + kA2};
+}
+__device__ __forceinline__ SplitTile T3(_Float16 *b, int s) {
+    return {b + s * kBuf + 2 * kA1 + 2 * kA2, b + s * kBuf + 2 * kA1 + 3 * kA2};
+}
+__device__ __forceinline__ SplitTile T4(_Float16 *b, int s) {
+    return {b + s * kBuf + 2 * kA1 + 4 * kA2, b + s * kBuf + 2 * kA1 + 4 * kA2 + kA4};
+}
+}  // namespace wide
+
+// kSave: also write the state entering every chunk to prm.chunk_states (the
+// varlen states read them).  kGate: the z gate.  kSeq: packed sequences.
+template <bool kSave = false, bool kGate = false, bool kSeq = false>
+__global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParams sp) {
+    using namespace wide;
+    constexpr int T = kT, P = 64, NS = kNC;
+    constexpr int TS = kSeq ? T : 1;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * kBuf];
+    struct ChunkTok {
+        float cs[2][T], q[2][T];
+        int sid[2][TS];
+        float off[2][TS];
+        float carry[2];
+        int mixed[2];
+    };
+    __shared__ __attribute__((aligned(16))) ChunkTok s_tok;
+    auto &s_cs = s_tok.cs, &s_q = s_tok.q;
+    auto &s_sid = s_tok.sid;
+    auto &s_off = s_tok.off;
+    auto &s_carry = s_tok.carry;
+    auto &s_mixed = s_tok.mixed;
+    __shared__ __attribute__((aligned(16))) float s_Dv[kPC]; // D of this half's channels
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const bool producer = wave >= 4;
+    const int w = wave & 3;
+    const int r16 = lane & 15, kq = lane >> 4;
+
+    // unit = (((b * G + g) * nseg + sg) * R + r) * 2 + ph
+    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, 2 * prm.R);
+    const int ph = u & 1;
+    const int r = (u >> 1) % prm.R;
+    const int sg = (u / (2 * prm.R)) % sp.nseg;
+    const int bg = u / (2 * prm.R * sp.nseg);
+    const int g = bg % prm.G, b = bg / prm.G;
+    const int h = g * prm.R + r;
+    const int H = prm.H, G = prm.G;
+    const int p0 = kPC * ph; // first channel of this half
+    const int64_t PNS = (int64_t)P * NS;
+    const int kbeg = sg * sp.M, kend = min(kbeg + sp.M, prm.K);
+
+    // ------------------------------------------------------------ producer
+    // Ring of kDepth register slots with the loads of the next kDepth chunks:
+    // x rows xrow + 32 j (columns p0 + cx .. + 3) and B rows brow + 8 j
+    // (columns cb .. cb + 3) of that chunk, and dt of token `lane`.
+    constexpr int kDepth = 3;
+    const int pt = tid - 4 * kWave;
+    const int xrow = pt >> 3, cx = (pt & 7) * 4;   // x: 8 threads per 32-column row
+    const int brow = pt >> 5, cb = (pt & 31) * 4;  // B: 32 threads per 128-column row
+    float4 xr[kDepth][2], br[kDepth][8];
+    float dtr[kDepth];
+    int sidr[kDepth], sprv[kDepth];
+    const int rowHP4 = (int)((int64_t)H * P * 4), rowGN4 = (int)((int64_t)G * NS * 4); // token strides, bytes
+    const int hr = h / prm.hdiv, Hr = H / prm.hdiv;
+    const float Ah2 = prm.A[hr] * kLog2e;
+    const float bias = prm.dt_bias ? prm.dt_bias[hr] : 0.f;
+    auto p_load = [&](int k, auto slot_c) {
+        constexpr int sl = decltype(slot_c)::value;
+        const bool real = k < kend;
+        const int64_t t0 = (int64_t)(real ? k : kbeg) * T;
+        const int tv = (int)min((int64_t)T, prm.L - t0);
+        const int range = real ? 0x7fffffff : 0;
+        const auto rx = buf_rsrc_n(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P + p0, range);
+        const auto rb = buf_rsrc_n(prm.B + (((int64_t)b * prm.L + t0) * G + g) * NS, range);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) xr[sl][j] = buf_load4(rx, min(xrow + 32 * j, tv - 1) * rowHP4 + cx * 4, 0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) br[sl][j] = buf_load4(rb, min(brow + 8 * j, tv - 1) * rowGN4 + cb * 4, 0);
+        dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * Hr + hr];
+        if (kSeq) {
+            const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + t0;
+            sidr[sl] = si[min(lane, tv - 1)];
+            const int pv = si[t0 > 0 ? -1 : 0];
+            sprv[sl] = t0 > 0 ? pv : 0;
+        }
+    };
+    auto p_stage = [&](int k, int s, auto slot_c) {
+        constexpr int sl = decltype(slot_c)::value;
+        const int tv = (int)min((int64_t)T, prm.L - (int64_t)k * T);
+        float q = 0.f, a = 0.f;
+        if (lane < tv) {
+            q = discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
+            a = Ah2 * q;
+        }
+        const float cs = wave_inclusive_scan(a);
+        const float cs_last = readlane_f(cs, T - 1);
+        ChunkTok *tk = opaque_lds_t(&s_tok);
+        if (w == 0) {
+            tk->cs[s][lane] = cs;
+            tk->q[s][lane] = q;
+        }
+        float dec = exp2_f(cs_last - cs);
+        if (kSeq) {
+            const int sid = sidr[sl], e_end = __shfl(sid, T - 1, kWave), e_prev = sprv[sl];
+            if (sid != e_end || e_end < 0) dec = 0.f;
+            const bool mixed = __ballot(sid != e_end) != 0;
+            if (w == 0) {
+                tk->sid[s][lane] = sid;
+                tk->off[s][lane] = sid == e_prev ? 1.f : 0.f;
+                if (lane == 0) {
+                    tk->carry[s] = e_end == e_prev ? 1.f : 0.f;
+                    tk->mixed[s] = mixed ? 1 : 0;
+                }
+            }
+        }
+        _Float16 *lp = opaque_lds(lds);
+        const SplitTile t1 = T1(lp, s), t2 = T2(lp, s), t3 = T3(lp, s);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int row = xrow + 32 * j;
+            const float dr = __shfl(dec * q, row, kWave);
+            const float4 xv = xr[sl][j];
+            store_split4(t2, row * kS2 + cx, xv);
+            store_split4(t3, row * kS2 + cx, make_float4(xv.x * dr, xv.y * dr, xv.z * dr, xv.w * dr));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) store_split4(t1, (brow + 8 * j) * kS1 + cb, br[sl][j]);
+    };
+
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    static_assert(kDepth == 3, "the unrolled ring below assumes three slots");
+    if (producer) {
+        p_load(kbeg, S0{});
+        p_load(kbeg + 1, S1{});
+        p_load(kbeg + 2, S2{});
+        p_stage(kbeg, 0, S0{});
+        p_load(kbeg + 3, S0{});
+        lds_barrier();
+        auto p_iter = [&](int k, auto slot_next) {
+            const int s = (k - kbeg) & 1;
+            p_stage(k + 1, s ^ 1, slot_next);
+            p_load(k + 1 + kDepth, slot_next);
+            lds_barrier();
+        };
+        int k0 = kbeg;
+        for (; k0 + kDepth <= kend; k0 += kDepth) {
+            p_iter(k0, S1{});
+            p_iter(k0 + 1, S2{});
+            p_iter(k0 + 2, S0{});
+        }
+        if (k0 < kend) p_iter(k0, S1{});
+        if (k0 + 1 < kend) p_iter(k0 + 1, S2{});
+        return;
+    }
+
+    // ------------------------------------------------------------ consumers
+    auto consumer = [&](auto wave_c) {
+        constexpr int W = decltype(wave_c)::value;
+        const int own = 16 * W + r16; // token row of this lane
+        // Sr[c][pb][i] = S[p0 + 16 pb + l % 16][n = 16 (W + 4 c) + 4 (l / 16) + i]
+        f32x4 Sr[2][2];
+        // C row `own` of the next chunk (128 columns: k-steps ks = 0..3, each
+        // 8 (l / 16) + 0..7 of its 32 columns), loaded one chunk ahead; past
+        // the segment end an empty-range read
+        float4 cr[8];
+        auto c_load = [&](int k) {
+            const bool real = k < kend;
+            const int64_t t0 = (int64_t)(real ? k : kbeg) * T;
+            const int tv = (int)min((int64_t)T, prm.L - t0);
+            const auto rc = buf_rsrc_n(prm.C + (((int64_t)b * prm.L + t0) * G + g) * NS, real ? 0x7fffffff : 0);
+            const int vo = (min(own, tv - 1) * G * NS + 8 * kq) * 4;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) cr[j] = buf_load4(rc, vo + (32 * (j >> 1) + 4 * (j & 1)) * 4, 0);
+        };
+        float4 zr[2];
+        auto z_load = [&](int k) {
+            if (!kGate) return;
+            const bool real = k < kend;
+            const int64_t t0 = (int64_t)(real ? k : kbeg) * T;
+            const int tv = (int)min((int64_t)T, prm.L - t0);
+            const auto rz = buf_rsrc_n(prm.z + (((int64_t)b * prm.L + t0) * H + h) * P + p0, real ? 0x7fffffff : 0);
+            const int vo = (min(own, tv - 1) * H * P + 4 * kq) * 4;
+#pragma unroll
+            for (int pb = 0; pb < 2; ++pb) zr[pb] = buf_load4(rz, vo + 64 * pb, 0);
+        };
+        auto write_T4 = [&](int s) {
+            const SplitTile t4 = T4(opaque_lds(lds), s);
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb)
+                    store_split4(t4, (16 * pb + r16) * kS1 + 16 * (W + 4 * c) + 4 * kq,
+                                 make_float4(Sr[c][pb][0], Sr[c][pb][1], Sr[c][pb][2], Sr[c][pb][3]));
+        };
+
+        {
+            const float *s0 = nullptr;
+            if (sp.seg_in)
+                s0 = sp.seg_in + (((int64_t)b * H + h) * sp.seg_in_n + sg * sp.in_mult) * PNS;
+            else if (prm.init)
+                s0 = prm.init + ((int64_t)b * H + h) * PNS;
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb) {
+                    if (s0) {
+                        const float4 v = *(const float4 *)(s0 + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq);
+                        Sr[c][pb] = f32x4{v.x, v.y, v.z, v.w};
+                    } else {
+                        Sr[c][pb] = zero4();
+                    }
+                }
+            write_T4(0);
+            c_load(kbeg);
+            z_load(kbeg);
+            if (W == 0 && lane < kPC) {
+                const float dv = prm.has_D ? prm.D[prm.d_per_channel ? h * P + p0 + lane : hr] : 0.f;
+                s_Dv[lane] = dv;
+            }
+        }
+        lds_barrier();
+
+        auto iter = [&](int k, auto full_c) {
+            constexpr bool kFull = decltype(full_c)::value;
+            const int s = (k - kbeg) & 1;
+            const int64_t t0 = (int64_t)k * T;
+            const int tv = (int)min((int64_t)T, prm.L - t0);
+            const float cs_last = s_cs[s][T - 1];
+            if (kSave) {
+                float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * PNS;
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int pb = 0; pb < 2; ++pb)
+                        *(float4 *)(cst + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq) =
+                            make_float4(Sr[c][pb][0], Sr[c][pb][1], Sr[c][pb][2], Sr[c][pb][3]);
+            }
+            Frag Cown[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const float4 v0 = cr[2 * ks], v1 = cr[2 * ks + 1];
+                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                Cown[ks] = pack_frag(vv);
+            }
+            c_load(k + 1);
+            _Float16 *la = opaque_lds(lds);
+            const SplitTile t1 = T1(la, s), t4 = T4(la, s);
+            const float cs_own = s_cs[s][own];
+
+            // W^T tiles: C_t . B_s exp2(cs_t - cs_s) q_s, s <= t, t = own
+            Frag WT[2];
+            {
+                float wv[2][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f32x4 cb = zero4();
+                    if (j <= W)
+#pragma unroll
+                        for (int ks = 0; ks < 4; ++ks)
+                            cb = mma3f(frag_s<kS1>(t1, 16 * j + r16, ks), Cown[ks], cb);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int so = 16 * j + 4 * kq + i;
+                        const float e = (j <= W && so <= own) ? exp2_f(cs_own - s_cs[s][so]) * s_q[s][so] : 0.f;
+                        wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
+                    }
+                }
+                if (kSeq && s_mixed[s]) {
+                    const int sid_own = s_sid[s][own];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int4 sv = *(const int4 *)&s_sid[s][16 * j + 4 * kq];
+                        const int sva[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (sva[i] != sid_own) wv[j >> 1][(j & 1) * 4 + i] = 0.f;
+                    }
+                }
+                WT[0] = pack_frag(wv[0]);
+                WT[1] = pack_frag(wv[1]);
+            }
+            // y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] q_s x_s, p in this half
+            f32x4 acc[2];
+#pragma unroll
+            for (int pb = 0; pb < 2; ++pb) {
+                acc[pb] = zero4();
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) acc[pb] = mma3f(frag_s<kS1>(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
+            }
+            const float ecs = kSeq ? exp2_f(cs_own) * s_off[s][own] : exp2_f(cs_own);
+#pragma unroll
+            for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[pb][i] *= ecs;
+            _Float16 *lb = opaque_lds(lds);
+            const SplitTile t2 = T2(lb, s), t3 = T3(lb, s), t1b = T1(lb, s);
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                if (2 * m <= W)
+#pragma unroll
+                    for (int pb = 0; pb < 2; ++pb)
+                        acc[pb] = mma3f(frag_tp_s<kS2>(t2, m, 16 * pb), WT[m], acc[pb]);
+            }
+            if (kFull || own < tv) {
+                const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P + p0;
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb) {
+                    const int p = 16 * pb + 4 * kq;
+                    float4 v = make_float4(acc[pb][0], acc[pb][1], acc[pb][2], acc[pb][3]);
+                    if (prm.has_D) {
+                        const f32x4 xa = tile_row4_s<kS2>(t2, own, p);
+                        const float4 d = *(const float4 *)&s_Dv[p];
+                        v.x += d.x * xa[0];
+                        v.y += d.y * xa[1];
+                        v.z += d.z * xa[2];
+                        v.w += d.w * xa[3];
+                    }
+                    if (prm.pre_gate) *(float4 *)(prm.pre_gate + row + p) = v;
+                    if (kGate) {
+                        const float4 zv = zr[pb];
+                        v.x *= silu_f(zv.x);
+                        v.y *= silu_f(zv.y);
+                        v.z *= silu_f(zv.z);
+                        v.w *= silu_f(zv.w);
+                    }
+                    *(float4 *)(prm.out + row + p) = v;
+                }
+            }
+            z_load(k + 1);
+            // U^T[n][p] = sum_t B[t][n] (decay q x)[t][p]; S <- exp2(cs_last) S + U
+            f32x4 U[2][2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb) U[c][pb] = zero4();
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                Frag f3[2];
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb) f3[pb] = frag_tp_s<kS2>(t3, m, 16 * pb);
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const Frag a1 = frag_tp_s<kS1>(t1b, m, 16 * (W + 4 * c));
+#pragma unroll
+                    for (int pb = 0; pb < 2; ++pb) U[c][pb] = mma3f(a1, f3[pb], U[c][pb]);
+                }
+            }
+            const float alpha = kSeq ? exp2_f(cs_last) * s_carry[s] : exp2_f(cs_last);
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) Sr[c][pb][i] = alpha * Sr[c][pb][i] + U[c][pb][i];
+            write_T4(s ^ 1);
+            lds_barrier(); // buffer s is free, buffer s ^ 1 and T4(s ^ 1) are complete
+        };
+        const int kfull = (int)min((int64_t)kend, prm.L / T);
+        int k = kbeg;
+        for (; k < kfull; ++k) iter(k, std::true_type{});
+        if (k < kend) iter(k, std::false_type{});
+
+        if (sp.write_final && prm.final_state) {
+            float *dst = prm.final_state + ((int64_t)b * H + h) * PNS;
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb)
+                    *(float4 *)(dst + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq) =
+                        make_float4(Sr[c][pb][0], Sr[c][pb][1], Sr[c][pb][2], Sr[c][pb][3]);
+        }
+    };
+    switch (w) {
+    case 0: consumer(std::integral_constant<int, 0>{}); break;
+    case 1: consumer(std::integral_constant<int, 1>{}); break;
+    case 2: consumer(std::integral_constant<int, 2>{}); break;
+    default: consumer(std::integral_constant<int, 3>{}); break;
+    }
+}
+
+}  // namespace ssd

@@ -16,6 +16,10 @@ struct SegParams;
 void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
                     const FwdParams &kp, const SegParams &sp);
 
+// k_fwd_wide<save, gate, seq> (dstate 128)
+void launch_fwd_wide(bool save, bool gate, bool seq, dim3 grid, hipStream_t st, const FwdParams &kp,
+                     const SegParams &sp);
+
 // the has_z halves of the two backward launchers, one per translation unit
 void launch_bwd_ws_z0(int rev_r, bool seq, dim3 grid, hipStream_t st, const BwdParams &bp, int nseg,
                       int M);

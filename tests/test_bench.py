@@ -40,7 +40,13 @@ def test_traced_names_map_to_distinct_models():
     assert key("k_bwd_ws<true, 2, false>") == "k_bwd_ws_rev_z"
     assert key("k_bwd_ws<false, 4, true>") == "k_bwd_ws_rev_seq"
     assert key("k_bwd_ws<true, 0, false>") == "k_bwd_ws"
+    assert key("k_fwd_wide<false, false, false>") == "k_fwd_wide"
+    assert key("k_fwd_wide<true, true, false>") == "k_fwd_wide_save_gate"
+    assert key("k_fwd_wide<false, false, true>") == "k_fwd_wide_seq"
+    assert bench._short("void ssd::bwd::k_bwd_ws<false, 4, false>(ssd::BwdParams, int, int)") == \
+        "k_bwd_ws<false, 4, false>"
     assert key("k_state_pass") == "k_state_pass"
     shape = bench.CONFIGS[3]
-    for name in ("k_fwd_seg_gate", "k_fwd_seg_save_gate", "k_bwd_ws_rev", "k_bwd_ws_rev_z"):
+    for name in ("k_fwd_seg_gate", "k_fwd_seg_save_gate", "k_bwd_ws_rev", "k_bwd_ws_rev_z", "k_fwd_wide",
+                 "k_fwd_wide_gate"):
         assert not math.isnan(bench.fwd_kernel_model(name, shape)["bytes"]), name

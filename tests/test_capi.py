@@ -82,9 +82,10 @@ def test_workspace_size_validation(kw, flags, code):
 
 def test_workspace_size_formula():
     """Forward plan: P = 64 with N = 64 or 128 runs the fused segment-serial
-    kernel, which needs no workspace when there are >= 1024 (b, h, state-half)
-    streams (C3) and a per-segment state buffer otherwise; N = 128 also needs
-    the second half's [B,L,H,P] output.  The backward needs states (unless the forward's
+    kernel, which needs no workspace when there are >= 256 (b, h, state-half)
+    streams (C3) or the sequence is short, and a per-segment state buffer
+    otherwise, for N = 128 too.
+    The backward needs states (unless the forward's
     are passed in), per-chunk partials, and dstates only where the state
     gradients are not carried in the reverse fused chunk kernel (fewer than
     256 (b, g) streams, or other than 1, 2 or 4 heads per group)."""
@@ -97,15 +98,22 @@ def test_workspace_size_formula():
 
     fwd = lib.mamba2_ssd_fwd_workspace_size
     assert ws(fwd, batch=8, seqlen=4096, nheads=256, ngroups=64) == 0
-    # 64 streams -> 16 segments of 2 chunks: [B,H,nseg,P,N] + [B,H,nseg]
+    # 64 streams, 32 chunks -> 4 segments of 8 chunks, whose entering states
+    # come from 8 pre-segments of 4: [B,H,8,P,N] + [B,H,8]
     got = ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4)
-    assert got >= 4 * 16 * 16 * 64 * 64 * 4 + 4 * 16 * 16 * 4
-    assert got < 4 * 16 * 32 * 64 * 64 * 4  # never the per-chunk buffer
-    # N = 128: 64 (b, h) x 2 halves = 128 streams -> 8 segments of 4 chunks
+    assert 4 * 16 * 8 * 64 * 64 * 4 + 4 * 16 * 8 * 4 <= got <= 4 * 16 * 8 * (64 * 64 + 1) * 4 + 2 * 256
+    # N = 128: 64 (b, h) x 2 workgroups = 128 streams -> 2 segments of 16
+    # chunks, 4 pre-segments; nothing else (each workgroup writes its
+    # channels of out itself)
     got = ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4, dstate=128)
-    seg = 4 * 16 * 8 * 64 * 128 * 4
-    y_half = 4 * 2048 * 16 * 64 * 4
-    assert seg + y_half <= got <= seg + y_half + 3 * 256 + 4 * 16 * 8 * 4
+    seg = 4 * 16 * 4 * 64 * 128 * 4
+    assert seg <= got <= seg + 2 * 256 + 4 * 16 * 4 * 4
+    # a short sequence is not cut (the cut would save fewer than 6 chunk steps)
+    assert ws(fwd, batch=1, seqlen=128, nheads=2, ngroups=1, dstate=128) == 0
+    assert ws(fwd, batch=1, seqlen=384, nheads=2, ngroups=1) == 0   # 6 chunks: saves 5
+    assert ws(fwd, batch=1, seqlen=512, nheads=2, ngroups=1) > 0    # 8 chunks: saves 7
+    # one segment per stream: no workspace at all
+    assert ws(fwd, batch=8, seqlen=4096, nheads=64, ngroups=8, dstate=128) == 0
     assert ws(fwd, seqlen=0) == 0
     # varlen states without saved states: the chunk states join the workspace
     one = _shape(batch=1, seqlen=4096, nheads=256, ngroups=64)
@@ -176,7 +184,8 @@ def test_fwd_rejects_null_and_flag_mismatch_without_gpu():
     args.shape, args.nseqs = _shape(batch=1), 0
     assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -1
     args.flags, args.cu_seqlens, args.varlen_states = 0, None, None
-    # fast-path shape without workspace
+    # a segmented shape (few streams, long sequence) without its workspace
+    args.shape = _shape(batch=1, seqlen=4096)
     assert lib.mamba2_ssd_fwd(ctypes.byref(args), None, 0, None) == -3
     assert lib.mamba2_ssd_fwd(None, None, 0, None) == -1
 

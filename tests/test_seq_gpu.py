@@ -133,13 +133,15 @@ def test_interleaved_and_negative_ids_at_chunk_64():
 
 def test_segmented_streams_with_cuts():
     """Few long streams run as several segments per stream (the segment
-    recurrence between them): sequences cut inside segments, on a segment
-    edge, and one sequence spanning several segments."""
+    recurrence between them; here 8 streams of 300 chunks: full segments of 10
+    chunks, state-only pre-segments of 5): sequences cut inside segments, on a
+    full-segment edge (token 1920), on a pre-segment edge inside a full segment
+    (token 7360), and one sequence spanning several segments."""
     _need_gpu()
     shape = [1, 19200, 8, 64, 64, 64, 8]
     _say(f"segmented packed {shape}")
     inp = make_inputs(shape, seed=312, features=("bias", "init"))
-    lengths = [100, 92, 3 * 64 * 7, 5000, 1, 64 * 3, 19200 - (100 + 92 + 1344 + 5000 + 1 + 192)]
+    lengths = [100, 92, 1728, 5000, 1, 439, 19200 - 7360]
     ids = _ids_from_lengths(lengths)[None]
     got_y, got_f = _run(inp, 64, ids)
     want_y, want_f = _ref(inp, 64, ids)

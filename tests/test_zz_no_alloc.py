@@ -36,12 +36,13 @@ def _args(rt, shape, dev, flags, limit, out, fin):
 
 
 CALLS = [
-    # shape [B, L, H, P, N, chunk, G], features: 16 (b, h) streams -> 32 segments
+    # shape [B, L, H, P, N, chunk, G], features: 16 (b, h) streams of 32
+    # chunks -> 16 segments of 2 chunks, 32 state-only pre-segments
     ([2, 2048, 8, 64, 64, 64, 2], ("D2", "z", "bias", "init")),
     # smaller: 4 streams -> 13 segments of one chunk, a ragged last chunk
     ([1, 800, 4, 64, 64, 64, 1], ("D",)),
-    # smaller still, dstate 128
-    ([1, 300, 2, 64, 128, 128, 1], ("z", "init")),
+    # smaller still, dstate 128: 4 streams of 10 chunks -> 10 segments
+    ([1, 600, 2, 64, 128, 128, 1], ("z", "init")),
 ]
 
 
