@@ -463,8 +463,10 @@ BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
     return l;
 }
 
-// Work units of the chunk backward kernel (one workgroup per CU at a time).
-constexpr int64_t kBwdUnits = 1024;
+// Work units of the chunk backward kernel: one workgroup per CU (it holds a
+// CU's LDS), in one round, so each pays its pipeline fill once (C4: 16 (b, g)
+// streams of 32 chunks as 16 runs of 2 chunks).
+constexpr int64_t kBwdUnits = 256;
 
 bool bwd_supported(const Mamba2SsdShape *s) { return s->headdim == 64 && s->dstate == 64; }
 
@@ -519,6 +521,11 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
                     (long long)s->headdim, (long long)s->dstate);
     if (s->seqlen == 0)
         return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "mamba2_ssd_bwd_m1 needs seqlen > 0");
+    // the reverse state pass addresses a stream's chunk states with 32-bit
+    // byte offsets
+    if (nchunks(s) * 64 * 64 * 4 > (int64_t)0x7fffffff)
+        return fail(MAMBA2_SSD_ERR_UNSUPPORTED, "mamba2_ssd_bwd_m1 needs seqlen < %lld",
+                    (long long)((int64_t)0x7fffffff / (64 * 64 * 4) * 64));
     const BwdLayout lay = bwd_layout(s, f);
     if (!workspace || workspace_bytes < lay.total)
         return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", lay.total,

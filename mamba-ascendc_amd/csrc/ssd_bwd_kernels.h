@@ -145,33 +145,52 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dstate(BwdParams prm) {
 __global__ __launch_bounds__(kThreads) void k_state_pass_bwd(float *ds, const float *log_decay,
                                                              const float *dfinal, float *dinit,
                                                              int K, int PN) {
+    constexpr int D = kStateRing;
     const int64_t bh = blockIdx.y;
     const int idx = (blockIdx.x * kThreads + threadIdx.x) * 4;
     if (idx >= PN) return;
-    float *d = ds + bh * K * (int64_t)PN + idx;
-    const float *ld = log_decay + bh * K;
+    float *d = ds + bh * K * (int64_t)PN;
     float4 g = dfinal ? *(const float4 *)(dfinal + bh * PN + idx) : make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k0 = K - 1; k0 >= 0; k0 -= kStateDepth) {
-        float4 buf[kStateDepth];
-        float dec[kStateDepth];
+    // step i handles chunk K - 1 - i; a ring of D steps in flight (step i in
+    // slot i % D, loaded D steps before it is used).  The loads are
+    // unconditional (exact wait counts): a step past chunk 0 re-reads chunk 0,
+    // and its value is never used.  The caller keeps K * PN * 4 below 2^31.
+    const auto rd = buf_rsrc_n(d, K * PN * 4);
+    const auto rl = buf_rsrc_n(log_decay + bh * K, K * 4);
+    float4 buf[D];
+    float lv[D];
 #pragma unroll
-        for (int i = 0; i < kStateDepth; ++i) {
-            const int kk = k0 - i;
-            if (kk >= 0) {
-                buf[i] = *(const float4 *)(d + (int64_t)kk * PN);
-                dec[i] = __expf(ld[kk]);
-            }
+    for (int i = 0; i < D; ++i) {
+        const int k = max(K - 1 - i, 0);
+        buf[i] = buf_load4(rd, (k * PN + idx) * 4, 0);
+        lv[i] = buf_load(rl, k * 4, 0);
+    }
+    int i0 = 0;
+    for (; i0 + D <= K; i0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int k = K - 1 - (i0 + i);
+            const float dec = __expf(lv[i]);
+            *(float4 *)(d + (int64_t)k * PN + idx) = g; // dU_k: the gradient of the state leaving chunk k
+            g.x = buf[i].x + dec * g.x;
+            g.y = buf[i].y + dec * g.y;
+            g.z = buf[i].z + dec * g.z;
+            g.w = buf[i].w + dec * g.w;
+            const int kn = max(k - D, 0);
+            buf[i] = buf_load4(rd, (kn * PN + idx) * 4, 0);
+            lv[i] = buf_load(rl, kn * 4, 0);
         }
+    }
 #pragma unroll
-        for (int i = 0; i < kStateDepth; ++i) {
-            const int kk = k0 - i;
-            if (kk >= 0) {
-                *(float4 *)(d + (int64_t)kk * PN) = g;
-                g.x = buf[i].x + dec[i] * g.x;
-                g.y = buf[i].y + dec[i] * g.y;
-                g.z = buf[i].z + dec[i] * g.z;
-                g.w = buf[i].w + dec[i] * g.w;
-            }
+    for (int i = 0; i < D; ++i) {
+        if (i0 + i < K) {
+            const int k = K - 1 - (i0 + i);
+            const float dec = __expf(lv[i]);
+            *(float4 *)(d + (int64_t)k * PN + idx) = g;
+            g.x = buf[i].x + dec * g.x;
+            g.y = buf[i].y + dec * g.y;
+            g.z = buf[i].z + dec * g.z;
+            g.w = buf[i].w + dec * g.w;
         }
     }
     if (dinit) *(float4 *)(dinit + bh * PN + idx) = g;

@@ -157,8 +157,7 @@ __global__ __launch_bounds__(kThreads) void k_chunk_state(FwdParams prm) {
 // --------------------------------------------------------------------------
 // state passing (elementwise over P*N, serial over chunks)
 // --------------------------------------------------------------------------
-constexpr int kStateDepth = 8;  // batch prefetch of k_state_pass_bwd
-constexpr int kStateRing = 16;  // chunks in flight per thread in k_state_pass
+constexpr int kStateRing = 16;  // chunks in flight per thread in k_state_pass (and _bwd)
 
 #ifndef SSD_KERNEL_TEMPLATES_ONLY
 __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_states,
