@@ -410,26 +410,45 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     return ok();
 }
 
-// The reverse fused chunk backward (k_bwd_ws<., R>) walks each (b, g) stream
-// serially, carrying the state gradients of the group's R heads in
-// registers: used for R = 1, 2, 4 with at least this many streams (one
-// workgroup per CU, so fewer streams would leave CUs idle).
-constexpr int64_t kMinFusedStreams = 256;
+// Work units of the chunk backward kernel: one workgroup per CU (it holds a
+// CU's LDS), in one round, so each pays its pipeline fill once (C4: 16 (b, g)
+// streams of 32 chunks as 16 runs of 2 chunks).
+constexpr int64_t kBwdUnits = 256;
 
-bool bwd_fused_rev(const Mamba2SsdShape *s) {
-    const int64_t R = s->nheads / s->ngroups;
-    return (R == 1 || R == 2 || R == 4) && s->batch * s->ngroups >= kMinFusedStreams;
+// The reverse fused chunk backward (k_bwd_ws<., R>, R = 1, 2 or 4 heads per
+// group) walks runs of chunks from last to first, carrying the state
+// gradients of the group's R heads in registers.  With at least kBwdUnits
+// (b, g) streams each stream is one run; with fewer, each is cut into about
+// kBwdUnits / (B G) runs of M chunks, and the gradient entering every run
+// from the right comes from a pre-pass over the same runs (k_bwd_dstate_rev
+// in segment mode: each run's own contribution and log decay) and the reverse
+// recurrence over runs (k_state_pass_bwd).  nseg = 0: other R, the split path
+// (per-chunk dU through HBM).
+struct RevPlan {
+    int64_t nseg, M;
+};
+
+RevPlan bwd_rev_plan(const Mamba2SsdShape *s) {
+    const int64_t R = s->nheads / s->ngroups, K = nchunks(s), bg = s->batch * s->ngroups;
+    if (!(R == 1 || R == 2 || R == 4)) return {0, 0};
+    int64_t nseg = (kBwdUnits + bg - 1) / bg;
+    nseg = nseg < K ? nseg : K;
+    const int64_t M = (K + nseg - 1) / nseg;
+    return {(K + M - 1) / M, M};
 }
 
 // Backward workspace: states [B,H,K,P,N] and, for the recompute of long
 // sequences with few streams, the forward plan's segment states and log decays
-// (both unless SAVED_STATES) | log decay [B,H,K] | dstates [B,H,K,P,N] (unless
-// the reverse fused path runs) | dA partials [B,H,K] | ddt_bias partials
-// [B,H,K,slots] | dD partials [B,H,K,slots,P] (slots = one per consumer wave
-// of the chunk kernel).
+// (both unless SAVED_STATES) | log decay [B,H,K] | dstates [B,H,K,P,N] (split
+// path) or, for the reverse fused path with several runs per stream, the run
+// carries [B,H,nseg,P,N] and run log decays [B,H,nseg] | dA partials [B,H,K] |
+// ddt_bias partials [B,H,K,slots] | dD partials [B,H,K,slots,P] (slots = one
+// per consumer wave of the chunk kernel).
 struct BwdLayout {
-    size_t states, seg_state, seg_decay, log_decay, dstates, part_dA, part_db, part_dD, total;
+    size_t states, seg_state, seg_decay, log_decay, dstates, rev_carry, rev_decay, part_dA, part_db,
+        part_dD, total;
     FwdPlan recompute; // plan of the state recompute (when the states are not passed in)
+    RevPlan rev;
 };
 
 BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
@@ -451,8 +470,16 @@ BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
     }
     l.log_decay = off;
     off += align256(bhk * sizeof(float));
+    l.rev = bwd_rev_plan(s);
     l.dstates = off;
-    if (!bwd_fused_rev(s)) off += align256(bhk * pn * sizeof(float));
+    if (l.rev.nseg == 0) off += align256(bhk * pn * sizeof(float));
+    l.rev_carry = off;
+    if (l.rev.nseg > 1) {
+        const size_t runs = (size_t)s->batch * s->nheads * l.rev.nseg;
+        off += align256(runs * pn * sizeof(float));
+        l.rev_decay = off;
+        off += align256(runs * sizeof(float));
+    }
     l.part_dA = off;
     off += align256(bhk * sizeof(float));
     l.part_db = off;
@@ -462,11 +489,6 @@ BwdLayout bwd_layout(const Mamba2SsdShape *s, uint32_t flags) {
     l.total = off;
     return l;
 }
-
-// Work units of the chunk backward kernel: one workgroup per CU (it holds a
-// CU's LDS), in one round, so each pays its pipeline fill once (C4: 16 (b, g)
-// streams of 32 chunks as 16 runs of 2 chunks).
-constexpr int64_t kBwdUnits = 256;
 
 bool bwd_supported(const Mamba2SsdShape *s) { return s->headdim == 64 && s->dstate == 64; }
 
@@ -634,9 +656,27 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
         if (int rc = launch_status("k_fwd_seg_state_save", tr, st)) return rc;
     }
     const int64_t bg = (int64_t)B * s->ngroups;
-    if (bwd_fused_rev(s)) {
-        // one pass: reverse chunk order, state gradients carried in registers
-        ssd::launch_bwd_ws(bp.has_z != 0, bp.R, seq, dim3((unsigned)bg), st, bp, 1, K);
+    if (lay.rev.nseg > 0) {
+        // reverse chunk order, state gradients carried in registers; with
+        // several runs per stream, the gradient entering each run first
+        const int nseg = (int)lay.rev.nseg;
+        if (nseg > 1) {
+            ssd::RevSeg rs{};
+            rs.nseg = nseg;
+            rs.M = (int)lay.rev.M;
+            rs.seg_carry = (float *)(ws + lay.rev_carry);
+            rs.seg_log_decay = (float *)(ws + lay.rev_decay);
+            ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, dim3((unsigned)(B * H * nseg)), st, bp,
+                                       nullptr, nullptr, rs);
+            if (int rc = launch_status("k_bwd_dstate_rev_seg", tr, st)) return rc;
+            // in place: run s's slot becomes the gradient entering it from the right
+            hipLaunchKernelGGL(ssd::k_state_pass_bwd, state_grid, dim3(ssd::kThreads), 0, st, rs.seg_carry,
+                               rs.seg_log_decay, a->dfinal_state, (float *)nullptr, nseg, PN);
+            if (int rc = launch_status("k_state_pass_bwd", tr, st)) return rc;
+            bp.carry_in = rs.seg_carry;
+        }
+        ssd::launch_bwd_ws(bp.has_z != 0, bp.R, seq, dim3((unsigned)(bg * nseg)), st, bp, nseg,
+                           (int)lay.rev.M);
         if (int rc = launch_status("k_bwd_ws_rev", tr, st)) return rc;
         hipLaunchKernelGGL(ssd::k_bwd_finalize_slots, dim3(H), dim3(ssd::kThreads), 0, st, bp.part_dA,
                            bp.part_dbias, bp.part_dD, a->dA, a->ddt_bias, a->dD, B, H, K, 64,
@@ -646,8 +686,11 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     }
     // state gradients dU_k (and dinitial_states)
     if ((int64_t)B * H >= kMinRevStreams) {
+        ssd::RevSeg one{};
+        one.nseg = 1;
+        one.M = K;
         ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, dim3((unsigned)(B * H)), st, bp,
-                                   a->dfinal_state, a->dinitial_states);
+                                   a->dfinal_state, a->dinitial_states, one);
         if (int rc = launch_status("k_bwd_dstate_rev", tr, st)) return rc;
     } else {
         hipLaunchKernelGGL(ssd::bwd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);

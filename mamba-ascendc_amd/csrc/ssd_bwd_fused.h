@@ -53,12 +53,14 @@ constexpr int kBwsSlots = 4;      // partial sums per (b, h, k): one per consume
 namespace bwd {
 
 // kRevR = 0: steps in chunk order, the state gradients dU_k read from
-// prm.dstates.  kRevR = R (1, 2 or 4 heads per group, one run per stream):
-// chunks from last to first, and the producers carry each head's state
-// gradient g in registers (the reverse recurrence of k_bwd_dstate_rev fused
-// in), so no dU reaches HBM:
+// prm.dstates.  kRevR = R (1, 2 or 4 heads per group): chunks from last to
+// first, and the producers carry each head's state gradient g in registers
+// (the reverse recurrence of k_bwd_dstate_rev fused in), so no dU reaches HBM:
 //   dU_k = g;   g <- dSoff_k + exp(cs_last_k) g,   dSoff_k = (gy exp(cs))^T C,
-// starting from dfinal_state and ending at dinitial_states.
+// starting from dfinal_state and ending at dinitial_states.  With nseg > 1
+// runs per stream, run sg starts from prm.carry_in (the gradient entering it
+// from the right, given by the segment pre-pass and recurrence) and only run 0
+// writes dinitial_states.
 //
 // kSeq: packed sequences (prm.seq_idx), the forward's masks in adjoint form:
 // W (and so dW, dCB and their dcs terms) only between equal ids, the state
@@ -194,16 +196,21 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         const int acc_off = (r16 * N + 16 * pw + 4 * kq) * 4; // bytes, + 16 pb rows
         if constexpr (kRev) {
 #pragma unroll
-            for (int rr = 0; rr < kRevR; ++rr)
+            for (int rr = 0; rr < kRevR; ++rr) {
+                // the gradient of the state leaving the run's last chunk: the
+                // segment recurrence's (segmented) or dfinal_state
+                const int64_t bh = (int64_t)b * H + g * R + rr;
+                const float *cin = prm.carry_in ? prm.carry_in + (bh * nseg + sg) * (P * N)
+                                                : (prm.dfinal ? prm.dfinal + bh * (P * N) : nullptr);
 #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) {
                     gc[rr][pb] = zero4();
-                    if (prm.dfinal) {
-                        const float4 v = *(const float4 *)((const char *)(prm.dfinal +
-                            ((int64_t)b * H + g * R + rr) * (P * N)) + acc_off + 16 * pb * N * 4);
+                    if (cin) {
+                        const float4 v = *(const float4 *)((const char *)cin + acc_off + 16 * pb * N * 4);
                         gc[rr][pb] = f32x4{v.x, v.y, v.z, v.w};
                     }
                 }
+            }
         }
         auto load_su = [&](int n) __attribute__((always_inline)) {
             n = min(n, NS - 1);
@@ -447,8 +454,8 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                     rev_step(n0 + 3, I3{});
                 }
             }
-            // the carries now hold the gradients of the initial states
-            if (prm.dinit) {
+            // the carries of the first run now hold the gradients of the initial states
+            if (prm.dinit && sg == 0) {
 #pragma unroll
                 for (int rr = 0; rr < kRevR; ++rr)
 #pragma unroll
@@ -783,9 +790,17 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 // (state_passing_bwd/design.md:44-61) with the dS_off product fused in.
 // kSeq: packed sequences, exp(cs_t) only for tokens that read the entering
 // state and the carry only where the state is not cut (as in k_bwd_ws).
+//
+// Segments (rs.seg_carry non-NULL): one workgroup per (b, h, segment of rs.M
+// chunks) walks its chunks from last to first starting from a zero gradient,
+// writes no per-chunk dU, and leaves the segment's contribution to the
+// gradient entering it from the right in rs.seg_carry [B, H, nseg, P, N] and
+// the segment's total log decay (natural units; -inf where a packed sequence
+// cuts the state) in rs.seg_log_decay [B, H, nseg]: the pre-pass of the
+// segmented reverse fused backward.
 template <bool kHasZ, bool kSeq = false>
 __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, const float *dfinal,
-                                                                float *dinit) {
+                                                                float *dinit, RevSeg rs) {
     constexpr int T = 64, P = 64, N = 64;
     __shared__ __attribute__((aligned(16))) __bf16 lds[8 * kTile]; // GE(s), CT(s), s = 0, 1
     __shared__ float s_alpha[2];
@@ -794,10 +809,14 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
     const int w = wave & 3, r16 = lane & 15, kq = lane >> 4;
     auto GE = [&](int s) { return tile_at(lds, 2 * s); };
     auto CT = [&](int s) { return tile_at(lds, 2 * s + 1); };
+    // unit = ((b * G + g) * nseg + sg) * R + r
     const int u = xcd_unit(blockIdx.x, (int)gridDim.x, prm.R);
-    const int r = u % prm.R, bg = u / prm.R;
+    const int r = u % prm.R, sg = (u / prm.R) % rs.nseg, bg = u / (prm.R * rs.nseg);
     const int g = bg % prm.G, b = bg / prm.G, h = g * prm.R + r;
     const int H = prm.H, G = prm.G, K = prm.K;
+    const int kbeg = sg * rs.M, kend = min(kbeg + rs.M, K);
+    const int nsteps = kend - kbeg; // step i handles chunk kend - 1 - i
+    const bool segmented = rs.seg_carry != nullptr;
     const int rowHP4 = H * P * 4, rowGN4 = G * N * 4;
     auto tvalid = [&](int k) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
 
@@ -819,8 +838,8 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         // chunk read through an empty-range resource (zeros, no traffic)
         auto p_load = [&](int i, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
-            const bool real = i < K;
-            const int k = real ? K - 1 - i : 0, tv = tvalid(k);
+            const bool real = i < nsteps;
+            const int k = real ? kend - 1 - i : kbeg, tv = tvalid(k);
             const int range = real ? 0x7fffffff : 0;
             const int64_t t0 = (int64_t)k * T;
             const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
@@ -843,9 +862,11 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
             }
         };
         auto put = [&](SplitTile d, int row, float4 v) { store_split4(d, row * kTS + c4, v); };
+        float ld_sum = 0.f; // the segment's log2 decay (lane 0 of producer wave 0)
+        bool cut = false;
         auto p_stage = [&](int i, int s, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
-            const int tv = i < K ? tvalid(K - 1 - i) : 0; // nothing valid past the first chunk
+            const int tv = i < nsteps ? tvalid(kend - 1 - i) : 0; // nothing valid past the first chunk
             float a = 0.f;
             if (lane < tv) a = Ah2 * discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
             const float cs = wave_inclusive_scan(a); // log2 units
@@ -855,7 +876,13 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
                 reads = sidr[sl] == sprv[sl] ? 1.f : 0.f;
                 carry = e_end == sprv[sl] ? 1.f : 0.f;
             }
-            if (w == 0 && lane == 0) s_alpha[s] = exp2_f(readlane_f(cs, T - 1)) * carry;
+            if (w == 0 && lane == 0) {
+                s_alpha[s] = exp2_f(readlane_f(cs, T - 1)) * carry;
+                if (i < nsteps) {
+                    ld_sum += readlane_f(cs, T - 1);
+                    cut = cut || carry == 0.f;
+                }
+            }
             const float ecs = exp2_f(cs) * reads;
             const SplitTile ge = GE(s), ct = CT(s);
 #pragma unroll
@@ -892,13 +919,15 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         };
         // whole rounds of the ring, then the 0..2 remaining steps
         int i0 = 0;
-        for (; i0 + kDepth <= K; i0 += kDepth) {
+        for (; i0 + kDepth <= nsteps; i0 += kDepth) {
             p_iter(i0, S1{});
             p_iter(i0 + 1, S2{});
             p_iter(i0 + 2, S0{});
         }
-        if (i0 < K) p_iter(i0, S1{});
-        if (i0 + 1 < K) p_iter(i0 + 1, S2{});
+        if (i0 < nsteps) p_iter(i0, S1{});
+        if (i0 + 1 < nsteps) p_iter(i0 + 1, S2{});
+        if (segmented && w == 0 && lane == 0)
+            rs.seg_log_decay[((int64_t)b * H + h) * rs.nseg + sg] = cut ? -INFINITY : ld_sum * kLn2;
         return;
     }
 
@@ -908,7 +937,7 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
     const int64_t bh = (int64_t)b * H + h;
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb) {
-        if (dfinal) {
+        if (dfinal && !segmented) {
             const float4 v = *(const float4 *)(dfinal + bh * (P * N) + (16 * pb + r16) * N + 16 * w + 4 * kq);
             gs[pb] = f32x4{v.x, v.y, v.z, v.w};
         } else {
@@ -916,13 +945,15 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         }
     }
     lds_barrier();
-    for (int i = 0; i < K; ++i) {
-        const int k = K - 1 - i, s = i & 1;
-        float *du = prm.dstates + (bh * K + k) * (int64_t)(P * N);
+    for (int i = 0; i < nsteps; ++i) {
+        const int k = kend - 1 - i, s = i & 1;
+        if (!segmented) {
+            float *du = prm.dstates + (bh * K + k) * (int64_t)(P * N);
 #pragma unroll
-        for (int pb = 0; pb < 4; ++pb)
-            *(float4 *)(du + (16 * pb + r16) * N + 16 * w + 4 * kq) =
-                make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
+            for (int pb = 0; pb < 4; ++pb)
+                *(float4 *)(du + (16 * pb + r16) * N + 16 * w + 4 * kq) =
+                    make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
+        }
         const SplitTile ge = GE(s), ct = CT(s);
         f32x4 U[4];
 #pragma unroll
@@ -940,10 +971,12 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
             for (int ii = 0; ii < 4; ++ii) gs[pb][ii] = alpha * gs[pb][ii] + U[pb][ii];
         lds_barrier(); // buffer s is free, buffer s ^ 1 is staged
     }
-    if (dinit) {
+    float *dst = segmented ? rs.seg_carry + (bh * rs.nseg + sg) * (P * N)
+                           : (dinit ? dinit + bh * (P * N) : nullptr);
+    if (dst) {
 #pragma unroll
         for (int pb = 0; pb < 4; ++pb)
-            *(float4 *)(dinit + bh * (P * N) + (16 * pb + r16) * N + 16 * w + 4 * kq) =
+            *(float4 *)(dst + (16 * pb + r16) * N + 16 * w + 4 * kq) =
                 make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
     }
 }

@@ -40,10 +40,19 @@ struct BwdParams {
     float *part_dA;         // [B, H, K]
     float *part_dbias;      // [B, H, K]
     float *part_dD;         // [B, H, K, P] (per-channel D) or [B, H, K]
+    const float *carry_in;  // [B, H, nseg, P, N] gradient entering each run of the reverse
+                            // fused kernel from the right, or NULL (one run: dfinal)
     int64_t L;
     int H, G, R, K;
     int softplus, has_D, d_per_channel, has_z;
     float lo, hi;
+};
+
+// Segments of the reverse state-gradient pre-pass (k_bwd_dstate_rev): nseg
+// runs of M chunks per (b, h); seg_carry NULL = one run over all chunks.
+struct RevSeg {
+    int nseg, M;
+    float *seg_carry, *seg_log_decay;
 };
 
 // q, cs and dq/ddt of the tokens of one chunk, by wave 0.  Returns this lane's cs.

@@ -24,8 +24,9 @@ void run_ws(dim3 grid, hipStream_t st, const BwdParams &bp, int nseg, int M) {
 }
 
 template <bool kSeq>
-void run_rev(dim3 grid, hipStream_t st, const BwdParams &bp, const float *dfinal, float *dinit) {
-    hipLaunchKernelGGL((bwd::k_bwd_dstate_rev<kZ, kSeq>), grid, dim3(kWsThreads), 0, st, bp, dfinal, dinit);
+void run_rev(dim3 grid, hipStream_t st, const BwdParams &bp, const float *dfinal, float *dinit,
+             const RevSeg &rs) {
+    hipLaunchKernelGGL((bwd::k_bwd_dstate_rev<kZ, kSeq>), grid, dim3(kWsThreads), 0, st, bp, dfinal, dinit, rs);
 }
 
 }  // namespace
@@ -42,8 +43,8 @@ void SSD_CAT(launch_bwd_ws_z, SSD_BWD_Z)(int rev_r, bool seq, dim3 grid, hipStre
 
 void SSD_CAT(launch_bwd_dstate_rev_z, SSD_BWD_Z)(bool seq, dim3 grid, hipStream_t st,
                                                   const BwdParams &bp, const float *dfinal,
-                                                  float *dinit) {
-    (seq ? run_rev<true> : run_rev<false>)(grid, st, bp, dfinal, dinit);
+                                                  float *dinit, const RevSeg &rs) {
+    (seq ? run_rev<true> : run_rev<false>)(grid, st, bp, dfinal, dinit, rs);
 }
 
 }  // namespace ssd

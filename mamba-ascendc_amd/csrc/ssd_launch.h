@@ -26,9 +26,9 @@ void launch_bwd_ws_z0(int rev_r, bool seq, dim3 grid, hipStream_t st, const BwdP
 void launch_bwd_ws_z1(int rev_r, bool seq, dim3 grid, hipStream_t st, const BwdParams &bp, int nseg,
                       int M);
 void launch_bwd_dstate_rev_z0(bool seq, dim3 grid, hipStream_t st, const BwdParams &bp,
-                              const float *dfinal, float *dinit);
+                              const float *dfinal, float *dinit, const RevSeg &rs);
 void launch_bwd_dstate_rev_z1(bool seq, dim3 grid, hipStream_t st, const BwdParams &bp,
-                              const float *dfinal, float *dinit);
+                              const float *dfinal, float *dinit, const RevSeg &rs);
 
 // k_bwd_ws<has_z, rev_r, seq> (rev_r 0, 1, 2 or 4)
 inline void launch_bwd_ws(bool has_z, int rev_r, bool seq, dim3 grid, hipStream_t st,
@@ -39,9 +39,10 @@ inline void launch_bwd_ws(bool has_z, int rev_r, bool seq, dim3 grid, hipStream_
 
 // k_bwd_dstate_rev<has_z, seq>
 inline void launch_bwd_dstate_rev(bool has_z, bool seq, dim3 grid, hipStream_t st,
-                                  const BwdParams &bp, const float *dfinal, float *dinit) {
-    if (has_z) launch_bwd_dstate_rev_z1(seq, grid, st, bp, dfinal, dinit);
-    else launch_bwd_dstate_rev_z0(seq, grid, st, bp, dfinal, dinit);
+                                  const BwdParams &bp, const float *dfinal, float *dinit,
+                                  const RevSeg &rs) {
+    if (has_z) launch_bwd_dstate_rev_z1(seq, grid, st, bp, dfinal, dinit, rs);
+    else launch_bwd_dstate_rev_z0(seq, grid, st, bp, dfinal, dinit, rs);
 }
 
 }  // namespace ssd

@@ -83,9 +83,16 @@ CASES = [
     ([2, 192, 4, 64, 64, 64, 2], ("bias",), True, (0.0, math.inf), "out"),    # output-only
     ([2, 192, 4, 64, 64, 128, 2], ("init",), True, (0.0, math.inf), "final"), # final-only
     ([1, 320, 16, 64, 64, 64, 2], ("D",), True, (0.0, math.inf), "both"),    # 8 heads per group
+    ([1, 260, 12, 64, 64, 64, 4], ("z", "init"), True, (0.0, math.inf), "both"),  # 3 heads per group
+    # fewer than 256 (b, g) streams with 1, 2 or 4 heads per group: reverse
+    # runs of M chunks (here 2, the last run 1 chunk with a ragged tail), the
+    # gradient entering each run from a pre-pass and the recurrence over runs
+    ([4, 1700, 8, 64, 64, 64, 4], ("D", "z", "init"), True, (0.0, math.inf), "both"),
+    ([2, 2600, 4, 64, 64, 64, 4], ("D2", "bias"), True, (0.0, math.inf), "final"),
     # >= 512 (b, h) streams: the fused reverse state-gradient pass
     ([2, 200, 256, 64, 64, 64, 64], ("D2", "z", "bias", "init"), True, (0.0, math.inf), "both"),
     ([1, 192, 512, 64, 64, 64, 128], (), True, (0.0, math.inf), "final"),
+    ([2, 150, 256, 64, 64, 64, 32], ("z", "init"), True, (0.0, math.inf), "both"),  # 8 heads per group
     # >= 256 (b, g) streams with 1, 2 or 4 heads per group: one reverse pass
     # with the state gradients carried in the chunk kernel
     ([4, 200, 256, 64, 64, 64, 64], ("D2", "z", "bias", "init"), True, (0.0, math.inf), "both"),
@@ -314,10 +321,11 @@ def test_ssdcore_module_trains():
 
 
 @pytest.mark.parametrize("shape,features,packed", [
-    ([2, 700, 8, 64, 64, 64, 2], ("D", "z", "bias", "init"), False),    # split path, segmented recompute
-    ([4, 330, 256, 64, 64, 64, 64], ("D2", "bias"), False),            # fused reverse, one segment
+    ([2, 700, 8, 64, 64, 64, 2], ("D", "z", "bias", "init"), False),    # reverse runs, segmented recompute
+    ([4, 330, 256, 64, 64, 64, 64], ("D2", "bias"), False),            # fused reverse, one run per stream
     ([2, 400, 16, 64, 64, 128, 4], ("z", "init"), True),               # packed sequences
-], ids=["split-segments", "fused-reverse", "packed"])
+    ([1, 700, 16, 64, 64, 64, 2], ("D", "init"), False),               # split path (8 heads per group)
+], ids=["reverse-runs", "fused-reverse", "packed", "split"])
 def test_training_policy_recompute_matches_saved(shape, features, packed):
     """The save-vs-recompute policy (TrainingPolicy.save_chunk_states) changes
     what autograd keeps between the passes, not the gradients: the backward

@@ -129,10 +129,13 @@ def test_forward_writes_stay_in_bounds(shape, feats, extra):
 
 
 BWD = [
-    ([2, 200, 4, 64, 64, 64, 2], ("D2", "z", "bias", "init"), True),    # split path, ragged
-    ([1, 700, 8, 64, 64, 64, 2], ("D",), False),                        # split path, segmented recompute
+    ([2, 200, 4, 64, 64, 64, 2], ("D2", "z", "bias", "init"), True),    # reverse runs of 1 chunk, ragged
+    ([1, 700, 8, 64, 64, 64, 2], ("D",), False),                        # reverse runs, segmented recompute
+    ([4, 2200, 8, 64, 64, 64, 4], ("D", "z", "init"), False),           # runs of 3 chunks, last of 2
+    ([2, 300, 16, 64, 64, 64, 2], ("z", "init"), True),                 # split path (8 heads per group)
     ([4, 150, 256, 64, 64, 64, 64], ("z", "init"), True),               # fused reverse, R = 4
-    ([2, 100, 512, 64, 64, 64, 128], ("D", "bias"), False),             # reverse dstate pass
+    ([2, 100, 512, 64, 64, 64, 128], ("D", "bias"), False),             # fused reverse, R = 4
+    ([2, 100, 256, 64, 64, 64, 32], ("z", "init"), True),               # reverse dstate pass (R = 8)
 ]
 
 
