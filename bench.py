@@ -105,7 +105,8 @@ def fwd_segments(shape):
     fwd_plan): dstate 128 runs two workgroups per head; with fewer than 256
     (b, h, half) streams the sequence is cut into segments (when that saves at
     least 6 chunk steps), and the state-only pass runs on segments twice as
-    fine."""
+    fine (only those before the last full segment when the full segments
+    fold them into their entering states themselves)."""
     b, l, h, p, n, _chunk, g = shape
     k = math.ceil(l / EXEC_CHUNK)
     nsplit = n // 64
@@ -119,7 +120,12 @@ def fwd_segments(shape):
     mt = math.ceil(k / nseg)
     mult = min(2, mt)
     mp = math.ceil(mt / mult)
-    return math.ceil(k / (mult * mp)), math.ceil(k / mp), nsplit
+    nseg = math.ceil(k / (mult * mp))
+    if (nseg - 1) * mult <= 8:
+        # each full segment folds the pre-segments before it: the last full
+        # segment's own pre-segments are not computed
+        return nseg, (nseg - 1) * mult, nsplit
+    return nseg, math.ceil(k / mp), nsplit
 
 
 def fwd_kernel_model(name: str, shape) -> dict:

@@ -101,11 +101,17 @@ int64_t nchunks(const Mamba2SsdShape *s) { return (s->seqlen + ssd::kChunk - 1) 
 constexpr int64_t kMinStreams = SSD_MIN_STREAMS;
 constexpr int64_t kPreMult = SSD_PRE_MULT;
 constexpr int64_t kMinSavedChunks = 6;
+// With at most this many pre-segments before the last full segment, each full
+// segment folds the pre-segment contributions onto the initial states in its
+// own prologue (independent loads, a few us) instead of a separate segment
+// recurrence launch (k_state_pass, about 6 us plus a launch gap at C4).
+constexpr int64_t kFoldMax = 8;
 
 struct FwdPlan {
     bool fused = false;
     int nseg = 1, M = 1, nsplit = 1;     // nsplit: workgroups per head (2 for dstate 128)
     int nseg_pre = 1, M_pre = 1, mult = 1; // segments of the state-only pass (nseg > 1)
+    bool fold = false;                     // full segments fold the pre-segments themselves
     size_t seg_state = 0, seg_decay = 0; // workspace offsets (fused, nseg > 1)
     size_t states = 0;                   // chunk states for VARLEN_STATES without SAVED_STATES
     size_t ws = 0;
@@ -156,6 +162,9 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags) {
             pl.M = (int)(mult * Mp);
             pl.nseg = (int)((K + pl.M - 1) / pl.M);
             pl.nseg_pre = (int)((K + Mp - 1) / Mp);
+            pl.fold = (int64_t)(pl.nseg - 1) * pl.mult <= kFoldMax;
+            // folded, only the pre-segments before the last full segment are read
+            if (pl.fold) pl.nseg_pre = (pl.nseg - 1) * pl.mult;
         } else {
             pl.M = (int)K;
         }
@@ -368,15 +377,21 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
             const unsigned pre_units = (unsigned)(vs.batch * vs.nheads * pl.nseg_pre * pl.nsplit);
             ssd::launch_fwd_seg(true, false, false, seq, dim3(pre_units), st, kp, pre);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
-            const int PN = (int)(vs.headdim * vs.dstate);
-            const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
-            hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, pre.seg_state,
-                               pre.seg_log_decay, prm.init, pre.seg_state, prm.final_state, pl.nseg_pre, PN);
-            if (int rc = launch_status("k_state_pass", tr, st)) return rc;
             sp.seg_in = pre.seg_state;
             sp.seg_in_n = pl.nseg_pre;
             sp.in_mult = pl.mult;
-            sp.write_final = 0;
+            if (pl.fold) {
+                // each full segment folds the contributions itself; the last writes the final state
+                sp.seg_in_log_decay = pre.seg_log_decay;
+                sp.write_final = 1;
+            } else {
+                const int PN = (int)(vs.headdim * vs.dstate);
+                const dim3 sgrid((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * prm.H);
+                hipLaunchKernelGGL(ssd::k_state_pass, sgrid, dim3(ssd::kThreads), 0, st, pre.seg_state,
+                                   pre.seg_log_decay, prm.init, pre.seg_state, prm.final_state, pl.nseg_pre, PN);
+                if (int rc = launch_status("k_state_pass", tr, st)) return rc;
+                sp.write_final = 0;
+            }
         } else {
             sp.write_final = 1;
         }
@@ -644,10 +659,14 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
             pre.seg_log_decay = (float *)(ws + lay.seg_decay);
             ssd::launch_fwd_seg(true, false, false, seq, dim3((unsigned)(B * H * pre.nseg)), st, kp, pre);
             if (int rc = launch_status("k_fwd_seg_state", tr, st)) return rc;
-            hipLaunchKernelGGL(ssd::k_state_pass, dim3((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * H),
-                               dim3(ssd::kThreads), 0, st, pre.seg_state, pre.seg_log_decay, fp.init,
-                               pre.seg_state, (float *)nullptr, pre.nseg, PN);
-            if (int rc = launch_status("k_state_pass", tr, st)) return rc;
+            if (lay.recompute.fold) {
+                sp.seg_in_log_decay = pre.seg_log_decay;
+            } else {
+                hipLaunchKernelGGL(ssd::k_state_pass, dim3((PN / 4 + ssd::kThreads - 1) / ssd::kThreads, B * H),
+                                   dim3(ssd::kThreads), 0, st, pre.seg_state, pre.seg_log_decay, fp.init,
+                                   pre.seg_state, (float *)nullptr, pre.nseg, PN);
+                if (int rc = launch_status("k_state_pass", tr, st)) return rc;
+            }
             sp.seg_in = pre.seg_state;
             sp.seg_in_n = pre.nseg;
             sp.in_mult = lay.recompute.mult;
@@ -666,7 +685,8 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
             rs.M = (int)lay.rev.M;
             rs.seg_carry = (float *)(ws + lay.rev_carry);
             rs.seg_log_decay = (float *)(ws + lay.rev_decay);
-            ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, dim3((unsigned)(B * H * nseg)), st, bp,
+            // all R heads of a (b, g) run in one workgroup (R = 1, 2 or 4 here)
+            ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, bp.R, dim3((unsigned)(bg * nseg)), st, bp,
                                        nullptr, nullptr, rs);
             if (int rc = launch_status("k_bwd_dstate_rev_seg", tr, st)) return rc;
             // in place: run s's slot becomes the gradient entering it from the right
@@ -689,7 +709,7 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
         ssd::RevSeg one{};
         one.nseg = 1;
         one.M = K;
-        ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, dim3((unsigned)(B * H)), st, bp,
+        ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, 1, dim3((unsigned)(B * H)), st, bp,
                                    a->dfinal_state, a->dinitial_states, one);
         if (int rc = launch_status("k_bwd_dstate_rev", tr, st)) return rc;
     } else {

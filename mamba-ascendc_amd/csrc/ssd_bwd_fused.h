@@ -778,29 +778,35 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     }
 }
 
-// Reverse state-gradient pass, one workgroup per (b, h) stream walking the
-// chunks from last to first with the state gradient g in registers:
+// Reverse state-gradient pass: each workgroup walks a run of chunks from last
+// to first with the state gradient g of kHeads heads (of one group) in
+// registers:
 //   dU_k = g;   g <- dSoff_k + exp(cs_last_k) g,   dSoff_k = (gy exp(cs))^T C
-// starting from g = dfinal_state; g at the end is dinitial_states.  dU_k (the
-// gradient of the state leaving chunk k) goes to prm.dstates.  The per-chunk
-// dS_off never reaches HBM.  Producer waves stage gy exp(cs) and C of the next
-// chunk (token-major, split fp16) while the consumer waves run the product
+// Step i handles chunk kend - 1 - i / kHeads, head h0 + i % kHeads, so the
+// heads of a chunk follow each other and share its C rows (read once from
+// HBM, then from L2).  Producer waves stage gy exp(cs) and C of the next step
+// (token-major, split bf16) while the consumer waves run the product
 // dSoff^T[n][p] = sum_t C[t][n] (gy exp(cs))[t][p], read transposed from LDS.
 // The recurrence is that of mamba_ascendc/csrc/ops/mamba2_ssd_state_passing_bwd
 // (state_passing_bwd/design.md:44-61) with the dS_off product fused in.
 // kSeq: packed sequences, exp(cs_t) only for tokens that read the entering
 // state and the carry only where the state is not cut (as in k_bwd_ws).
 //
-// Segments (rs.seg_carry non-NULL): one workgroup per (b, h, segment of rs.M
-// chunks) walks its chunks from last to first starting from a zero gradient,
-// writes no per-chunk dU, and leaves the segment's contribution to the
-// gradient entering it from the right in rs.seg_carry [B, H, nseg, P, N] and
-// the segment's total log decay (natural units; -inf where a packed sequence
-// cuts the state) in rs.seg_log_decay [B, H, nseg]: the pre-pass of the
-// segmented reverse fused backward.
-template <bool kHasZ, bool kSeq = false>
+// Whole streams (rs.seg_carry NULL, kHeads = 1): one workgroup per (b, h),
+// starting from g = dfinal_state; dU_k goes to prm.dstates and the final g is
+// dinitial_states.  The per-chunk dS_off never reaches HBM.
+//
+// Runs (rs.seg_carry non-NULL): one workgroup per (b, heads h0 .. h0 + kHeads
+// - 1, run of rs.M chunks), starting from a zero gradient and writing no
+// per-chunk dU; it leaves each head's run contribution to the gradient
+// entering the run from the right in rs.seg_carry [B, H, nseg, P, N] and the
+// run's total log decay (natural units; -inf where a packed sequence cuts the
+// state) in rs.seg_log_decay [B, H, nseg]: the pre-pass of the segmented
+// reverse fused backward.
+template <bool kHasZ, bool kSeq, int kHeads>
 __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, const float *dfinal,
                                                                 float *dinit, RevSeg rs) {
+    static_assert(kHeads == 1 || kHeads == 2 || kHeads == 4, "heads per workgroup");
     constexpr int T = 64, P = 64, N = 64;
     __shared__ __attribute__((aligned(16))) __bf16 lds[8 * kTile]; // GE(s), CT(s), s = 0, 1
     __shared__ float s_alpha[2];
@@ -809,37 +815,37 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
     const int w = wave & 3, r16 = lane & 15, kq = lane >> 4;
     auto GE = [&](int s) { return tile_at(lds, 2 * s); };
     auto CT = [&](int s) { return tile_at(lds, 2 * s + 1); };
-    // unit = ((b * G + g) * nseg + sg) * R + r
-    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, prm.R);
-    const int r = u % prm.R, sg = (u / prm.R) % rs.nseg, bg = u / (prm.R * rs.nseg);
-    const int g = bg % prm.G, b = bg / prm.G, h = g * prm.R + r;
+    // unit = ((b * G + g) * nseg + sg) * (R / kHeads) + head block
+    const int nhb = prm.R / kHeads;
+    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, nhb);
+    const int hb = u % nhb, sg = (u / nhb) % rs.nseg, bg = u / (nhb * rs.nseg);
+    const int g = bg % prm.G, b = bg / prm.G, h0 = g * prm.R + hb * kHeads;
     const int H = prm.H, G = prm.G, K = prm.K;
     const int kbeg = sg * rs.M, kend = min(kbeg + rs.M, K);
-    const int nsteps = kend - kbeg; // step i handles chunk kend - 1 - i
+    const int nsteps = (kend - kbeg) * kHeads;
     const bool segmented = rs.seg_carry != nullptr;
     const int rowHP4 = H * P * 4, rowGN4 = G * N * 4;
     auto tvalid = [&](int k) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
 
     if (wave >= 4) {
         // ---------------------------------------------------------- producers
-        // ring of kDepth register slots; step i (chunk K - 1 - i) uses slot i % kDepth
+        // ring of kDepth register slots; step i uses slot i % kDepth
         constexpr int kDepth = 3;
         const int pt = tid - 4 * kWave;
         const int rt = pt >> 4, c4 = (pt & 15) * 4; // rows rt + 16 j, columns c4 .. c4 + 3
         const bool has_dout = prm.dout != nullptr;
         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float Ah2 = prm.A[h] * kLog2e;
-        const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
         float4 gr[kDepth][4], zr[kDepth][4], cr[kDepth][4];
         float dtr[kDepth];
         int sidr[kDepth], sprv[kDepth]; // kSeq: id of token `lane`, id of the token before the chunk
         // unconditional loads (exact wait counts): rows past the sequence end
-        // re-read its last row (zeroed when staged), steps past the first
-        // chunk read through an empty-range resource (zeros, no traffic)
+        // re-read its last row (zeroed when staged), steps past the run read
+        // through an empty-range resource (zeros, no traffic)
         auto p_load = [&](int i, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
             const bool real = i < nsteps;
-            const int k = real ? kend - 1 - i : kbeg, tv = tvalid(k);
+            const int k = real ? kend - 1 - i / kHeads : kbeg, tv = tvalid(k);
+            const int h = h0 + (real ? i % kHeads : 0);
             const int range = real ? 0x7fffffff : 0;
             const int64_t t0 = (int64_t)k * T;
             const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
@@ -862,14 +868,25 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
             }
         };
         auto put = [&](SplitTile d, int row, float4 v) { store_split4(d, row * kTS + c4, v); };
-        float ld_sum = 0.f; // the segment's log2 decay (lane 0 of producer wave 0)
-        bool cut = false;
+        // each head's run log2 decay and cut flag (lane 0 of producer wave 0)
+        float ld_sum[kHeads];
+        bool cut[kHeads];
+#pragma unroll
+        for (int rr = 0; rr < kHeads; ++rr) {
+            ld_sum[rr] = 0.f;
+            cut[rr] = false;
+        }
         auto p_stage = [&](int i, int s, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
-            const int tv = i < nsteps ? tvalid(kend - 1 - i) : 0; // nothing valid past the first chunk
+            const bool real = i < nsteps;
+            const int hi = real ? i % kHeads : 0;
+            const int tv = real ? tvalid(kend - 1 - i / kHeads) : 0; // nothing valid past the run
+            const float Ah2 = prm.A[h0 + hi] * kLog2e;
+            const float bias = prm.dt_bias ? prm.dt_bias[h0 + hi] : 0.f;
             float a = 0.f;
             if (lane < tv) a = Ah2 * discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
             const float cs = wave_inclusive_scan(a); // log2 units
+            const float cs_last = readlane_f(cs, T - 1);
             float reads = 1.f, carry = 1.f;
             if (kSeq) {
                 const int e_end = __shfl(sidr[sl], T - 1, kWave);
@@ -877,11 +894,13 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
                 carry = e_end == sprv[sl] ? 1.f : 0.f;
             }
             if (w == 0 && lane == 0) {
-                s_alpha[s] = exp2_f(readlane_f(cs, T - 1)) * carry;
-                if (i < nsteps) {
-                    ld_sum += readlane_f(cs, T - 1);
-                    cut = cut || carry == 0.f;
-                }
+                s_alpha[s] = exp2_f(cs_last) * carry;
+#pragma unroll
+                for (int rr = 0; rr < kHeads; ++rr)
+                    if (real && hi == rr) {
+                        ld_sum[rr] += cs_last;
+                        cut[rr] = cut[rr] || carry == 0.f;
+                    }
             }
             const float ecs = exp2_f(cs) * reads;
             const SplitTile ge = GE(s), ct = CT(s);
@@ -926,33 +945,39 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         }
         if (i0 < nsteps) p_iter(i0, S1{});
         if (i0 + 1 < nsteps) p_iter(i0 + 1, S2{});
-        if (segmented && w == 0 && lane == 0)
-            rs.seg_log_decay[((int64_t)b * H + h) * rs.nseg + sg] = cut ? -INFINITY : ld_sum * kLn2;
+        if (segmented && w == 0 && lane == 0) {
+#pragma unroll
+            for (int rr = 0; rr < kHeads; ++rr)
+                rs.seg_log_decay[((int64_t)b * H + h0 + rr) * rs.nseg + sg] =
+                    cut[rr] ? -INFINITY : ld_sum[rr] * kLn2;
+        }
         return;
     }
 
     // -------------------------------------------------------------- consumers
-    // g[p = 16 pb + l % 16][n = 16 w + 4 (l / 16) + i] in gs[pb][i]
-    f32x4 gs[4];
-    const int64_t bh = (int64_t)b * H + h;
+    // g[p = 16 pb + l % 16][n = 16 w + 4 (l / 16) + i] of head rr in gs[rr][pb][i]
+    f32x4 gs[kHeads][4];
+    const int goff = (r16 * N + 16 * w + 4 * kq); // + 16 pb N
 #pragma unroll
-    for (int pb = 0; pb < 4; ++pb) {
-        if (dfinal && !segmented) {
-            const float4 v = *(const float4 *)(dfinal + bh * (P * N) + (16 * pb + r16) * N + 16 * w + 4 * kq);
-            gs[pb] = f32x4{v.x, v.y, v.z, v.w};
-        } else {
-            gs[pb] = zero4();
+    for (int rr = 0; rr < kHeads; ++rr)
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb) {
+            gs[rr][pb] = zero4();
+            if (dfinal && !segmented) {
+                const float4 v = *(const float4 *)(dfinal + ((int64_t)b * H + h0 + rr) * (P * N) + goff + 16 * pb * N);
+                gs[rr][pb] = f32x4{v.x, v.y, v.z, v.w};
+            }
         }
-    }
     lds_barrier();
-    for (int i = 0; i < nsteps; ++i) {
-        const int k = kend - 1 - i, s = i & 1;
+    auto c_step = [&](int i, auto rr_c) __attribute__((always_inline)) {
+        constexpr int rr = decltype(rr_c)::value;
+        const int k = kend - 1 - i / kHeads, s = i & 1;
         if (!segmented) {
-            float *du = prm.dstates + (bh * K + k) * (int64_t)(P * N);
+            float *du = prm.dstates + ((((int64_t)b * H + h0 + rr) * K + k) * (P * N));
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb)
-                *(float4 *)(du + (16 * pb + r16) * N + 16 * w + 4 * kq) =
-                    make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
+                *(float4 *)(du + goff + 16 * pb * N) =
+                    make_float4(gs[rr][pb][0], gs[rr][pb][1], gs[rr][pb][2], gs[rr][pb][3]);
         }
         const SplitTile ge = GE(s), ct = CT(s);
         f32x4 U[4];
@@ -968,16 +993,32 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
 #pragma unroll
         for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) gs[pb][ii] = alpha * gs[pb][ii] + U[pb][ii];
+            for (int ii = 0; ii < 4; ++ii) gs[rr][pb][ii] = alpha * gs[rr][pb][ii] + U[pb][ii];
         lds_barrier(); // buffer s is free, buffer s ^ 1 is staged
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    for (int i = 0; i < nsteps; i += kHeads) {
+        c_step(i, I0{});
+        if constexpr (kHeads >= 2) c_step(i + 1, I1{});
+        if constexpr (kHeads == 4) {
+            c_step(i + 2, I2{});
+            c_step(i + 3, I3{});
+        }
     }
-    float *dst = segmented ? rs.seg_carry + (bh * rs.nseg + sg) * (P * N)
-                           : (dinit ? dinit + bh * (P * N) : nullptr);
-    if (dst) {
 #pragma unroll
-        for (int pb = 0; pb < 4; ++pb)
-            *(float4 *)(dst + (16 * pb + r16) * N + 16 * w + 4 * kq) =
-                make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
+    for (int rr = 0; rr < kHeads; ++rr) {
+        const int64_t bh = (int64_t)b * H + h0 + rr;
+        float *dst = segmented ? rs.seg_carry + (bh * rs.nseg + sg) * (P * N)
+                               : (dinit ? dinit + bh * (P * N) : nullptr);
+        if (dst) {
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb)
+                *(float4 *)(dst + goff + 16 * pb * N) =
+                    make_float4(gs[rr][pb][0], gs[rr][pb][1], gs[rr][pb][2], gs[rr][pb][3]);
+        }
     }
 }
 

@@ -162,17 +162,17 @@ __global__ __launch_bounds__(kThreads) void k_state_pass_bwd(float *ds, const fl
     float4 g = dfinal ? *(const float4 *)(dfinal + bh * PN + idx) : make_float4(0.f, 0.f, 0.f, 0.f);
     // step i handles chunk K - 1 - i; a ring of D steps in flight (step i in
     // slot i % D, loaded D steps before it is used).  The loads are
-    // unconditional (exact wait counts): a step past chunk 0 re-reads chunk 0,
-    // and its value is never used.  The caller keeps K * PN * 4 below 2^31.
-    const auto rd = buf_rsrc_n(d, K * PN * 4);
-    const auto rl = buf_rsrc_n(log_decay + bh * K, K * 4);
+    // unconditional (exact wait counts): a step past chunk 0 reads through an
+    // empty-range resource (zeros, no memory traffic), and its value is never
+    // used.  The caller keeps K * PN * 4 below 2^31.
+    const float *ld = log_decay + bh * K;
     float4 buf[D];
     float lv[D];
 #pragma unroll
     for (int i = 0; i < D; ++i) {
         const int k = max(K - 1 - i, 0);
-        buf[i] = buf_load4(rd, (k * PN + idx) * 4, 0);
-        lv[i] = buf_load(rl, k * 4, 0);
+        buf[i] = buf_load4(buf_rsrc_n(d, i < K ? K * PN * 4 : 0), (k * PN + idx) * 4, 0);
+        lv[i] = buf_load(buf_rsrc_n(ld, i < K ? K * 4 : 0), k * 4, 0);
     }
     int i0 = 0;
     for (; i0 + D <= K; i0 += D) {
@@ -186,8 +186,8 @@ __global__ __launch_bounds__(kThreads) void k_state_pass_bwd(float *ds, const fl
             g.z = buf[i].z + dec * g.z;
             g.w = buf[i].w + dec * g.w;
             const int kn = max(k - D, 0);
-            buf[i] = buf_load4(rd, (kn * PN + idx) * 4, 0);
-            lv[i] = buf_load(rl, kn * 4, 0);
+            buf[i] = buf_load4(buf_rsrc_n(d, k >= D ? K * PN * 4 : 0), (kn * PN + idx) * 4, 0);
+            lv[i] = buf_load(buf_rsrc_n(ld, k >= D ? K * 4 : 0), kn * 4, 0);
         }
     }
 #pragma unroll

@@ -23,10 +23,11 @@ void run_ws(dim3 grid, hipStream_t st, const BwdParams &bp, int nseg, int M) {
     hipLaunchKernelGGL((bwd::k_bwd_ws<kZ, kR, kSeq>), grid, dim3(kBwsThreads), 0, st, bp, nseg, M);
 }
 
-template <bool kSeq>
+template <bool kSeq, int kHeads>
 void run_rev(dim3 grid, hipStream_t st, const BwdParams &bp, const float *dfinal, float *dinit,
              const RevSeg &rs) {
-    hipLaunchKernelGGL((bwd::k_bwd_dstate_rev<kZ, kSeq>), grid, dim3(kWsThreads), 0, st, bp, dfinal, dinit, rs);
+    hipLaunchKernelGGL((bwd::k_bwd_dstate_rev<kZ, kSeq, kHeads>), grid, dim3(kWsThreads), 0, st, bp,
+                       dfinal, dinit, rs);
 }
 
 }  // namespace
@@ -41,10 +42,14 @@ void SSD_CAT(launch_bwd_ws_z, SSD_BWD_Z)(int rev_r, bool seq, dim3 grid, hipStre
     }
 }
 
-void SSD_CAT(launch_bwd_dstate_rev_z, SSD_BWD_Z)(bool seq, dim3 grid, hipStream_t st,
+void SSD_CAT(launch_bwd_dstate_rev_z, SSD_BWD_Z)(bool seq, int heads, dim3 grid, hipStream_t st,
                                                   const BwdParams &bp, const float *dfinal,
                                                   float *dinit, const RevSeg &rs) {
-    (seq ? run_rev<true> : run_rev<false>)(grid, st, bp, dfinal, dinit, rs);
+    switch (heads) {
+    case 4: (seq ? run_rev<true, 4> : run_rev<false, 4>)(grid, st, bp, dfinal, dinit, rs); break;
+    case 2: (seq ? run_rev<true, 2> : run_rev<false, 2>)(grid, st, bp, dfinal, dinit, rs); break;
+    default: (seq ? run_rev<true, 1> : run_rev<false, 1>)(grid, st, bp, dfinal, dinit, rs); break;
+    }
 }
 
 }  // namespace ssd

@@ -71,8 +71,11 @@ struct SegParams {
     float *seg_log_decay;  // [B, H, nseg]
     const float *seg_in;   // [B, H, seg_in_n, P, N] states at the segment-pass boundaries, or
                            // NULL; segment sg starts from entry sg * in_mult
+    const float *seg_in_log_decay; // [B, H, seg_in_n] non-NULL: seg_in holds the state-only
+                           // pass's contributions (from a zero state) and segment sg folds
+                           // entries 0 .. sg * in_mult - 1 onto the initial states itself
     int seg_in_n, in_mult;
-    int write_final;       // full pass writes final_state (single segment)
+    int write_final;       // the last segment writes final_state
     int nsplit;            // 64-column state halves per head: 1 (N = 64) or 2 (N = 128,
                            // state-only pass; the full pass of N = 128 is k_fwd_wide)
 };
@@ -92,6 +95,46 @@ __device__ __forceinline__ int xcd_unit(int id, int total, int R) {
 }
 
 constexpr int kWsThreads = 512; // 4 producer + 4 consumer waves
+
+// State entering segment sg when the segment recurrence is folded into the
+// full pass (sp.seg_in_log_decay non-NULL): with U_j the contribution of
+// pre-segment j (from a zero state) and ld_j its log decay,
+//   S = sum_{j < J} exp(ld_{j+1} + .. + ld_{J-1}) U_j + exp(ld_0 + .. + ld_{J-1}) init,
+// J = sg * in_mult, every term an independent load (no chain of dependent
+// steps).  `off(i)` is the element offset of this thread's float4 i within a
+// [P, N] state; U points at pre-segment 0 of the stream, init at the stream's
+// initial state or NULL.
+template <int kN, typename Off>
+__device__ __forceinline__ void fold_entry(f32x4 (&acc)[kN], const float *U, const float *ld, int J,
+                                          int64_t PNS, const float *init, Off off) {
+#pragma unroll
+    for (int i = 0; i < kN; ++i) acc[i] = zero4();
+    float lw = 0.f; // log weight of entry j: the decays after it
+#pragma unroll 2
+    for (int j = J - 1; j >= 0; --j) {
+        const float wj = __expf(lw);
+#pragma unroll
+        for (int i = 0; i < kN; ++i) {
+            const float4 v = *(const float4 *)(U + j * PNS + off(i));
+            acc[i][0] += wj * v.x;
+            acc[i][1] += wj * v.y;
+            acc[i][2] += wj * v.z;
+            acc[i][3] += wj * v.w;
+        }
+        lw += ld[j];
+    }
+    if (init) {
+        const float wi = __expf(lw);
+#pragma unroll
+        for (int i = 0; i < kN; ++i) {
+            const float4 v = *(const float4 *)(init + off(i));
+            acc[i][0] += wi * v.x;
+            acc[i][1] += wi * v.y;
+            acc[i][2] += wi * v.z;
+            acc[i][3] += wi * v.w;
+        }
+    }
+}
 
 // kSave: also write the state entering every chunk to prm.chunk_states; with
 // kStateOnly, a state pass that starts each segment from its entering state
@@ -339,19 +382,26 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
 
         {
             const float *s0 = nullptr;
-            if (!kStateOnly || kSave) {
-                if (sp.seg_in)
-                    s0 = sp.seg_in + (((int64_t)b * H + h) * sp.seg_in_n + sg * sp.in_mult) * PNS + n0;
-                else if (prm.init)
-                    s0 = prm.init + ((int64_t)b * H + h) * PNS + n0;
-            }
+            const int64_t bh = (int64_t)b * H + h;
+            if ((!kStateOnly || kSave) && sp.seg_in && sp.seg_in_log_decay) {
+                fold_entry(Sr, sp.seg_in + bh * sp.seg_in_n * PNS + n0, sp.seg_in_log_decay + bh * sp.seg_in_n,
+                           sg * sp.in_mult, PNS, prm.init ? prm.init + bh * PNS + n0 : nullptr,
+                           [&](int pb) { return (16 * pb + r16) * NS + 16 * W + 4 * kq; });
+            } else {
+                if (!kStateOnly || kSave) {
+                    if (sp.seg_in)
+                        s0 = sp.seg_in + (bh * sp.seg_in_n + sg * sp.in_mult) * PNS + n0;
+                    else if (prm.init)
+                        s0 = prm.init + bh * PNS + n0;
+                }
     #pragma unroll
-            for (int pb = 0; pb < 4; ++pb) {
-                if (s0) {
-                    const float4 v = *(const float4 *)(s0 + (16 * pb + r16) * NS + 16 * W + 4 * kq);
-                    Sr[pb] = f32x4{v.x, v.y, v.z, v.w};
-                } else {
-                    Sr[pb] = zero4();
+                for (int pb = 0; pb < 4; ++pb) {
+                    if (s0) {
+                        const float4 v = *(const float4 *)(s0 + (16 * pb + r16) * NS + 16 * W + 4 * kq);
+                        Sr[pb] = f32x4{v.x, v.y, v.z, v.w};
+                    } else {
+                        Sr[pb] = zero4();
+                    }
                 }
             }
             if (!kStateOnly) {
@@ -532,7 +582,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             // natural units; -inf (a factor of 0) where the state was cut
             if (tid == 0 && nh == 0)
                 sp.seg_log_decay[si] = seg_carry > 0.f ? log_decay_sum * kLn2 : -INFINITY;
-        } else if (sp.write_final && prm.final_state) {
+        } else if (sp.write_final && sg == sp.nseg - 1 && prm.final_state) {
             dst = prm.final_state + ((int64_t)b * H + h) * PNS + n0;
         }
         if (dst) {

@@ -251,21 +251,34 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
 
         {
             const float *s0 = nullptr;
-            if (sp.seg_in)
-                s0 = sp.seg_in + (((int64_t)b * H + h) * sp.seg_in_n + sg * sp.in_mult) * PNS;
-            else if (prm.init)
-                s0 = prm.init + ((int64_t)b * H + h) * PNS;
+            const int64_t bh = (int64_t)b * H + h;
+            if (sp.seg_in && sp.seg_in_log_decay) {
+                f32x4 acc[4];
+                fold_entry(acc, sp.seg_in + bh * sp.seg_in_n * PNS, sp.seg_in_log_decay + bh * sp.seg_in_n,
+                           sg * sp.in_mult, PNS, prm.init ? prm.init + bh * PNS : nullptr, [&](int i) {
+                               return (p0 + 16 * (i & 1) + r16) * NS + 16 * (W + 4 * (i >> 1)) + 4 * kq;
+                           });
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
+                for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int pb = 0; pb < 2; ++pb) {
-                    if (s0) {
-                        const float4 v = *(const float4 *)(s0 + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq);
-                        Sr[c][pb] = f32x4{v.x, v.y, v.z, v.w};
-                    } else {
-                        Sr[c][pb] = zero4();
+                    for (int pb = 0; pb < 2; ++pb) Sr[c][pb] = acc[2 * c + pb];
+            } else {
+                if (sp.seg_in)
+                    s0 = sp.seg_in + (bh * sp.seg_in_n + sg * sp.in_mult) * PNS;
+                else if (prm.init)
+                    s0 = prm.init + bh * PNS;
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int pb = 0; pb < 2; ++pb) {
+                        if (s0) {
+                            const float4 v = *(const float4 *)(s0 + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq);
+                            Sr[c][pb] = f32x4{v.x, v.y, v.z, v.w};
+                        } else {
+                            Sr[c][pb] = zero4();
+                        }
                     }
-                }
+            }
             write_T4(0);
             c_load(kbeg);
             z_load(kbeg);
@@ -416,7 +429,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         for (; k < kfull; ++k) iter(k, std::true_type{});
         if (k < kend) iter(k, std::false_type{});
 
-        if (sp.write_final && prm.final_state) {
+        if (sp.write_final && sg == sp.nseg - 1 && prm.final_state) {
             float *dst = prm.final_state + ((int64_t)b * H + h) * PNS;
 #pragma unroll
             for (int c = 0; c < 2; ++c)

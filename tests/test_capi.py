@@ -100,15 +100,20 @@ def test_workspace_size_formula():
     fwd = lib.mamba2_ssd_fwd_workspace_size
     assert ws(fwd, batch=8, seqlen=4096, nheads=256, ngroups=64) == 0
     # 64 streams, 32 chunks -> 4 segments of 8 chunks, whose entering states
-    # come from 8 pre-segments of 4: [B,H,8,P,N] + [B,H,8]
+    # each segment folds from the pre-segments of 4 chunks before it: the 6
+    # before the last segment, [B,H,6,P,N] + [B,H,6]
     got = ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4)
-    assert 4 * 16 * 8 * 64 * 64 * 4 + 4 * 16 * 8 * 4 <= got <= 4 * 16 * 8 * (64 * 64 + 1) * 4 + 2 * 256
+    assert 4 * 16 * 6 * 64 * 64 * 4 + 4 * 16 * 6 * 4 <= got <= 4 * 16 * 6 * (64 * 64 + 1) * 4 + 2 * 256
     # N = 128: 64 (b, h) x 2 workgroups = 128 streams -> 2 segments of 16
-    # chunks, 4 pre-segments; nothing else (each workgroup writes its
-    # channels of out itself)
+    # chunks, 2 pre-segments before the last; nothing else (each workgroup
+    # writes its channels of out itself)
     got = ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4, dstate=128)
-    seg = 4 * 16 * 4 * 64 * 128 * 4
-    assert seg <= got <= seg + 2 * 256 + 4 * 16 * 4 * 4
+    seg = 4 * 16 * 2 * 64 * 128 * 4
+    assert seg <= got <= seg + 2 * 256 + 4 * 16 * 2 * 4
+    # many segments (2 streams, 64 chunks -> 32 segments of 2): no fold, all
+    # 64 pre-segments of 1 chunk and the segment recurrence over them
+    got = ws(fwd, batch=1, seqlen=4096, nheads=2, ngroups=1)
+    assert 2 * 64 * 64 * 64 * 4 <= got <= 2 * 64 * (64 * 64 + 1) * 4 + 2 * 256
     # a short sequence is not cut (the cut would save fewer than 6 chunk steps)
     assert ws(fwd, batch=1, seqlen=128, nheads=2, ngroups=1, dstate=128) == 0
     assert ws(fwd, batch=1, seqlen=384, nheads=2, ngroups=1) == 0   # 6 chunks: saves 5
@@ -137,11 +142,11 @@ def test_workspace_size_formula():
     split = ws(bwd, batch=8, seqlen=4096, nheads=256, ngroups=32)
     assert split >= 2 * state_buf
     # 16 (b, g) streams of 32 chunks -> 16 runs of 2 chunks each: states
-    # [B,H,K,P,N] + the recompute's segment states [B,H,8,P,N] + run carries
-    # [B,H,16,P,N] + partials, no dstates
+    # [B,H,K,P,N] + the recompute's pre-segment states [B,H,6,P,N] + run
+    # carries [B,H,16,P,N] + partials, no dstates
     k = 2048 // 64
     states = 4 * 16 * k * 64 * 64 * 4
-    segs = 4 * 16 * 8 * 64 * 64 * 4
+    segs = 4 * 16 * 6 * 64 * 64 * 4
     carries = 4 * 16 * 16 * 64 * 64 * 4
     got = ws(bwd, batch=4, seqlen=2048, nheads=16, ngroups=4)
     assert states + segs + carries <= got < states + segs + carries + states // 8
