@@ -121,7 +121,7 @@ def fwd_segments(shape):
     mult = min(2, mt)
     mp = math.ceil(mt / mult)
     nseg = math.ceil(k / (mult * mp))
-    if (nseg - 1) * mult <= 8:
+    if (nseg - 1) * mult <= 12:
         # each full segment folds the pre-segments before it: the last full
         # segment's own pre-segments are not computed
         return nseg, (nseg - 1) * mult, nsplit
@@ -156,6 +156,11 @@ def fwd_kernel_model(name: str, shape) -> dict:
         per = f4 * (2 * p * n + 1)
         return {"bytes": su * per + b * h * p * n * f4, "flops": su * 2 * p * n, "units": su,
                 "bytes_per_unit": per}
+    elif name == "k_chunk_cb":
+        # C . B^T of every (b, g, chunk): B, C in, the 64 x 64 product out,
+        # once per group (1/R per head unit)
+        per = f4 * (2 * T * n + T * T) / r
+        fl = 2 * T * T * n / r
     elif name in ("k_fwd_seg", "k_fwd_wide"):
         # fused: x, dt, B, C in, y out; the state stays on chip (segment
         # entry/exit states are a few per stream and not counted).  dstate
@@ -199,6 +204,10 @@ def fwd_kernel_model(name: str, shape) -> dict:
         fl = 2 * (2 * T * T * n / r + 2 * T * T * p + 2 * T * T * n + 4 * T * n * p)
     else:
         per, fl = float("nan"), float("nan")
+    if name.startswith("k_fwd_wide") and n == 128 and r >= 8:
+        # C . B^T comes from k_chunk_cb (read once per group, not formed)
+        per += f4 * T * T / r
+        fl -= 2 * T * T * n / r
     return {"bytes": units * per, "flops": units * fl, "units": units, "bytes_per_unit": per}
 
 

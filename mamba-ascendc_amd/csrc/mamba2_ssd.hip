@@ -105,13 +105,21 @@ constexpr int64_t kMinSavedChunks = 6;
 // segment folds the pre-segment contributions onto the initial states in its
 // own prologue (independent loads, a few us) instead of a separate segment
 // recurrence launch (k_state_pass, about 6 us plus a launch gap at C4).
-constexpr int64_t kFoldMax = 8;
+constexpr int64_t kFoldMax = 12;
+// Heads per group from which the dstate-128 forward reads C . B^T from a
+// per-chunk precompute (k_chunk_cb) instead of forming it per workgroup: the
+// precompute (a launch, B and C read, the products written) pays off when 16
+// or more workgroups share each product (C5, 32 heads per group: 0.250 ->
+// 0.242 ms; C2, 4 heads per group: 0.072 -> 0.080 ms, so not there).
+constexpr int64_t kMinCbHeads = 8;
 
 struct FwdPlan {
     bool fused = false;
     int nseg = 1, M = 1, nsplit = 1;     // nsplit: workgroups per head (2 for dstate 128)
     int nseg_pre = 1, M_pre = 1, mult = 1; // segments of the state-only pass (nseg > 1)
     bool fold = false;                     // full segments fold the pre-segments themselves
+    bool cb = false;                     // dstate 128: C . B^T per (b, g, chunk) formed once
+    size_t cb_off = 0;                   // workspace offset of those products [B, G, K, 64, 64]
     size_t seg_state = 0, seg_decay = 0; // workspace offsets (fused, nseg > 1)
     size_t states = 0;                   // chunk states for VARLEN_STATES without SAVED_STATES
     size_t ws = 0;
@@ -140,7 +148,7 @@ Mamba2SsdShape fused_view(const Mamba2SsdShape *s) {
     return v;
 }
 
-FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags) {
+FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags, bool allow_cb = true) {
     FwdPlan pl;
     if (s->seqlen == 0) return pl;
     const int64_t K = nchunks(s), streams = s->batch * s->nheads;
@@ -180,14 +188,24 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags) {
             pl.states = off;
             off += align256((size_t)streams * K * pn * sizeof(float));
         }
+        // dstate 128 with kMinCbHeads or more heads per group: the 2 R
+        // workgroups of a group's chunk read one C . B^T (16 KB) instead of
+        // each forming it (about 45% of k_fwd_wide's matrix work)
+        if (allow_cb && pl.nsplit == 2 && s->nheads / s->ngroups >= kMinCbHeads) {
+            pl.cb = true;
+            pl.cb_off = off;
+            off += align256((size_t)s->batch * s->ngroups * K * 64 * 64 * sizeof(float));
+        }
         pl.ws = off;
     }
     return pl;
 }
 
-size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags) {
+// allow_cb = false: the least workspace the forward runs with (without the
+// C . B^T precompute, which is only a speed-up)
+size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags, bool allow_cb = true) {
     const Mamba2SsdShape v = fused_view(s);
-    return fwd_plan(&v, flags).ws;
+    return fwd_plan(&v, flags, allow_cb).ws;
 }
 
 // Optional per-kernel event trace: events[0] is recorded before the first
@@ -291,10 +309,13 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
             return fail(MAMBA2_SSD_ERR_UNSUPPORTED,
                         "VARLEN_STATES needs seqlen < 2^31 and chunk_size <= 2^30");
     }
-    const size_t need = fwd_ws_bytes(s, f);
-    if (need && (!workspace || workspace_bytes < need))
-        return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need,
-                    workspace ? workspace_bytes : (size_t)0);
+    // a workspace of the queried size runs the full plan; one that only holds
+    // the plan without the C . B^T precompute runs that plan
+    const size_t need = fwd_ws_bytes(s, f), need_min = fwd_ws_bytes(s, f, false);
+    const size_t have = workspace ? workspace_bytes : 0;
+    if (need_min && have < need_min)
+        return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need, have);
+    const bool allow_cb = have >= need;
     hipStream_t st = (hipStream_t)stream;
 
     ssd::FwdParams prm{};
@@ -351,7 +372,7 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
     // the fused kernels' view of the shape (heads of dim 64)
     const Mamba2SsdShape vs = fused_view(s);
     const int m = head_split(s);
-    const FwdPlan pl = fwd_plan(&vs, f);
+    const FwdPlan pl = fwd_plan(&vs, f, allow_cb);
     if (pl.fused && m > 1) {
         prm.H = (int)vs.nheads;
         prm.R = (int)(vs.nheads / vs.ngroups);
@@ -396,6 +417,12 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
             sp.write_final = 1;
         }
         kp.chunk_states = prm.chunk_states;
+        if (pl.cb) {
+            kp.cb = (const float *)((char *)workspace + pl.cb_off);
+            ssd::launch_chunk_cb((int)vs.dstate, dim3((unsigned)(vs.batch * vs.ngroups * prm.K)), st, prm.C,
+                                 prm.B, (float *)kp.cb, prm.L, prm.G, prm.K);
+            if (int rc = launch_status("k_chunk_cb", tr, st)) return rc;
+        }
         if (pl.nsplit > 1) {
             // dstate 128: two workgroups per head, 32 channels and all 128
             // state columns each, writing out directly
@@ -938,16 +965,19 @@ extern "C" {
 int mamba2_ssd_fwd_noalloc(const Mamba2SsdFwdArgs *a, void *stream) {
     if (!a) return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT, "args is NULL");
     if (int rc = check_shape(&a->shape, a->flags)) return rc;
-    const size_t need = fwd_ws_bytes(&a->shape, a->flags);
+    // the least workspace the forward runs with (fwd_impl leaves out the
+    // C . B^T precompute when the scratch cannot also hold it)
+    const size_t need = fwd_ws_bytes(&a->shape, a->flags, false);
     if (need > (size_t)MAMBA2_SSD_NOALLOC_SCRATCH_BYTES)
         return fail(MAMBA2_SSD_ERR_WORKSPACE,
                     "this forward needs %zu bytes of scratch; mamba2_ssd_fwd_noalloc has %zu "
                     "(use mamba2_ssd_fwd with a workspace)",
                     need, (size_t)MAMBA2_SSD_NOALLOC_SCRATCH_BYTES);
     void *ws = nullptr;
-    if (need)
+    const bool any = fwd_ws_bytes(&a->shape, a->flags) > 0;
+    if (any)
         if (int rc = scratch_for_current_device(&ws)) return rc;
-    return fwd_impl(a, ws, need ? (size_t)MAMBA2_SSD_NOALLOC_SCRATCH_BYTES : 0, stream, nullptr);
+    return fwd_impl(a, ws, any ? (size_t)MAMBA2_SSD_NOALLOC_SCRATCH_BYTES : 0, stream, nullptr);
 }
 
 int mamba2_ssd_bwd_m1_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, size_t *bytes) {

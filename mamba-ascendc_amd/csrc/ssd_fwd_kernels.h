@@ -38,6 +38,8 @@ struct FwdParams {
                             // indexed by h / hdiv, dt's token stride is H / hdiv
     int softplus, has_D, d_per_channel, has_z;
     float lo, hi;
+    const float *cb;        // [B, G, K, 64, 64] C_t . B_s of every chunk (k_chunk_cb), read by
+                            // k_fwd_wide<.., kCB = true>; NULL otherwise
 };
 
 // Chunk-local q and cs for (b, h, chunk k) by wave 0: s_q[t], s_cs[t].

@@ -62,9 +62,69 @@ __device__ __forceinline__ SplitTile T4(_Float16 *b, int s) {
 }
 }  // namespace wide
 
+// C_t . B_s of one 64-token chunk of one (b, g):
+// cb[((b G + g) K + k) 64 + t][s] = sum_n C[t][n] B[s][n] for the blocks
+// s <= t (16-token blocks; the others are never read), rows past the sequence
+// end zero.  Every workgroup of the group's heads (2 R of them in k_fwd_wide)
+// reads it instead of forming the product itself.  The operands are split
+// fp16 exactly as in k_fwd_wide's own product (same fragments, same MFMA
+// order), so both give the same bits.  One workgroup (4 waves) per (b, g, k);
+// wave W forms the blocks of tokens t in 16 W .. 16 W + 15.
+constexpr int kCbThreads = 256;
+template <int kN>
+__global__ __launch_bounds__(kCbThreads) void k_chunk_cb(const float *C, const float *B, float *cb, int64_t L,
+                                                         int G, int K) {
+    constexpr int T = 64, kS = kN + 8; // row stride (halves)
+    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * T * kS];
+    const SplitTile tb{lds, lds + T * kS}, tc{lds + 2 * T * kS, lds + 3 * T * kS};
+    const int64_t id = blockIdx.x; // (b G + g) K + k
+    const int k = (int)(id % K);
+    const int64_t bg = id / K;
+    const int g = (int)(bg % G);
+    const int64_t b = bg / G;
+    const int64_t t0 = (int64_t)k * T;
+    const int tv = (int)min((int64_t)T, L - t0);
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    // every load issued before the first is used: rows past the sequence end
+    // re-read its last row and are zeroed when staged
+    constexpr int kIt = T * kN / 4 / kCbThreads;
+    static_assert(kIt * kCbThreads * 4 == T * kN, "whole rows per pass");
+    float4 vb[kIt], vc[kIt];
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) {
+        const int e = threadIdx.x + i * kCbThreads, row = e / (kN / 4), c4 = (e % (kN / 4)) * 4;
+        const int64_t o = ((b * L + t0 + min(row, tv - 1)) * G + g) * kN + c4;
+        vb[i] = *(const float4 *)(B + o);
+        vc[i] = *(const float4 *)(C + o);
+    }
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) {
+        const int e = threadIdx.x + i * kCbThreads, row = e / (kN / 4), c4 = (e % (kN / 4)) * 4;
+        store_split4(tb, row * kS + c4, row < tv ? vb[i] : z4);
+        store_split4(tc, row * kS + c4, row < tv ? vc[i] : z4);
+    }
+    __syncthreads();
+    const int W = wave_id(), lane = threadIdx.x & 63, r16 = lane & 15, kq = lane >> 4;
+    const int own = 16 * W + r16;
+    Frag Co[kN / 32];
+#pragma unroll
+    for (int ks = 0; ks < kN / 32; ++ks) Co[ks] = frag_s<kS>(tc, own, ks);
+    float *dst = cb + id * (T * T);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j > W) break;
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < kN / 32; ++ks) acc = mma3f(frag_s<kS>(tb, 16 * j + r16, ks), Co[ks], acc);
+        *(float4 *)(dst + own * T + 16 * j + 4 * kq) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
+}
+
 // kSave: also write the state entering every chunk to prm.chunk_states (the
 // varlen states read them).  kGate: the z gate.  kSeq: packed sequences.
-template <bool kSave = false, bool kGate = false, bool kSeq = false>
+// kCB: C . B^T of each chunk comes from prm.cb (k_chunk_cb) instead of
+// being formed here (the 2 R workgroups of a group would each form it).
+template <bool kSave = false, bool kGate = false, bool kSeq = false, bool kCB = false>
 __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParams sp) {
     using namespace wide;
     constexpr int T = kT, P = 64, NS = kNC;
@@ -228,6 +288,18 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
 #pragma unroll
             for (int j = 0; j < 8; ++j) cr[j] = buf_load4(rc, vo + (32 * (j >> 1) + 4 * (j & 1)) * 4, 0);
         };
+        // kCB: this lane's C . B^T values of the next chunk, (t = own,
+        // s = 16 j + 4 (l / 16) + 0..3) for s-blocks j <= W
+        float4 cbr[4];
+        auto cb_load = [&](int k) {
+            if (!kCB) return;
+            const bool real = k < kend;
+            const auto rcb = buf_rsrc_n(prm.cb + (((int64_t)b * G + g) * prm.K + (real ? k : kbeg)) * (T * T),
+                                        real ? T * T * 4 : 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j <= W) cbr[j] = buf_load4(rcb, (own * T + 16 * j + 4 * kq) * 4, 0);
+        };
         float4 zr[2];
         auto z_load = [&](int k) {
             if (!kGate) return;
@@ -281,6 +353,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             }
             write_T4(0);
             c_load(kbeg);
+            cb_load(kbeg);
             z_load(kbeg);
             if (W == 0 && lane < kPC) {
                 const float dv = prm.has_D ? prm.D[prm.d_per_channel ? h * P + p0 + lane : hr] : 0.f;
@@ -311,7 +384,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
                 const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
                 Cown[ks] = pack_frag(vv);
             }
+            float4 cbv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cbv[j] = kCB ? cbr[j] : make_float4(0.f, 0.f, 0.f, 0.f);
             c_load(k + 1);
+            cb_load(k + 1);
             _Float16 *la = opaque_lds(lds);
             const SplitTile t1 = T1(la, s), t4 = T4(la, s);
             const float cs_own = s_cs[s][own];
@@ -323,10 +400,13 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     f32x4 cb = zero4();
-                    if (j <= W)
+                    if (kCB) {
+                        if (j <= W) cb = f32x4{cbv[j].x, cbv[j].y, cbv[j].z, cbv[j].w};
+                    } else if (j <= W) {
 #pragma unroll
                         for (int ks = 0; ks < 4; ++ks)
                             cb = mma3f(frag_s<kS1>(t1, 16 * j + r16, ks), Cown[ks], cb);
+                    }
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int so = 16 * j + 4 * kq + i;

@@ -16,9 +16,13 @@ struct SegParams;
 void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
                     const FwdParams &kp, const SegParams &sp);
 
-// k_fwd_wide<save, gate, seq> (dstate 128)
+// k_fwd_wide<save, gate, seq, kp.cb != NULL> (dstate 128)
 void launch_fwd_wide(bool save, bool gate, bool seq, dim3 grid, hipStream_t st, const FwdParams &kp,
                      const SegParams &sp);
+
+// k_chunk_cb<n>: C . B^T of every (b, g, chunk), grid B G K
+void launch_chunk_cb(int n, dim3 grid, hipStream_t st, const float *C, const float *B, float *cb, int64_t L,
+                     int G, int K);
 
 // the has_z halves of the two backward launchers, one per translation unit
 void launch_bwd_ws_z0(int rev_r, bool seq, dim3 grid, hipStream_t st, const BwdParams &bp, int nseg,

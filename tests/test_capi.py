@@ -105,21 +105,27 @@ def test_workspace_size_formula():
     got = ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4)
     assert 4 * 16 * 6 * 64 * 64 * 4 + 4 * 16 * 6 * 4 <= got <= 4 * 16 * 6 * (64 * 64 + 1) * 4 + 2 * 256
     # N = 128: 64 (b, h) x 2 workgroups = 128 streams -> 2 segments of 16
-    # chunks, 2 pre-segments before the last; nothing else (each workgroup
-    # writes its channels of out itself)
+    # chunks, 2 pre-segments before the last; nothing else with 4 heads per
+    # group (each workgroup writes its channels of out itself)
     got = ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4, dstate=128)
     seg = 4 * 16 * 2 * 64 * 128 * 4
     assert seg <= got <= seg + 2 * 256 + 4 * 16 * 2 * 4
+    # with 8 heads per group C . B^T of every (b, g, chunk) [B,G,K,64,64]
+    # (256 streams here: no segments)
+    assert ws(fwd, batch=4, seqlen=2048, nheads=32, ngroups=4, dstate=128) == 4 * 4 * 32 * 64 * 64 * 4
     # many segments (2 streams, 64 chunks -> 32 segments of 2): no fold, all
     # 64 pre-segments of 1 chunk and the segment recurrence over them
     got = ws(fwd, batch=1, seqlen=4096, nheads=2, ngroups=1)
     assert 2 * 64 * 64 * 64 * 4 <= got <= 2 * 64 * (64 * 64 + 1) * 4 + 2 * 256
-    # a short sequence is not cut (the cut would save fewer than 6 chunk steps)
+    # a short sequence is not cut (the cut would save fewer than 6 chunk
+    # steps); dstate 128 with 8 heads per group keeps C . B^T of its 2 chunks
     assert ws(fwd, batch=1, seqlen=128, nheads=2, ngroups=1, dstate=128) == 0
+    assert ws(fwd, batch=1, seqlen=128, nheads=8, ngroups=1, dstate=128) == 2 * 64 * 64 * 4
     assert ws(fwd, batch=1, seqlen=384, nheads=2, ngroups=1) == 0   # 6 chunks: saves 5
     assert ws(fwd, batch=1, seqlen=512, nheads=2, ngroups=1) > 0    # 8 chunks: saves 7
-    # one segment per stream: no workspace at all
-    assert ws(fwd, batch=8, seqlen=4096, nheads=64, ngroups=8, dstate=128) == 0
+    # one segment per stream: no segment buffers (dstate 128: C . B^T only)
+    assert ws(fwd, batch=8, seqlen=4096, nheads=64, ngroups=8, dstate=128) == 8 * 8 * 64 * 64 * 64 * 4
+    assert ws(fwd, batch=8, seqlen=4096, nheads=64, ngroups=8) == 0
     assert ws(fwd, seqlen=0) == 0
     # varlen states without saved states: the chunk states join the workspace
     one = _shape(batch=1, seqlen=4096, nheads=256, ngroups=64)

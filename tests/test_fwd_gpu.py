@@ -145,9 +145,10 @@ def _slice_groups(inp, g0, g1, r):
     return out
 
 
-def _fwd_capi_nan_filled(dev, shape):
+def _fwd_capi_nan_filled(dev, shape, ws_less=0):
     """Forward through the C ABI into output buffers filled with NaN, so that
-    an element the kernels never write stays NaN."""
+    an element the kernels never write stays NaN.  ws_less: pass a workspace
+    that many bytes smaller than the queried size."""
     import ctypes
 
     from ascend_kernel import _runtime as rt
@@ -160,7 +161,7 @@ def _fwd_capi_nan_filled(dev, shape):
     rt.check(lib.mamba2_ssd_fwd_workspace_size(ctypes.byref(shp), flags, ctypes.byref(nb)), "ws", lib)
     out = torch.full_like(dev["x"], math.nan)
     fin = torch.full((b, h, p, n), math.nan, device=dev["x"].device)
-    ws = torch.empty(max(1, nb.value), dtype=torch.uint8, device=dev["x"].device)
+    ws = torch.empty(max(1, nb.value - ws_less), dtype=torch.uint8, device=dev["x"].device)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     args = rt.Mamba2SsdFwdArgs(shp, flags, 0.0, math.inf, P(dev["x"]), P(dev["dt"]), P(dev["A"]),
                                P(dev["B"]), P(dev["C"]), None, None, None, None, P(out), P(fin))
@@ -230,3 +231,31 @@ def test_split_rounding_ties():
         fma, frl = parity_metrics(fin.cpu(), ref_fin)
         _say(f"  ties N={n}: out maxabs {ma:.3e} rel {rl:.3e} | final maxabs {fma:.3e} rel {frl:.3e}")
         assert rl <= 1e-6 and frl <= 1e-6, (n, ma, rl, fma, frl)
+
+
+def test_dstate128_forward_without_the_cb_precompute():
+    """dstate 128 with several heads per group reads C . B^T of every (b, g,
+    chunk) from a precompute in the workspace (k_chunk_cb); a workspace of the
+    queried size less that buffer runs the kernel that forms the product
+    itself.  Both form it from the same split-fp16 fragments in the same MFMA
+    order, so the outputs are the same bits, and both match the oracle; the
+    shape (8 heads per group) is cut into segments that fold their entering
+    states (the last from 4 pre-segments)."""
+    _need_gpu()
+    shape = [2, 700, 16, 64, 128, 64, 2]
+    b, l, h, p, n, chunk, g = shape
+    _say(f"dstate 128 with and without the C.B^T precompute {shape}")
+    inp = make_inputs(shape, seed=41)
+    dev = {k: v.cuda() for k, v in inp.items()}
+    cb_bytes = b * g * math.ceil(l / 64) * 64 * 64 * 4
+    full = _fwd_capi_nan_filled(dev, shape)
+    less = _fwd_capi_nan_filled(dev, shape, ws_less=cb_bytes)
+    ref, ref_fin = _run_ref(inp, chunk)
+    for name, (o, f) in (("precompute", full), ("in-kernel", less)):
+        assert bool(torch.isfinite(o).all()) and bool(torch.isfinite(f).all()), name
+        ma, rl = parity_metrics(o.cpu(), ref)
+        fma, frl = parity_metrics(f.cpu(), ref_fin)
+        _say(f"  {name}: out maxabs {ma:.3e} rel {rl:.3e} | final maxabs {fma:.3e} rel {frl:.3e}")
+        assert ma <= MAXABS and rl <= 1e-5
+        assert fma <= MAXABS and frl <= 1e-5
+    assert torch.equal(full[0], less[0]) and torch.equal(full[1], less[1])
