@@ -864,7 +864,7 @@ def model_key(short: str) -> str:
         if len(args) > 1 and args[1] != "0":
             return ("k_bwd_ws_rev_z" if args[0] == "true" else "k_bwd_ws_rev") + seq
         return "k_bwd_ws" + seq
-    return base if base == "k_bwd_dstate_rev" else short
+    return base if base in ("k_bwd_dstate_rev", "k_chunk_cb") else short
 
 
 SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs

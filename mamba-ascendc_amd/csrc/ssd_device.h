@@ -1,12 +1,15 @@
 // Device helpers shared by the Mamba-2 SSD kernels (gfx950 / CDNA4).
 //
-// Precision scheme: every contraction runs on the fp16 matrix cores with
-// fp32 accumulation, but each fp32 operand v is carried as an unevaluated sum
-// hi + lo of two fp16 values (hi = fp16(v), lo = fp16(v - hi), see split2),
-// and a product is formed from three MFMAs: hi*hi + hi*lo + lo*hi.  This keeps
-// about 21 bits of operand precision, which is what the fp32 contract needs (plain
-// fp16 or bf16 operands miss a 2e-2 max-abs bound by one to two orders of
-// magnitude on long sequences with slow decay).
+// Precision scheme of the forward kernels: every contraction runs on the
+// fp16 matrix cores with fp32 accumulation, but each fp32 operand v is carried
+// as an unevaluated sum hi + lo of two fp16 values (hi = fp16(v),
+// lo = fp16(v - hi), see split2), and a product is formed from three MFMAs:
+// hi*hi + hi*lo + lo*hi.  This keeps about 21 bits of operand precision, which
+// is what the fp32 contract needs: one fp16 product per contraction misses the
+// 2e-2 max-abs bound by 3-10x on the BASELINE shapes (outputs in the hundreds),
+// one bf16 product by 25-90x.  The backward kernels split into bf16 instead
+// (ssd_bf16.h): their operands scale with the upstream gradient, which a
+// mean-reduced loss makes smaller than fp16's normal range.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -15,12 +15,13 @@
 // columns.
 //
 // Long sequences with few (b, h) streams are cut into segments so the grid
-// still fills the GPU: a state-only pass (kStateOnly) computes each
-// segment's state contribution from zero and its total log decay, the
-// inter-segment recurrence (k_state_pass over segments) gives the state
-// entering every segment, and the full pass starts each segment from it.
-// With one segment per stream the full pass alone does everything and needs
-// no workspace.
+// still fills the GPU: a state-only pass (kStateOnly) computes the state
+// contribution from zero and the total log decay of each pre-segment (the
+// segments cut finer), and the full pass starts each segment from the state
+// entering it: either folded from those contributions in its own prologue
+// (fold_entry, sp.seg_in_log_decay) or, with many pre-segments, from the
+// recurrence k_state_pass ran over them.  With one segment per stream the
+// full pass alone does everything and needs no workspace.
 //
 // Exponentials are taken in the log2 domain: the chunk cumsum is formed over
 // A q log2(e), so every decay factor is a single exp2 of a difference.
@@ -34,7 +35,8 @@
 // ssd_chunk_state.py:208-231, ssd_state_passing.py:62-72,
 // ssd_chunk_scan.py:375-376).  The producers turn the ids into the three
 // per-token / per-chunk factors; a segment whose state is cut reports a log
-// decay of -inf, so the segment recurrence drops the state before it.
+// decay of -inf, so the fold (or the segment recurrence) drops the state
+// before it.
 //
 // Tiles (split fp16, LDS, all stored row-major in their first index), for
 // the chunk being processed:

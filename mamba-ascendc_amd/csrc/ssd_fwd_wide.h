@@ -28,9 +28,13 @@
 //
 // Long sequences with few streams are cut into segments exactly as for
 // k_fwd_seg: the state-only pass of k_fwd_seg (two 64-column halves) gives each
-// segment's contribution in the same [B, H, nseg, P, N] layout, the segment
-// recurrence (k_state_pass) the state entering each segment, and this kernel
-// starts each segment from it (sp.seg_in).
+// pre-segment's contribution in the same [B, H, nseg, P, N] layout, and this
+// kernel starts each segment from the state entering it, folded from those
+// contributions in its prologue (fold_entry) or read from the boundary states
+// of the segment recurrence (k_state_pass) when there are many.
+//
+// kCB: with many heads per group the 2 R workgroups of a group's chunk read
+// C . B^T from k_chunk_cb's per-chunk products instead of each forming it.
 //
 // The math is that of mamba_ascendc/csrc/ops/mamba2_ssd_fwd/design.md:10-20 and
 // the chunked decomposition of mamba_torch/ssd_reference.py:113-189; the

@@ -1,0 +1,95 @@
+"""Operand-rounding emulation of the fused forward's matrix products
+(test infrastructure, never shipped).
+
+The HIP forward forms four products per 64-token chunk on the matrix cores,
+each with fp32 accumulation: C . B^T, the decayed mask W (times q) against x,
+C . S (the entering state) and B^T . (decay q x) (the chunk's state update).
+This module recomputes the forward with the operands of exactly those four
+products rounded as a matrix-core scheme would see them, everything else
+(cumsums, exponentials, masks, the state recurrence) in float64, so the
+error of a rounding scheme can be measured on the CPU without building it:
+
+* ``fp16`` / ``bf16``         -- one product per contraction on rounded operands
+* ``split16`` / ``splitbf16`` -- each operand as hi + lo (hi = round(v),
+                                 lo = round(v - hi)) and three products
+                                 hi.hi + hi.lo + lo.hi (the kernels' scheme:
+                                 split fp16 in the forward)
+* ``fp32``                    -- no rounding (the chunked algorithm itself)
+
+The chunked algorithm is that of ``oracle.ssd_reference.ssd_chunked_core``
+(mamba_torch/ssd_reference.py:113-189) in the kernels' arrangement: q folded
+into W and into the state update's right operand instead of into x.  Only
+``tests/`` import this module.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+MODES = ("fp32", "fp16", "bf16", "split16", "splitbf16")
+
+
+def _round(t: torch.Tensor, kind: str) -> torch.Tensor:
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16}[kind]
+    return t.to(dt).to(t.dtype)
+
+
+def _product(eq: str, a: torch.Tensor, b: torch.Tensor, mode: str) -> torch.Tensor:
+    if mode == "fp32":
+        return torch.einsum(eq, a, b)
+    if mode in ("fp16", "bf16"):
+        return torch.einsum(eq, _round(a, mode), _round(b, mode))
+    base = "fp16" if mode == "split16" else "bf16"
+    ah, bh = _round(a, base), _round(b, base)
+    al, bl = _round(a - ah, base), _round(b - bh, base)
+    return torch.einsum(eq, ah, bh) + torch.einsum(eq, ah, bl) + torch.einsum(eq, al, bh)
+
+
+def ssd_forward_emulated(x, dt, A, B, C, mode: str, chunk: int = 64):
+    """y [b, l, h, p] and the final state [b, h, p, n] (float32) of the SSD
+    forward with softplus(dt), no D / z / initial state, the four matrix
+    products' operands rounded per ``mode`` and float64 everywhere else."""
+    if mode not in MODES:
+        raise ValueError(f"mode {mode!r} is not one of {MODES}")
+    b, l, h, p = x.shape
+    g, n = B.shape[2], B.shape[3]
+    r = h // g
+    T = chunk
+    x, B, C = x.double(), B.double(), C.double()
+    q = F.softplus(dt.double())
+    a = A.double()[None, None, :] * q
+    k = math.ceil(l / T)
+    pad = k * T - l
+    if pad:
+        x = F.pad(x, (0, 0, 0, 0, 0, pad))
+        q = F.pad(q, (0, 0, 0, pad))
+        a = F.pad(a, (0, 0, 0, pad))
+        B = F.pad(B, (0, 0, 0, 0, 0, pad))
+        C = F.pad(C, (0, 0, 0, 0, 0, pad))
+    xc = x.reshape(b, k, T, h, p)
+    qc = q.reshape(b, k, T, h)
+    cs = a.reshape(b, k, T, h).cumsum(2)
+    Bc = B.repeat_interleave(r, dim=2).reshape(b, k, T, h, n)
+    Cc = C.repeat_interleave(r, dim=2).reshape(b, k, T, h, n)
+    # (1) C_t . B_s and (2) W[t][s] = (C_t . B_s) exp(cs_t - cs_s) q_s (s <= t) against x
+    cb = _product("bkthn,bkshn->bkhts", Cc, Bc, mode)
+    csh = cs.permute(0, 1, 3, 2)  # [b, k, h, T]
+    lower = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    w = torch.where(lower, cb * torch.exp(csh[..., :, None] - csh[..., None, :]), torch.zeros((), dtype=cb.dtype))
+    w = w * qc.permute(0, 1, 3, 2)[..., None, :]
+    y_diag = _product("bkhts,bkshp->bkthp", w, xc, mode)
+    # (4) the chunk's state update B^T . (exp(cs_last - cs_t) q_t x_t)
+    to_end = torch.exp(cs[:, :, -1:, :] - cs) * qc
+    U = _product("bkthn,bkthp->bkhpn", Bc, xc * to_end[..., None], mode)
+    # (3) exp(cs_t) C_t . S with S the state entering the chunk
+    S = torch.zeros(b, h, p, n, dtype=torch.float64)
+    ys = []
+    for kk in range(k):
+        y_off = _product("bthn,bhpn->bthp", Cc[:, kk], S, mode) * torch.exp(cs[:, kk])[..., None]
+        ys.append(y_diag[:, kk] + y_off)
+        S = torch.exp(cs[:, kk, -1])[..., None, None] * S + U[:, kk]
+    y = torch.stack(ys, 1).reshape(b, k * T, h, p)[:, :l]
+    return y.float(), S.float()

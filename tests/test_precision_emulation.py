@@ -1,0 +1,78 @@
+"""Why the forward splits its matrix operands: the four products of a chunk
+recomputed on the CPU with their operands rounded as a matrix-core scheme
+would see them (oracle/precision_emulation.py), against the fp32 oracle, on
+independent (batch, group) units of the BASELINE configurations with their
+bench seeds.
+
+Measured (y max-abs; the contract is max-abs <= 2e-2, rel-L2 <= 5e-3):
+
+    unit               |y|max   split fp16   fp16      split bf16   bf16
+    C3 batch 0 group 0  114     3.8e-5       6.0e-2    1.1e-3       0.50
+    C4 batch 0 group 0  120     4.2e-5       7.0e-2    1.0e-3       0.65
+    C2 batch 0 group 0  527     2.1e-4       2.1e-1    3.4e-3       1.77
+    C5 heads 0..7       279     3.1e-4       1.4e-1    2.7e-3       1.13
+
+One product per contraction (fp16 or bf16) misses the max-abs contract at
+every configuration, though its rel-L2 (4.2e-4 fp16, 3.4e-3 bf16) would pass:
+the outputs reach the hundreds and the absolute bound does not scale with
+them.  Split fp16, the kernels' scheme, stays two to three orders of magnitude
+inside, which is what the GPU measures too.  The cases here are the C4 unit
+(one second of CPU) and the C3 unit (about twenty).
+"""
+
+import pytest
+import torch
+
+from oracle.precision_emulation import ssd_forward_emulated
+from oracle.ssd_reference import bench_seed, make_inputs, parity_metrics, ssd_chunk_scan_ref
+
+MAXABS = 2e-2
+
+
+def _unit(cfg_index, shape):
+    """Batch 0, group 0 of a BASELINE configuration (units share nothing)."""
+    inp = make_inputs(shape, seed=bench_seed(cfg_index))
+    r = shape[2] // shape[6]
+    return {"x": inp["x"][0:1, :, 0:r], "dt": inp["dt"][0:1, :, 0:r], "A": inp["A"][0:r],
+            "B": inp["B"][0:1, :, 0:1], "C": inp["C"][0:1, :, 0:1]}
+
+
+@pytest.mark.parametrize("cfg_index,shape", [
+    (3, [4, 2048, 16, 64, 64, 64, 4]),
+    (2, [8, 4096, 256, 64, 64, 64, 64]),
+], ids=["C4", "C3"])
+def test_single_products_miss_the_contract_split_fp16_does_not(cfg_index, shape):
+    u = _unit(cfg_index, shape)
+    ref, ref_fin = ssd_chunk_scan_ref(u["x"], u["dt"], u["A"], u["B"], u["C"], shape[5],
+                                      dt_softplus=True, return_final_state=True)
+    err = {}
+    for mode in ("fp32", "split16", "fp16", "splitbf16", "bf16"):
+        y, fin = ssd_forward_emulated(u["x"], u["dt"], u["A"], u["B"], u["C"], mode)
+        err[mode] = parity_metrics(y, ref) + parity_metrics(fin, ref_fin)
+    # the emulation itself is the oracle's algorithm (no rounding: fp32-level agreement)
+    assert err["fp32"][1] < 1e-6 and err["fp32"][3] < 1e-6
+    # the kernels' split fp16: far inside the contract
+    assert err["split16"][0] < 5e-4 and err["split16"][1] < 1e-6
+    # one fp16 or bf16 product per contraction: max-abs outside the contract
+    assert err["fp16"][0] > MAXABS and err["bf16"][0] > MAXABS
+    # relative error of one fp16 product: about fp16's half ulp (2^-12) on average
+    assert 1e-4 < err["fp16"][1] < 1e-3
+    # split bf16 (the backward's scheme) would also pass here, with less margin
+    assert err["splitbf16"][0] < MAXABS / 4
+
+
+def test_emulation_rounding_is_live():
+    """A planted check: with operands rounded to fp16 the emulated products
+    differ from the exact ones, and hi + lo recovers more than fp16 alone."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 128, 2, 64, generator=g)
+    dt = torch.rand(1, 128, 2, generator=g)
+    A = -torch.rand(2, generator=g)
+    B = torch.randn(1, 128, 1, 64, generator=g)
+    C = torch.randn(1, 128, 1, 64, generator=g)
+    exact, _ = ssd_forward_emulated(x, dt, A, B, C, "fp32")
+    single, _ = ssd_forward_emulated(x, dt, A, B, C, "fp16")
+    split, _ = ssd_forward_emulated(x, dt, A, B, C, "split16")
+    d_single = float((single - exact).abs().max())
+    d_split = float((split - exact).abs().max())
+    assert d_single > 0 and d_split < d_single / 100
