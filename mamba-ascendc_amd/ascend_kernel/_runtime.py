@@ -1,10 +1,13 @@
-"""Loader and ctypes binding of the HIP library ``libmamba2_ssd.so``.
+"""Loaders of the HIP library ``libmamba2_ssd.so`` (ctypes binding) and of
+the torch operator library ``libmamba2_ssd_torch.so``.
 
 Mirrors the role of the reference's runtime loader
 (mamba_ascendc/python/ascend_kernel/ascend_kernel/_runtime.py:35-65), which
-dlopens the operator library once at import.  Here the library is the C ABI of
-include/mamba2_ssd.h; the structures below are its ctypes mirror.  There is no
-fallback: if the library is missing or fails to load, every GPU call raises.
+dlopens the operator library once at import.  Here the HIP library is the C ABI
+of include/mamba2_ssd.h (the structures below are its ctypes mirror), and the
+operator library registers ``torch.ops.mamba_ascend.*`` in C++ over that ABI.
+There is no fallback: if either library is missing or fails to load, import
+raises.
 """
 
 from __future__ import annotations
@@ -16,6 +19,7 @@ import threading
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIBRARY_NAME = "libmamba2_ssd.so"
 LIBRARY_PATH = os.environ.get("MAMBA2_SSD_LIBRARY", os.path.join(_PKG_ROOT, LIBRARY_NAME))
+TORCH_OPS_PATH = os.path.join(_PKG_ROOT, "libmamba2_ssd_torch.so")
 
 ABI_VERSION = 4
 
@@ -188,6 +192,28 @@ def load_library(path: str | None = None):
         if path is None:
             _lib = lib
         return lib
+
+
+_torch_ops_loaded = False
+
+
+def load_torch_ops() -> None:
+    """Load (once) the torch operator library, which registers
+    ``torch.ops.mamba_ascend.*`` (no GPU work).  Raises RuntimeError when it is
+    missing."""
+    global _torch_ops_loaded
+    with _lock:
+        if _torch_ops_loaded:
+            return
+        if not os.path.exists(TORCH_OPS_PATH):
+            raise RuntimeError(
+                f"torch operator library {TORCH_OPS_PATH} not found; build it with "
+                "`python -c \"import __graft_entry__ as g; g.build()\"`"
+            )
+        import torch
+
+        torch.ops.load_library(TORCH_OPS_PATH)
+        _torch_ops_loaded = True
 
 
 def last_error(lib=None) -> str:

@@ -10,13 +10,15 @@ Public surface mirrors mamba_ascendc/python/ascend_kernel/ascend_kernel/mamba2.p
   training spec, mamba2.py:1978-1982).
 * ``torch.ops.mamba_ascend.mamba2_ssd_fwd`` / ``mamba2_ssd_bwd_m1`` /
   ``mamba2_ssd_state_passing``: op schemas of mamba_ascendc/csrc/register.cpp
-  (forward 175-179, state passing 89-90), registered here on the CUDA key
-  (ROCm tensors are ``device.type == "cuda"``) plus a Meta implementation.
+  (forward 175-179, state passing 89-90), registered in C++ by the operator
+  library (csrc/torch_ops.cpp) on the CUDA key (ROCm tensors are
+  ``device.type == "cuda"``), CPU (rejected) and Meta.
 
-Every op calls the HIP library through its C ABI (include/mamba2_ssd.h):
-outputs and workspace come from torch's caching allocator, work is enqueued on
-the current stream, and a nonzero status becomes RuntimeError.  There is no CPU
-path: CPU tensors are rejected.
+The public calls go through those C++ operators, which validate, allocate
+outputs and workspace from torch's caching allocator and enqueue the HIP
+library's kernels on the current stream; packed-sequence calls (seq_idx,
+cu_seqlens) use the ctypes binding of the same C ABI below.  A nonzero status
+becomes RuntimeError.  There is no CPU path: CPU tensors are rejected.
 """
 
 from __future__ import annotations
@@ -32,9 +34,6 @@ import torch
 
 from . import _runtime as rt
 
-_NS = "mamba_ascend"
-_OPS_DEFINED = False
-_lib_frag = None
 
 
 # ----------------------------------------------------------------------------- validation
@@ -263,135 +262,14 @@ def _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states, 
 
 # ----------------------------------------------------------------------------- torch ops
 
-_FWD_SCHEMA = (
-    "mamba2_ssd_fwd(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D=None, "
-    "Tensor? z=None, Tensor? dt_bias=None, Tensor? initial_states=None, int chunk_size=256, "
-    "bool dt_softplus=False, float dt_limit_min=0.0, float dt_limit_max=3.402823466e+38) "
-    "-> (Tensor, Tensor)"
-)
-_BWD_SCHEMA = (
-    "mamba2_ssd_bwd_m1(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor dout, "
-    "Tensor? dfinal_state=None, Tensor? D=None, Tensor? z=None, Tensor? dt_bias=None, "
-    "Tensor? initial_states=None, Tensor? pre_gate=None, Tensor? chunk_states=None, "
-    "int chunk_size=64, "
-    "bool dt_softplus=False, float dt_limit_min=0.0, float dt_limit_max=3.402823466e+38, "
-    "Tensor? seq_idx=None) "
-    "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
-    "Tensor, Tensor)"
-)
-_SP_SCHEMA = (
-    "mamba2_ssd_state_passing(Tensor chunk_states, Tensor dA_cumsum, "
-    "Tensor? initial_states=None) -> (Tensor, Tensor)"
-)
-
-
-def _op_fwd_cuda(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, chunk_size=256,
-                 dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.402823466e+38):
-    _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
-                  dt_limit_min, dt_limit_max)
-    out, final, _, _, _ = _fwd_raw(x, dt, A, B, C, D, z, dt_bias, initial_states, chunk_size,
-                                   dt_softplus, dt_limit_min, dt_limit_max)
-    return out, final
-
-
-def _op_fwd_meta(x, dt, A, B, C, D=None, z=None, dt_bias=None, initial_states=None, chunk_size=256,
-                 dt_softplus=False, dt_limit_min=0.0, dt_limit_max=3.402823466e+38):
-    b, _, h, p = x.shape
-    return torch.empty_like(x), x.new_empty(b, h, p, B.shape[3], dtype=torch.float32)
-
-
-def _empty_like_or_none(t, ref):
-    return ref.new_empty(0) if t is None else t
-
-
-def _op_bwd_cuda(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bias=None,
-                 initial_states=None,
-                 pre_gate=None, chunk_states=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
-                 dt_limit_max=3.402823466e+38, seq_idx=None):
-    op = "mamba2_ssd_bwd_m1"
-    _validate_fwd(op, x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states,
-                  dt_limit_min, dt_limit_max)
-    _check_tensor(op, "dout", dout)
-    if dout.shape != x.shape:
-        raise RuntimeError(f"{op}: dout shape must match x")
-    if dfinal_state is not None:
-        _check_tensor(op, "dfinal_state", dfinal_state)
-        if tuple(dfinal_state.shape) != (x.shape[0], x.shape[2], x.shape[3], B.shape[3]):
-            raise RuntimeError(f"{op}: dfinal_state must have shape [B,H,P,N]")
-    if z is not None:
-        if pre_gate is None:
-            raise RuntimeError(f"{op}: z needs the forward's pre_gate (y + D x before the gate)")
-        _check_tensor(op, "pre_gate", pre_gate)
-        if pre_gate.shape != x.shape:
-            raise RuntimeError(f"{op}: pre_gate shape must match x")
-    if chunk_states is not None:
-        _check_tensor(op, "chunk_states", chunk_states)
-        want = (x.shape[0], x.shape[2], _nchunks(x), x.shape[3], B.shape[3])
-        if tuple(chunk_states.shape) != want:
-            raise RuntimeError(f"{op}: chunk_states must have shape [B,H,ceil(L/64),P,N] = {list(want)}")
-    if seq_idx is not None:
-        seq_idx = _check_seq_idx(x, seq_idx, chunk_size, B)
-    grads = _bwd_raw(x, dt, A, B, C, dout, dfinal_state, D, z, dt_bias, initial_states,
-                     chunk_size, dt_softplus, dt_limit_min, dt_limit_max,
-                     pre_gate if z is not None else None, chunk_states, seq_idx)
-    return tuple(_empty_like_or_none(g, x) for g in grads)
-
-
-def _op_bwd_meta(x, dt, A, B, C, dout, dfinal_state=None, D=None, z=None, dt_bias=None,
-                 initial_states=None,
-                 pre_gate=None, chunk_states=None, chunk_size=64, dt_softplus=False, dt_limit_min=0.0,
-                 dt_limit_max=3.402823466e+38, seq_idx=None):
-    like = lambda t: x.new_empty(0) if t is None else torch.empty_like(t)  # noqa: E731
-    return (torch.empty_like(x), torch.empty_like(dt), torch.empty_like(A), torch.empty_like(B),
-            torch.empty_like(C), like(D), like(z), like(dt_bias), like(initial_states))
-
-
-def _op_sp_cuda(chunk_states, dA_cumsum, initial_states=None):
-    op = "mamba2_ssd_state_passing"
-    _check_tensor(op, "chunk_states", chunk_states)
-    _check_tensor(op, "dA_cumsum", dA_cumsum)
-    if chunk_states.dim() != 5:
-        raise RuntimeError(f"{op}: chunk_states must have shape [B,H,K,P,N]")
-    b, h, k, p, n = chunk_states.shape
-    if dA_cumsum.dim() != 4 or tuple(dA_cumsum.shape[:3]) != (b, h, k):
-        raise RuntimeError(f"{op}: dA_cumsum must have shape [B,H,K,T]")
-    if initial_states is not None:
-        _check_tensor(op, "initial_states", initial_states)
-        if tuple(initial_states.shape) != (b, h, p, n):
-            raise RuntimeError(f"{op}: initial_states must have shape [B,H,P,N]")
-    log_decay = dA_cumsum[..., -1].contiguous()
-    states = torch.empty_like(chunk_states)
-    final = chunk_states.new_empty(b, h, p, n)
-    lib = rt.load_library()
-    with torch.cuda.device(chunk_states.device):
-        rt.check(lib.mamba2_ssd_state_passing(
-            _ptr(chunk_states), _ptr(log_decay), _ptr(initial_states), _ptr(states), _ptr(final),
-            b, h, k, p, n, _stream(chunk_states.device)), op, lib)
-    return states, final
-
-
-def _op_sp_meta(chunk_states, dA_cumsum, initial_states=None):
-    b, h, k, p, n = chunk_states.shape
-    return torch.empty_like(chunk_states), chunk_states.new_empty(b, h, p, n)
-
-
 def register_ops() -> None:
-    """Define ``torch.ops.mamba_ascend.*`` once (CUDA + Meta implementations)."""
-    global _OPS_DEFINED, _lib_frag
-    if _OPS_DEFINED:
-        return
-    frag = torch.library.Library(_NS, "FRAGMENT")
-    for schema, cuda_fn, meta_fn in (
-        (_FWD_SCHEMA, _op_fwd_cuda, _op_fwd_meta),
-        (_BWD_SCHEMA, _op_bwd_cuda, _op_bwd_meta),
-        (_SP_SCHEMA, _op_sp_cuda, _op_sp_meta),
-    ):
-        name = schema.split("(", 1)[0]
-        frag.define(schema)
-        frag.impl(name, cuda_fn, "CUDA")
-        frag.impl(name, meta_fn, "Meta")
-    _lib_frag = frag
-    _OPS_DEFINED = True
+    """Make ``torch.ops.mamba_ascend.*`` available: load (once) the C++
+    operator library, which registers the reference's ``mamba2_ssd_fwd`` and
+    ``mamba2_ssd_state_passing`` schemas (mamba_ascendc/csrc/register.cpp:
+    175-179, 89-90), this build's ``mamba2_ssd_bwd_m1`` and the internal
+    ``mamba2_ssd_fwd_ex`` (the forward with the training outputs) on the CUDA,
+    CPU (rejected by the device check) and Meta keys."""
+    rt.load_torch_ops()
 
 
 # ----------------------------------------------------------------------------- training policy
@@ -480,18 +358,28 @@ class _Mamba2SsdAutogradM1(torch.autograd.Function):
     def forward(ctx, x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus,
                 dt_limit_min, dt_limit_max, initial_states, seq_idx=None, cu_seqlens=None,
                 save_states=True):
-        _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
-                      initial_states, dt_limit_min, dt_limit_max)
+        if seq_idx is not None or cu_seqlens is not None:
+            _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
+                          initial_states, dt_limit_min, dt_limit_max)
+        # (without them the C++ operator validates)
         # the pre-gate output y + D x is saved when z is present (dz needs it),
         # as the reference's Train forward does (mamba2.py:1682-1770), and the
         # chunk-start states when the policy keeps them (the reference's
         # training forward returns states_start for its backward,
         # mamba2.py:228,322,408-418); varlen states are read from them
-        out, final_state, pre_gate, states, varlen = _fwd_raw(
-            x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
-            float(dt_limit_min), float(dt_limit_max), want_final=True,
-            want_pre_gate=z is not None, want_states=bool(save_states), seq_idx=seq_idx,
-            cu_seqlens=cu_seqlens)
+        if seq_idx is None and cu_seqlens is None:
+            out, final_state, pre_gate, states = torch.ops.mamba_ascend.mamba2_ssd_fwd_ex(
+                x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
+                float(dt_limit_min), float(dt_limit_max), True, z is not None, bool(save_states))
+            pre_gate = pre_gate if z is not None else None
+            states = states if save_states else None
+            varlen = None
+        else:
+            out, final_state, pre_gate, states, varlen = _fwd_raw(
+                x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus),
+                float(dt_limit_min), float(dt_limit_max), want_final=True,
+                want_pre_gate=z is not None, want_states=bool(save_states), seq_idx=seq_idx,
+                cu_seqlens=cu_seqlens)
         empty = x.new_empty(0)
         ctx.save_for_backward(
             x, dt, A, B, C,
@@ -600,6 +488,11 @@ def mamba2_ssd_fwd(
             seq32, cu32, save)
         if cu32 is not None:
             return (out, final_state, varlen) if return_final_state else (out, varlen)
+    elif seq32 is None and cu32 is None:
+        # the C++ operator validates, allocates and launches (a few us of host work)
+        out, final_state, _, _ = torch.ops.mamba_ascend.mamba2_ssd_fwd_ex(
+            x, dt, A, B, C, D, z, dt_bias, initial_states, int(chunk_size), bool(dt_softplus), lo, hi,
+            bool(return_final_state), False, False)
     else:
         _validate_fwd("mamba2_ssd_fwd", x, dt, A, B, C, chunk_size, D, z, dt_bias,
                       initial_states, lo, hi)

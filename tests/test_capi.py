@@ -338,6 +338,36 @@ def test_public_api_packed_sequence_errors():
                            seq_idx=torch.zeros(b, l, dtype=torch.int32))
 
 
+def test_operator_library_schemas():
+    """torch.ops.mamba_ascend.* come from the C++ operator library with the
+    reference's schemas for the forward and the state-passing op
+    (mamba_ascendc/csrc/register.cpp:175-179, 89-90), this build's backward,
+    and the internal forward with the training outputs."""
+    api.register_ops()
+    want = {
+        "mamba2_ssd_fwd": "mamba2_ssd_fwd(Tensor x, Tensor dt, Tensor A, Tensor B, Tensor C, Tensor? D=None, "
+                          "Tensor? z=None, Tensor? dt_bias=None, Tensor? initial_states=None, int chunk_size=256, "
+                          "bool dt_softplus=False, float dt_limit_min=0.0, float dt_limit_max=3.402823466e+38) "
+                          "-> (Tensor, Tensor)",
+        "mamba2_ssd_state_passing": "mamba2_ssd_state_passing(Tensor chunk_states, Tensor dA_cumsum, "
+                                    "Tensor? initial_states=None) -> (Tensor, Tensor)",
+    }
+    for name, schema in want.items():
+        got = getattr(torch.ops.mamba_ascend, name).default._schema
+        assert got == torch._C.parse_schema("mamba_ascend::" + schema), str(got)
+    bwd = str(torch.ops.mamba_ascend.mamba2_ssd_bwd_m1.default._schema)
+    assert bwd.endswith("Tensor? seq_idx=None) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
+                        "Tensor, Tensor)")
+    ex = str(torch.ops.mamba_ascend.mamba2_ssd_fwd_ex.default._schema)
+    assert "bool want_final, bool want_pre_gate, bool want_states" in ex
+    # the operators' device check runs first for CPU tensors
+    x, dt, A, B, C = _cpu_inputs()
+    with pytest.raises(RuntimeError, match="x must be a ROCm GPU tensor"):
+        torch.ops.mamba_ascend.mamba2_ssd_fwd(x, dt, A, B, C)
+    with pytest.raises(RuntimeError, match="chunk_states must be a ROCm GPU tensor"):
+        torch.ops.mamba_ascend.mamba2_ssd_state_passing(torch.zeros(1, 1, 2, 4, 4), torch.zeros(1, 1, 2, 8))
+
+
 def test_meta_shape_inference():
     api.register_ops()
     x = torch.empty(2, 100, 8, 64, device="meta")

@@ -259,3 +259,45 @@ def test_dstate128_forward_without_the_cb_precompute():
         assert ma <= MAXABS and rl <= 1e-5
         assert fma <= MAXABS and frl <= 1e-5
     assert torch.equal(full[0], less[0]) and torch.equal(full[1], less[1])
+
+
+@pytest.mark.parametrize("mutate,match", [
+    (lambda t: {**t, "dt": t["dt"][..., :1].contiguous()}, "dt shape must equal"),
+    (lambda t: {**t, "A": t["A"][:1].contiguous()}, "A shape must equal"),
+    (lambda t: {**t, "C": t["C"][:, :, :, :32].contiguous()}, "B and C shapes must match"),
+    (lambda t: {**t, "x": t["x"].transpose(1, 2)}, "x must be contiguous"),
+    (lambda t: {**t, "x": t["x"].double()}, "x must be float32"),
+    (lambda t: {**t, "D": torch.zeros(3, device="cuda")}, r"D must have shape \[H\] or \[H,P\]"),
+    (lambda t: {**t, "dt": t["dt"].cpu()}, "dt must be a ROCm GPU tensor"),
+], ids=["dt", "A", "BC", "layout", "dtype", "D", "device"])
+def test_operator_validation_messages(mutate, match):
+    """The C++ operators check GPU tensors with the Python layer's messages
+    (the reference host wrapper's checks), before any GPU work."""
+    _need_gpu()
+    inp = {k: v.cuda() for k, v in make_inputs([1, 64, 2, 64, 64, 64, 1], seed=3).items()}
+    t = mutate(dict(inp, D=None))
+    with pytest.raises(RuntimeError, match=match):
+        torch.ops.mamba_ascend.mamba2_ssd_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], None, None,
+                                              None, 64, True)
+    with pytest.raises(RuntimeError, match=match):
+        torch.ops.mamba_ascend.mamba2_ssd_bwd_m1(t["x"], t["dt"], t["A"], t["B"], t["C"], inp["x"], None,
+                                                 t["D"], None, None, None, None, None, 64, True)
+
+
+def test_public_forward_runs_through_the_operator_library():
+    """The public no-grad forward calls torch.ops.mamba_ascend.mamba2_ssd_fwd_ex
+    (C++), and its result equals the ctypes path's bit for bit."""
+    _need_gpu()
+    import ascend_kernel
+    from ascend_kernel import mamba2 as api
+
+    inp = make_inputs([2, 200, 4, 64, 64, 64, 2], seed=9, features=("D", "z", "bias", "init"))
+    dev = {k: v.cuda() for k, v in inp.items()}
+    out, fin = ascend_kernel.mamba2_ssd_fwd(
+        dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"], 64, D=dev["D"], z=dev["z"],
+        dt_bias=dev["dt_bias"], dt_softplus=True, initial_states=dev["initial_states"], return_final_state=True)
+    ref = api._fwd_raw(dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"], dev["D"], dev["z"], dev["dt_bias"],
+                       dev["initial_states"], 64, True, 0.0, math.inf)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref[0]) and torch.equal(fin, ref[1])
+    assert torch.ops.mamba_ascend.mamba2_ssd_fwd_ex.default._schema.name == "mamba_ascend::mamba2_ssd_fwd_ex"

@@ -16,8 +16,9 @@ One product per contraction (fp16 or bf16) misses the max-abs contract at
 every configuration, though its rel-L2 (4.2e-4 fp16, 3.4e-3 bf16) would pass:
 the outputs reach the hundreds and the absolute bound does not scale with
 them.  Split fp16, the kernels' scheme, stays two to three orders of magnitude
-inside, which is what the GPU measures too.  The cases here are the C4 unit
-(one second of CPU) and the C3 unit (about twenty).
+inside, which is what the GPU measures too.  The test runs the C4 unit (a
+second of CPU); the other rows come from the same function on the units named
+(drawing the C3 inputs alone takes about a minute).
 """
 
 import pytest
@@ -39,8 +40,7 @@ def _unit(cfg_index, shape):
 
 @pytest.mark.parametrize("cfg_index,shape", [
     (3, [4, 2048, 16, 64, 64, 64, 4]),
-    (2, [8, 4096, 256, 64, 64, 64, 64]),
-], ids=["C4", "C3"])
+], ids=["C4"])
 def test_single_products_miss_the_contract_split_fp16_does_not(cfg_index, shape):
     u = _unit(cfg_index, shape)
     ref, ref_fin = ssd_chunk_scan_ref(u["x"], u["dt"], u["A"], u["B"], u["C"], shape[5],
