@@ -6,6 +6,7 @@
 // allocates device memory.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -203,7 +204,66 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags, bool allow_cb = true) 
 
 // allow_cb = false: the least workspace the forward runs with (without the
 // C . B^T precompute, which is only a speed-up)
-size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags, bool allow_cb = true) {
+// Shapes the fused kernels take after zero padding: a headdim that is not a
+// multiple of 64 (padded up to one, the heads then split as usual) and/or a
+// dstate below 64 or between 64 and 128 (padded to 64 or 128), for the plain
+// forward (no saved chunk states, varlen states or packed sequences, whose
+// layouts would change).  The padded channels of x and z and the padded state
+// columns of B, C and the initial states are zero, so every padded product
+// term is an exact zero: the padded problem's output restricted to the real
+// channels, and its final state to the real rows and columns, are the
+// forward's (the extra channels come out zero and are dropped).  The
+// reference runs such shapes (multiples of 16 with P N <= 8192) on its BMM
+// route (mamba2.py:30-44, 429-557); here they reach the MFMA kernels instead
+// of the per-row token recurrence.
+struct PadPlan {
+    bool on = false;
+    Mamba2SsdShape ps{};               // the padded shape
+    bool pad_p = false, pad_n = false; // which dimensions change
+    // workspace offsets: x, z (P padded), B, C (N padded), per-channel D,
+    // initial states, out and pre_gate (P padded), final state, inner workspace
+    size_t x = 0, z = 0, b = 0, c = 0, d = 0, init = 0, out = 0, pre = 0, fin = 0, inner = 0, total = 0;
+};
+
+size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags, bool allow_cb = true);
+
+PadPlan pad_plan(const Mamba2SsdShape *s, uint32_t f, bool allow_cb) {
+    PadPlan pp;
+    const uint32_t layout_flags = MAMBA2_SSD_SAVED_STATES | MAMBA2_SSD_VARLEN_STATES | MAMBA2_SSD_HAS_SEQ_IDX;
+    if (s->seqlen == 0 || fused_shape(s) || head_split(s) > 1 || s->dstate > 128 || (f & layout_flags))
+        return pp;
+    pp.on = true;
+    pp.ps = *s;
+    pp.ps.headdim = (s->headdim + 63) / 64 * 64;
+    pp.ps.dstate = s->dstate <= 64 ? 64 : 128;
+    pp.pad_p = pp.ps.headdim != s->headdim;
+    pp.pad_n = pp.ps.dstate != s->dstate;
+    const size_t blh = (size_t)s->batch * s->seqlen * s->nheads, blg = (size_t)s->batch * s->seqlen * s->ngroups;
+    const size_t bh = (size_t)s->batch * s->nheads, P = pp.ps.headdim, N = pp.ps.dstate;
+    size_t off = 0;
+    auto take = [&](size_t &at, size_t floats) {
+        at = off;
+        off += align256(floats * sizeof(float));
+    };
+    if (pp.pad_p) take(pp.x, blh * P);
+    if (pp.pad_p && (f & MAMBA2_SSD_HAS_Z)) take(pp.z, blh * P);
+    if (pp.pad_n) {
+        take(pp.b, blg * N);
+        take(pp.c, blg * N);
+    }
+    if (pp.pad_p && (f & MAMBA2_SSD_D_PER_CHANNEL)) take(pp.d, (size_t)s->nheads * P);
+    if (f & MAMBA2_SSD_HAS_INITIAL) take(pp.init, bh * P * N);
+    if (pp.pad_p) take(pp.out, blh * P);
+    if (pp.pad_p && (f & MAMBA2_SSD_HAS_Z)) take(pp.pre, blh * P);
+    take(pp.fin, bh * P * N);
+    pp.inner = off;
+    pp.total = off + fwd_ws_bytes(&pp.ps, f, allow_cb);
+    return pp;
+}
+
+size_t fwd_ws_bytes(const Mamba2SsdShape *s, uint32_t flags, bool allow_cb) {
+    const PadPlan pp = pad_plan(s, flags, allow_cb);
+    if (pp.on) return pp.total;
     const Mamba2SsdShape v = fused_view(s);
     return fwd_plan(&v, flags, allow_cb).ws;
 }
@@ -255,6 +315,67 @@ int mamba2_ssd_fwd_workspace_size(const Mamba2SsdShape *shape, uint32_t flags, s
 }  // extern "C"
 
 namespace {
+
+int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes, void *stream, Trace *tr);
+
+// [outer, rs, cs] -> [outer, rd, cd] with zero fill (or the padding cut off)
+int pad_copy(const float *src, int64_t outer, int64_t rs, int64_t cs, float *dst, int64_t rd, int64_t cd,
+             hipStream_t st, Trace *tr) {
+    const int64_t total = outer * rd * cd;
+    const int64_t blocks = std::min<int64_t>((total + ssd::kPadThreads - 1) / ssd::kPadThreads, 8192);
+    hipLaunchKernelGGL(ssd::k_pad_copy, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(ssd::kPadThreads), 0, st,
+                       src, outer, (int)rs, (int)cs, dst, (int)rd, (int)cd);
+    return launch_status("k_pad_copy", tr, st);
+}
+
+// The forward on a zero-padded copy of the problem (PadPlan), then the real
+// channels of out / pre_gate and the real rows and columns of the final state
+// copied back.
+int fwd_padded(const Mamba2SsdFwdArgs *a, const PadPlan &pp, char *ws, size_t have, hipStream_t st, Trace *tr) {
+    const Mamba2SsdShape *s = &a->shape;
+    const uint32_t f = a->flags;
+    const int64_t P = s->headdim, N = s->dstate, Pp = pp.ps.headdim, Np = pp.ps.dstate;
+    const int64_t blh = s->batch * s->seqlen * s->nheads, blg = s->batch * s->seqlen * s->ngroups;
+    const int64_t bh = s->batch * s->nheads;
+    Mamba2SsdFwdArgs pa = *a;
+    pa.shape = pp.ps;
+    auto at = [&](size_t off) { return (float *)(ws + off); };
+    // inputs: padded copies of what changes shape (traced with the inner kernels' events)
+    if (pp.pad_p) {
+        if (int rc = pad_copy(a->x, blh, 1, P, at(pp.x), 1, Pp, st, nullptr)) return rc;
+        pa.x = at(pp.x);
+        if (f & MAMBA2_SSD_HAS_Z) {
+            if (int rc = pad_copy(a->z, blh, 1, P, at(pp.z), 1, Pp, st, nullptr)) return rc;
+            pa.z = at(pp.z);
+        }
+        if (f & MAMBA2_SSD_D_PER_CHANNEL) {
+            if (int rc = pad_copy(a->D, s->nheads, 1, P, at(pp.d), 1, Pp, st, nullptr)) return rc;
+            pa.D = at(pp.d);
+        }
+        pa.out = at(pp.out);
+        pa.pre_gate = (f & MAMBA2_SSD_HAS_Z) && a->pre_gate ? at(pp.pre) : nullptr;
+    }
+    if (pp.pad_n) {
+        if (int rc = pad_copy(a->B, blg, 1, N, at(pp.b), 1, Np, st, nullptr)) return rc;
+        if (int rc = pad_copy(a->C, blg, 1, N, at(pp.c), 1, Np, st, nullptr)) return rc;
+        pa.B = at(pp.b);
+        pa.C = at(pp.c);
+    }
+    if (f & MAMBA2_SSD_HAS_INITIAL) {
+        if (int rc = pad_copy(a->initial_states, bh, P, N, at(pp.init), Pp, Np, st, nullptr)) return rc;
+        pa.initial_states = at(pp.init);
+    }
+    pa.final_state = a->final_state ? at(pp.fin) : nullptr;
+    if (int rc = fwd_impl(&pa, ws + pp.inner, have - pp.inner, st, tr)) return rc;
+    if (pp.pad_p) {
+        if (int rc = pad_copy(pa.out, blh, 1, Pp, a->out, 1, P, st, tr)) return rc;
+        if (pa.pre_gate)
+            if (int rc = pad_copy(pa.pre_gate, blh, 1, Pp, a->pre_gate, 1, P, st, tr)) return rc;
+    }
+    if (a->final_state)
+        if (int rc = pad_copy(pa.final_state, bh, Pp, Np, a->final_state, P, N, st, tr)) return rc;
+    return ok();
+}
 
 int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes, void *stream,
              Trace *tr) {
@@ -317,6 +438,8 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
         return fail(MAMBA2_SSD_ERR_WORKSPACE, "workspace of %zu bytes needed, got %zu", need, have);
     const bool allow_cb = have >= need;
     hipStream_t st = (hipStream_t)stream;
+    const PadPlan pp = pad_plan(s, f, allow_cb);
+    if (pp.on) return fwd_padded(a, pp, (char *)workspace, have, st, tr);
 
     ssd::FwdParams prm{};
     prm.x = a->x;

@@ -226,6 +226,27 @@ __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_stat
 #endif
 
 // --------------------------------------------------------------------------
+// zero-padding copy: dst[o][r][c] = (r < rs && c < cs) ? src[o][r][c] : 0 for
+// r < rd, c < cd (a [outer, rs, cs] array into [outer, rd, cd]; with rd <= rs
+// and cd <= cs it cuts the padding off again).  Grid-stride over dst.
+// --------------------------------------------------------------------------
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
+constexpr int kPadThreads = 256;
+__global__ __launch_bounds__(kPadThreads) void k_pad_copy(const float *src, int64_t outer, int rs, int cs,
+                                                          float *dst, int rd, int cd) {
+    const int64_t total = outer * rd * cd;
+    for (int64_t i = (int64_t)blockIdx.x * kPadThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kPadThreads) {
+        const int c = (int)(i % cd);
+        const int64_t orow = i / cd;
+        const int r = (int)(orow % rd);
+        const int64_t o = orow / rd;
+        dst[i] = (r < rs && c < cs) ? src[(o * rs + r) * cs + c] : 0.f;
+    }
+}
+#endif
+
+// --------------------------------------------------------------------------
 // generic token recurrence (any headdim / dstate <= 256); one wave per (b,h,p)
 // --------------------------------------------------------------------------
 #ifndef SSD_KERNEL_TEMPLATES_ONLY

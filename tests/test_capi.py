@@ -123,6 +123,15 @@ def test_workspace_size_formula():
     assert ws(fwd, batch=1, seqlen=128, nheads=8, ngroups=1, dstate=128) == 2 * 64 * 64 * 4
     assert ws(fwd, batch=1, seqlen=384, nheads=2, ngroups=1) == 0   # 6 chunks: saves 5
     assert ws(fwd, batch=1, seqlen=512, nheads=2, ngroups=1) > 0    # 8 chunks: saves 7
+    # headdim 32, dstate 128 (zero-padded into the fused kernels): x and out
+    # padded to [B,L,H,64], the final state to [B,H,64,128], then the fused
+    # plan of the padded shape (here one segment: nothing more)
+    got = ws(fwd, batch=8, seqlen=4096, nheads=64, ngroups=64, headdim=32, dstate=128)
+    blh = 8 * 4096 * 64
+    assert got == 2 * blh * 64 * 4 + 8 * 64 * 64 * 128 * 4
+    # dstate 32: B and C padded to [B,L,G,64], the final state to [B,H,64,64]
+    got = ws(fwd, batch=8, seqlen=4096, nheads=256, ngroups=64, dstate=32)
+    assert got == 2 * 8 * 4096 * 64 * 64 * 4 + 8 * 256 * 64 * 64 * 4
     # one segment per stream: no segment buffers (dstate 128: C . B^T only)
     assert ws(fwd, batch=8, seqlen=4096, nheads=64, ngroups=8, dstate=128) == 8 * 8 * 64 * 64 * 64 * 4
     assert ws(fwd, batch=8, seqlen=4096, nheads=64, ngroups=8) == 0

@@ -67,8 +67,15 @@ CASES = [
     ([2, 300, 4, 128, 64, 64, 2], ("D", "z", "bias", "init"), True, (0.0, math.inf)),
     ([1, 200, 2, 128, 128, 128, 1], ("D2", "z", "init"), True, (0.0, math.inf)),
     ([1, 700, 2, 192, 64, 64, 1], ("D", "bias"), False, (0.05, 0.9)),  # segments
-    # generic token-recurrence path (headdim/dstate outside the MFMA kernels)
+    # zero-padded into the MFMA kernels: headdim below or between multiples of
+    # 64, dstate below 64 or between 64 and 128
     ([2, 70, 4, 32, 16, 16, 2], ("D", "z", "init"), True, (0.0, math.inf)),
+    ([2, 200, 4, 32, 128, 64, 2], ("D2", "z", "bias", "init"), True, (0.0, math.inf)),
+    ([1, 300, 4, 64, 32, 64, 2], ("D", "init"), True, (0.0, math.inf)),
+    ([2, 150, 3, 48, 96, 64, 1], ("D2", "z", "bias", "init"), False, (0.05, 0.9)),
+    ([1, 130, 2, 80, 16, 64, 1], ("D2", "init"), True, (0.0, math.inf)),  # P 80 -> 2 heads of 64
+    ([1, 900, 2, 16, 48, 64, 1], ("bias", "init"), True, (0.0, math.inf)),  # segmented after padding
+    # generic token-recurrence path (dstate above 128)
     ([1, 33, 3, 20, 200, 8, 1], ("bias",), True, (0.0, math.inf)),
 ]
 

@@ -76,7 +76,9 @@ FWD = [
     ([2, 150, 4, 64, 64, 64, 2], ("z", "bias", "init"), "save"),  # training forward
     ([1, 270, 4, 64, 128, 64, 1], ("D",), "packed"),              # packed sequences, dstate 128
     ([1, 250, 4, 64, 64, 64, 2], ("init",), "varlen"),            # varlen states
-    ([2, 70, 3, 32, 16, 16, 1], ("D", "z"), ""),                  # generic path
+    ([2, 70, 3, 32, 16, 16, 1], ("D", "z"), ""),                  # zero-padded (P 32, N 16)
+    ([1, 200, 2, 80, 96, 64, 1], ("D2", "z", "init"), ""),        # zero-padded (P 80, N 96)
+    ([1, 40, 2, 20, 200, 8, 1], ("D",), ""),                      # generic path (N 200)
 ]
 
 
