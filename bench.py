@@ -694,17 +694,19 @@ def api_host_cost(torch, api, inp, chunk, calls=50):
     return host * 1e6
 
 
-def bench_fwd_bwd(torch, api, inp, chunk, steps, warmup):
+def bench_fwd_bwd(torch, api, inp, chunk, steps, warmup, save=True):
     """fwd + bwd through autograd; None if the backward is not available for
     this shape.  The upstream gradients are those of the loss
     mean(y^2) + mean(final^2), formed once outside the timed calls, so the
     timing covers the op's forward and backward and not torch's elementwise
-    loss kernels."""
+    loss kernels.  save: the training policy (keep the chunk-start states, or
+    recompute them in the backward)."""
     leaves = {k: v.detach().clone().requires_grad_(True) for k, v in inp.items()}
 
     def fwd():
         return api.mamba2_ssd_fwd(leaves["x"], leaves["dt"], leaves["A"], leaves["B"],
-                                  leaves["C"], chunk, dt_softplus=True, return_final_state=True)
+                                  leaves["C"], chunk, dt_softplus=True, return_final_state=True,
+                                  save_chunk_states=save)
 
     grads = []
 
@@ -740,13 +742,14 @@ def bench_fwd_bwd(torch, api, inp, chunk, steps, warmup):
     return statistics.median(samples), None
 
 
-def autograd_memory(torch, api, inp, chunk):
+def autograd_memory(torch, api, inp, chunk, save=True):
     """Saved-tensor bytes and peak memory of one autograd forward + backward
     (the reference backward bench's saved-tensor and extra-peak figures,
-    mamba2_backward_bench.py:168-215, 420-489).  saved: bytes of the distinct
-    storages autograd keeps between the passes beyond the inputs; peak_extra:
-    the allocator's peak during forward + backward above what was allocated
-    before (inputs and upstream gradients)."""
+    mamba2_backward_bench.py:168-215, 420-489) under the training policy
+    ``save`` (keep the chunk-start states or recompute them).  saved: bytes of
+    the distinct storages autograd keeps between the passes beyond the inputs;
+    peak_extra: the allocator's peak during forward + backward above what was
+    allocated before (inputs and upstream gradients)."""
     leaves = {k: v.detach().clone().requires_grad_(True) for k, v in inp.items()}
     inputs = {v.untyped_storage().data_ptr() for v in leaves.values()}
     seen = {}
@@ -768,7 +771,8 @@ def autograd_memory(torch, api, inp, chunk):
     torch.cuda.reset_peak_memory_stats()
     with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
         out, fin = api.mamba2_ssd_fwd(leaves["x"], leaves["dt"], leaves["A"], leaves["B"],
-                                      leaves["C"], chunk, dt_softplus=True, return_final_state=True)
+                                      leaves["C"], chunk, dt_softplus=True, return_final_state=True,
+                                      save_chunk_states=save)
     torch.autograd.backward((out, fin), (gy, gf))
     torch.cuda.synchronize()
     peak = torch.cuda.max_memory_allocated() - base
@@ -1091,8 +1095,16 @@ def main(argv=None):
             log(f"public API (autograd) fwd+bwd median {api_fwd_bwd_ms:.4f} ms per step "
                 "(runs of 3 consecutive steps)")
             memory = autograd_memory(torch, api, inp, chunk)
-            log(f"autograd memory: saved {memory['saved_bytes'] / 2**30:.3f} GiB beyond the inputs, "
-                f"peak {memory['peak_extra_bytes'] / 2**30:.3f} GiB above inputs + upstream grads")
+            log(f"autograd memory (keep chunk states): saved {memory['saved_bytes'] / 2**30:.3f} GiB "
+                f"beyond the inputs, peak {memory['peak_extra_bytes'] / 2**30:.3f} GiB above inputs + "
+                "upstream grads")
+            # the other training policy: chunk-start states recomputed in the backward
+            rec_ms, _ = bench_fwd_bwd(torch, api, inp, chunk, max(5, args.steps // 3), 3, save=False)
+            rec_mem = autograd_memory(torch, api, inp, chunk, save=False)
+            memory = {**memory, "policy": "save_chunk_states=True",
+                      "recompute": {**rec_mem, "api_fwd_bwd_ms": rec_ms, "policy": "save_chunk_states=False"}}
+            log(f"recompute policy: fwd+bwd {rec_ms:.4f} ms per step, saved "
+                f"{rec_mem['saved_bytes'] / 2**30:.3f} GiB, peak {rec_mem['peak_extra_bytes'] / 2**30:.3f} GiB")
     packed = None
     if not args.no_full and shape[3] == 64 and shape[4] in (64, 128):
         # packed sequences (seq_idx) on the same shape: the cost of the masks
