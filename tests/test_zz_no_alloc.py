@@ -1,9 +1,10 @@
 """mamba2_ssd_fwd_noalloc (the allocation-free forward) against mamba2_ssd_fwd.
 
 Both entry points run the same kernels on the same plan; the allocation-free one
-takes its scratch (segment states and log decays of long sequences with few
-streams) from the library's static device array instead of a workspace, so the
-results must be bit-identical.  The calls come in a row on one GPU, each
+takes its scratch (segment contributions and log decays of long sequences with
+few streams, the C . B^T products of dstate 128 with many heads per group, the
+padded copies of headdims off multiples of 64) from the library's static device
+array instead of a workspace, so the results must be bit-identical.  The calls come in a row on one GPU, each
 smaller than the one before, so a call that read scratch contents left by the
 previous one would show.  Output buffers start as NaN: every element must be
 written.
@@ -37,12 +38,18 @@ def _args(rt, shape, dev, flags, limit, out, fin):
 
 CALLS = [
     # shape [B, L, H, P, N, chunk, G], features: 16 (b, h) streams of 32
-    # chunks -> 16 segments of 2 chunks, 32 state-only pre-segments
+    # chunks -> 16 segments of 2 chunks, 32 state-only pre-segments and the
+    # segment recurrence over them (too many to fold)
     ([2, 2048, 8, 64, 64, 64, 2], ("D2", "z", "bias", "init")),
-    # smaller: 4 streams -> 13 segments of one chunk, a ragged last chunk
+    # smaller: 4 streams -> 13 segments of one chunk folding up to 12
+    # pre-segments, a ragged last chunk
     ([1, 800, 4, 64, 64, 64, 1], ("D",)),
     # smaller still, dstate 128: 4 streams of 10 chunks -> 10 segments
     ([1, 600, 2, 64, 128, 128, 1], ("z", "init")),
+    # dstate 128 with 8 heads per group: C . B^T of each chunk in the scratch
+    ([1, 300, 8, 64, 128, 64, 1], ("D",)),
+    # headdim 32, dstate 48: zero-padded copies in the scratch
+    ([1, 200, 2, 32, 48, 64, 1], ("D2", "z", "init")),
 ]
 
 
