@@ -232,19 +232,6 @@ __device__ __forceinline__ SplitTile tile_at(_Float16 *base, int i) {
     return SplitTile{base + (2 * i) * kTile, base + (2 * i + 1) * kTile};
 }
 
-// Token-major staging: tile[t][c] = f(t, c4) (a float4 of columns c4..c4+3),
-// for the 64 x 64 tile, using all threads of a 256-thread workgroup.
-template <class F>
-__device__ __forceinline__ void stage_rows(SplitTile d, F f) {
-    for (int i = threadIdx.x; i < 64 * 16; i += 256) {
-        const int t = i >> 4, c4 = (i & 15) * 4;
-        half4 vh, vl;
-        split4(f(t, c4), vh, vl);
-        *(half4 *)&d.hi[t * kTS + c4] = vh;
-        *(half4 *)&d.lo[t * kTS + c4] = vl;
-    }
-}
-
 // Column-major staging: tile[c][slot] = f(t, c) with t = the token of `slot`
 // (perm_token order when PERM, else slot itself).  Thread c = tid % 64 reads
 // one column, so for each token the 64 lanes of a wave read 64 consecutive
@@ -384,13 +371,6 @@ __device__ __forceinline__ f32x4 join4(half4 h, half4 l) {
         : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
         : "v"(hb[0]), "v"(hb[1]), "v"(lb[0]), "v"(lb[1]));
     return f32x4{a, b, c, d};
-}
-
-// fp32 values of rows row0 + 4 (l / 16) + r, column c0 + l % 16 (r = 0..3):
-// the MFMA accumulator layout of a 16-row block.
-__device__ __forceinline__ f32x4 tile_acc(SplitTile s, int row0, int c0) {
-    const int k0 = row0 + 4 * ((threadIdx.x & 63) >> 4);
-    return join4(tr4(s.hi, k0, c0), tr4(s.lo, k0, c0));
 }
 
 // fp32 values of tile[row][c0 .. c0 + 3] (one 8-byte read of each half).
