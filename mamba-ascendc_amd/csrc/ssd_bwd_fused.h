@@ -555,9 +555,19 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             if (lane == 0) prm.part_dbias[bhk * kBwsSlots + W] = dbias;
         };
 
+        // kRev: C . B^T of the chunk in both orientations (the blocks of
+        // phase A), formed on a chunk's first head step and reused by its
+        // other heads (B and C stay staged for the whole chunk)
+        f32x4 cbT[4], cbS[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            cbT[j] = zero4();
+            cbS[j] = zero4();
+        }
         lds_barrier(); // first tiles staged
         for (int n = 0; n < NS; ++n) {
             const int k = chunk_of(n), r = n % R, par = n & 1;
+            const bool form_cb = !kRev || r == 0;
             if (n > 0) epilogue(n - 1);
             __bf16 *la = opaque_lds_t(lds);
             const SplitTile xt = tile_at(la, par), gt = tile_at(la, 2 + par);
@@ -586,12 +596,16 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         if (j <= W) {
-                            f32x4 cb = zero4(), dw = zero4();
+                            f32x4 dw = zero4();
+                            if (form_cb) {
+                                f32x4 cbn = zero4();
 #pragma unroll
-                            for (int ks = 0; ks < 2; ++ks) {
-                                cb = mma3f(frag(Bt, 16 * j + r16, ks), Co[ks], cb);
-                                dw = mma3f(frag(xt, 16 * j + r16, ks), Go[ks], dw);
+                                for (int ks = 0; ks < 2; ++ks) cbn = mma3f(frag(Bt, 16 * j + r16, ks), Co[ks], cbn);
+                                cbT[j] = cbn;
                             }
+                            const f32x4 cb = cbT[j];
+#pragma unroll
+                            for (int ks = 0; ks < 2; ++ks) dw = mma3f(frag(xt, 16 * j + r16, ks), Go[ks], dw);
                             const float4 qv = *(const float4 *)&q_[16 * j + 4 * kq];
                             const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
                             const float qa[4] = {qv.x, qv.y, qv.z, qv.w}, cva[4] = {cv.x, cv.y, cv.z, cv.w};
@@ -622,12 +636,16 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         if (j >= W) {
-                            f32x4 cb = zero4(), dw = zero4();
+                            f32x4 dw = zero4();
+                            if (form_cb) {
+                                f32x4 cbn = zero4();
 #pragma unroll
-                            for (int ks = 0; ks < 2; ++ks) {
-                                cb = mma3f(frag(Ct, 16 * j + r16, ks), Bo[ks], cb);
-                                dw = mma3f(frag(gt, 16 * j + r16, ks), Xo[ks], dw);
+                                for (int ks = 0; ks < 2; ++ks) cbn = mma3f(frag(Ct, 16 * j + r16, ks), Bo[ks], cbn);
+                                cbS[j] = cbn;
                             }
+                            const f32x4 cb = cbS[j];
+#pragma unroll
+                            for (int ks = 0; ks < 2; ++ks) dw = mma3f(frag(gt, 16 * j + r16, ks), Xo[ks], dw);
                             const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
                             const float cva[4] = {cv.x, cv.y, cv.z, cv.w};
                             int sva[4] = {0, 0, 0, 0};
