@@ -15,6 +15,12 @@ error of a rounding scheme can be measured on the CPU without building it:
                                  hi.hi + hi.lo + lo.hi (the kernels' scheme:
                                  split fp16 in the forward)
 * ``fp32``                    -- no rounding (the chunked algorithm itself)
+* ``split16_a`` / ``split16_b`` -- two products: only the left (a) or right (b)
+                                 operand split, the other rounded to fp16
+
+``mode`` is one scheme for all four products, or a dict naming one per
+product (keys ``cb``, ``wx``, ``cs``, ``u``; missing keys take ``split16``),
+which measures what each product contributes on its own.
 
 The chunked algorithm is that of ``oracle.ssd_reference.ssd_chunked_core``
 (mamba_torch/ssd_reference.py:113-189) in the kernels' arrangement: q folded
@@ -29,7 +35,8 @@ import math
 import torch
 import torch.nn.functional as F
 
-MODES = ("fp32", "fp16", "bf16", "split16", "splitbf16")
+MODES = ("fp32", "fp16", "bf16", "split16", "splitbf16", "split16_a", "split16_b")
+PRODUCTS = ("cb", "wx", "cs", "u")
 
 
 def _round(t: torch.Tensor, kind: str) -> torch.Tensor:
@@ -42,18 +49,31 @@ def _product(eq: str, a: torch.Tensor, b: torch.Tensor, mode: str) -> torch.Tens
         return torch.einsum(eq, a, b)
     if mode in ("fp16", "bf16"):
         return torch.einsum(eq, _round(a, mode), _round(b, mode))
-    base = "fp16" if mode == "split16" else "bf16"
+    base = "bf16" if mode == "splitbf16" else "fp16"
     ah, bh = _round(a, base), _round(b, base)
     al, bl = _round(a - ah, base), _round(b - bh, base)
+    if mode == "split16_a":
+        return torch.einsum(eq, ah, bh) + torch.einsum(eq, al, bh)
+    if mode == "split16_b":
+        return torch.einsum(eq, ah, bh) + torch.einsum(eq, ah, bl)
     return torch.einsum(eq, ah, bh) + torch.einsum(eq, ah, bl) + torch.einsum(eq, al, bh)
 
 
 def ssd_forward_emulated(x, dt, A, B, C, mode: str, chunk: int = 64):
     """y [b, l, h, p] and the final state [b, h, p, n] (float32) of the SSD
     forward with softplus(dt), no D / z / initial state, the four matrix
-    products' operands rounded per ``mode`` and float64 everywhere else."""
-    if mode not in MODES:
-        raise ValueError(f"mode {mode!r} is not one of {MODES}")
+    products' operands rounded per ``mode`` (one scheme, or a dict per
+    product) and float64 everywhere else."""
+    per = dict.fromkeys(PRODUCTS, "split16")
+    if isinstance(mode, dict):
+        if set(mode) - set(PRODUCTS):
+            raise ValueError(f"products {sorted(set(mode) - set(PRODUCTS))} are not among {PRODUCTS}")
+        per.update(mode)
+    else:
+        per = dict.fromkeys(PRODUCTS, mode)
+    for m in per.values():
+        if m not in MODES:
+            raise ValueError(f"mode {m!r} is not one of {MODES}")
     b, l, h, p = x.shape
     g, n = B.shape[2], B.shape[3]
     r = h // g
@@ -75,20 +95,20 @@ def ssd_forward_emulated(x, dt, A, B, C, mode: str, chunk: int = 64):
     Bc = B.repeat_interleave(r, dim=2).reshape(b, k, T, h, n)
     Cc = C.repeat_interleave(r, dim=2).reshape(b, k, T, h, n)
     # (1) C_t . B_s and (2) W[t][s] = (C_t . B_s) exp(cs_t - cs_s) q_s (s <= t) against x
-    cb = _product("bkthn,bkshn->bkhts", Cc, Bc, mode)
+    cb = _product("bkthn,bkshn->bkhts", Cc, Bc, per["cb"])
     csh = cs.permute(0, 1, 3, 2)  # [b, k, h, T]
     lower = torch.tril(torch.ones(T, T, dtype=torch.bool))
     w = torch.where(lower, cb * torch.exp(csh[..., :, None] - csh[..., None, :]), torch.zeros((), dtype=cb.dtype))
     w = w * qc.permute(0, 1, 3, 2)[..., None, :]
-    y_diag = _product("bkhts,bkshp->bkthp", w, xc, mode)
+    y_diag = _product("bkhts,bkshp->bkthp", w, xc, per["wx"])
     # (4) the chunk's state update B^T . (exp(cs_last - cs_t) q_t x_t)
     to_end = torch.exp(cs[:, :, -1:, :] - cs) * qc
-    U = _product("bkthn,bkthp->bkhpn", Bc, xc * to_end[..., None], mode)
+    U = _product("bkthn,bkthp->bkhpn", Bc, xc * to_end[..., None], per["u"])
     # (3) exp(cs_t) C_t . S with S the state entering the chunk
     S = torch.zeros(b, h, p, n, dtype=torch.float64)
     ys = []
     for kk in range(k):
-        y_off = _product("bthn,bhpn->bthp", Cc[:, kk], S, mode) * torch.exp(cs[:, kk])[..., None]
+        y_off = _product("bthn,bhpn->bthp", Cc[:, kk], S, per["cs"]) * torch.exp(cs[:, kk])[..., None]
         ys.append(y_diag[:, kk] + y_off)
         S = torch.exp(cs[:, kk, -1])[..., None, None] * S + U[:, kk]
     y = torch.stack(ys, 1).reshape(b, k * T, h, p)[:, :l]

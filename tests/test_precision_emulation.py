@@ -61,6 +61,31 @@ def test_single_products_miss_the_contract_split_fp16_does_not(cfg_index, shape)
     assert err["splitbf16"][0] < MAXABS / 4
 
 
+PARTIAL = {"cb": "C . B^T", "wx": "W . x", "cs": "C . S", "u": "B^T . (decay q x)"}
+
+
+@pytest.mark.parametrize("product", sorted(PARTIAL))
+def test_every_product_needs_its_full_split(product):
+    """Per product, on the C4 unit: the other three split, this one rounded
+    (one fp16 product, or two with only one operand split).  Measured y
+    max-abs (all split: 4.2e-5):
+
+        product   fp16     a split   b split
+        C.B^T     3.6e-2   2.6e-2    2.7e-2
+        W.x       6.7e-2   3.8e-2    3.6e-2
+        C.S       2.8e-2   1.6e-2    2.5e-2
+        B^T.(qx)  2.4e-2   2.0e-2    2.6e-2
+
+    Every variant uses at least 80 % of the 2e-2 bound, against 0.2 % with
+    the three-product split: no product can drop a term."""
+    u = _unit(3, [4, 2048, 16, 64, 64, 64, 4])
+    ref, _ = ssd_chunk_scan_ref(u["x"], u["dt"], u["A"], u["B"], u["C"], 64, dt_softplus=True,
+                                return_final_state=True)
+    for mode in ("fp16", "split16_a", "split16_b"):
+        y, _ = ssd_forward_emulated(u["x"], u["dt"], u["A"], u["B"], u["C"], {product: mode})
+        assert parity_metrics(y, ref)[0] > 0.75 * MAXABS, (product, mode)
+
+
 def test_emulation_rounding_is_live():
     """A planted check: with operands rounded to fp16 the emulated products
     differ from the exact ones, and hi + lo recovers more than fp16 alone."""
