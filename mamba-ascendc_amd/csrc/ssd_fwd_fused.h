@@ -156,7 +156,16 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     // T3(s) = tiles 3 s .. 3 s + 2 and T4(s) = tile 6 + s; state-only pass
     // T2(s), T3(s) = tiles 2 s, 2 s + 1
     constexpr int kTiles = kStateOnly ? 4 : 8;
-    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * kTiles * kTile];
+    // full pass: T1..T3 rows kXS = 80 halves apart, T4 rows kTS = 72 apart
+    // (80 for all eight would not fit in LDS).  At 80 the 16-byte operand
+    // reads of T1 and the transposing reads of T2, T3 are free of LDS bank
+    // conflicts (two-way at 72): C3 forward 0.9 % faster.  The state-only
+    // pass keeps 72, so two of its workgroups share a CU, and so do the z
+    // gate and the saving packed pass, whose registers the extra address
+    // offsets crowd (the gate 1 % slower at 80; the other spilled).
+    constexpr int kXS = (kStateOnly || kGate || (kSave && kSeq)) ? kTS : 80, kXTile = 64 * kXS;
+    constexpr int kXTiles = kStateOnly ? 4 : 6;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * kXTiles * kXTile + 2 * (kTiles - kXTiles) * kTile];
     // Per-token values of a chunk written by the producers' dt prologue, by
     // chunk parity; one struct, so the writing wave addresses every member
     // from one base (see the prologue).
@@ -181,10 +190,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     const int w = wave & 3; // index of the wave within its role
     const int r16 = lane & 15, kq = lane >> 4;
 
-    auto T1 = [&](int s) { return tile_at(lds, 3 * s); };
-    auto T2 = [&](int s) { return tile_at(lds, kStateOnly ? 2 * s : 3 * s + 1); };
-    auto T3 = [&](int s) { return tile_at(lds, kStateOnly ? 2 * s + 1 : 3 * s + 2); };
-    auto T4 = [&](int s) { return tile_at(lds, 6 + s); };
+    auto xtile = [&](int i) { return SplitTile{lds + (2 * i) * kXTile, lds + (2 * i + 1) * kXTile}; };
+    auto T1 = [&](int s) { return xtile(3 * s); };
+    auto T2 = [&](int s) { return xtile(kStateOnly ? 2 * s : 3 * s + 1); };
+    auto T3 = [&](int s) { return xtile(kStateOnly ? 2 * s + 1 : 3 * s + 2); };
+    auto T4 = [&](int s) { return tile_at(lds + 2 * kXTiles * kXTile, s); };
 
     // unit = (((b * G + g) * nseg + sg) * R + r) * nsplit + nh: the column
     // halves of a head next to each other, so the second reads the head's x
@@ -248,8 +258,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     auto put = [&](SplitTile d, int row, float4 v) {
         half4 vh, vl;
         split4(v, vh, vl);
-        *(half4 *)&d.hi[row * kTS + c4] = vh;
-        *(half4 *)&d.lo[row * kTS + c4] = vl;
+        *(half4 *)&d.hi[row * kXS + c4] = vh;
+        *(half4 *)&d.lo[row * kXS + c4] = vl;
     };
     // discretise (lane = token), cumsum in log2 units, fill the stage tiles
     auto p_stage = [&](int k, int s, auto slot_c) {
@@ -470,7 +480,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         if (j <= W)
     #pragma unroll
                             for (int ks = 0; ks < 2; ++ks)
-                                cb = mma3f(frag(t1, 16 * j + r16, ks), Cown[ks], cb);
+                                cb = mma3f(frag_s<kXS>(t1, 16 * j + r16, ks), Cown[ks], cb);
     #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int so = 16 * j + 4 * kq + i;
@@ -511,10 +521,10 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 // each x fragment feeds both y^T (W part) and U^T
     #pragma unroll
                 for (int m = 0; m < 2; ++m) {
-                    const Frag a3 = frag_tp(t3, m, 16 * W);
+                    const Frag a3 = frag_tp_s<kXS>(t3, m, 16 * W);
     #pragma unroll
                     for (int pb = 0; pb < 4; ++pb) {
-                        const Frag f2 = frag_tp(t2, m, 16 * pb);
+                        const Frag f2 = frag_tp_s<kXS>(t2, m, 16 * pb);
                         if (2 * m <= W) acc[pb] = mma3f(f2, WT[m], acc[pb]);
                         U[pb] = mma3f(a3, f2, U[pb]);
                     }
@@ -526,7 +536,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         const int p = 16 * pb + 4 * kq;
                         float4 v = make_float4(acc[pb][0], acc[pb][1], acc[pb][2], acc[pb][3]);
                         if (prm.has_D) {
-                            const f32x4 xa = tile_row4(t2, own, p); // x from the staged tile
+                            const f32x4 xa = tile_row4_s<kXS>(t2, own, p); // x from the staged tile
                             const float4 xv = make_float4(xa[0], xa[1], xa[2], xa[3]);
                             const float4 d = *(const float4 *)&s_Dv[p];
                             v.x += d.x * xv.x;
@@ -553,9 +563,9 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 if (kStateOnly) {
     #pragma unroll
                     for (int m = 0; m < 2; ++m) {
-                        const Frag a3 = frag_tp(t3, m, 16 * W);
+                        const Frag a3 = frag_tp_s<kXS>(t3, m, 16 * W);
     #pragma unroll
-                        for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag_tp(t2, m, 16 * pb), U[pb]);
+                        for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag_tp_s<kXS>(t2, m, 16 * pb), U[pb]);
                     }
                 }
                 const float alpha = kSeq ? exp2_f(cs_last) * s_carry[s] : exp2_f(cs_last);
