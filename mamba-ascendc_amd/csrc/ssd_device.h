@@ -192,6 +192,55 @@ __device__ __forceinline__ float sum_kq(float v) { return add_xor32(add_xor16(v)
 // Sum over the 64 lanes, in every lane.
 __device__ __forceinline__ float wave_sum(float v) { return sum_kq(sum16(v)); }
 
+// Maximum over the 64 lanes, in every lane (the pattern of wave_sum).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, xor16_f(v));
+    return fmaxf(v, xor32_f(v));
+}
+
+// Binary exponent e of v = m 2^e, m in [1, 2), clamped to [-126, 126] (0
+// for v = 0): 2^-e scales v into [1, 2), and 2^e and 2^-e are finite.
+__device__ __forceinline__ int scale_exp(float v) {
+    return min(max(__builtin_amdgcn_frexp_expf(v) - 1, -126), 126);
+}
+
+// Power-of-two scales of the fused forwards' split-fp16 operands.  q enters
+// W and the state update, and the state scales with it, so for tiny q
+// (softplus of a very negative dt) those operands would fall into fp16's
+// subnormal range and lose their low bits.  A chunk's q is scaled by 2^-ek
+// with its sum in [8, 16) (mean in [1/8, 1/4), largest below 16), and the
+// state leaving it is held as S 2^-eN:
+//   eN = ek                                  where the state is cut (packed sequences),
+//   eN = min(max(ek, eS + floor(cs_last)), 126)  otherwise,
+// with eS the exponent of the state entering the chunk and cs_last its log2
+// decay, since |S'| <= 2^(eS + cs_last) |S 2^-eS| + 2^ek |U 2^-ek|.  All
+// scales are exact, so they change results only where fp16 would have lost
+// bits.
+__device__ __forceinline__ int chunk_q_exp(float q_sum) { return max(scale_exp(q_sum) - 3, -126); }
+__device__ __forceinline__ int next_state_exp(int eS, int ek, float cs_last, bool cut) {
+    return cut ? ek : min(max(ek, eS + (int)floorf(fmaxf(cs_last, -512.f))), 126);
+}
+
+// Exponent of a state known to be zero (any scale holds it exactly; far
+// below every exponent the rules above produce).
+constexpr int kZeroState = -1000;
+
+// Exponent of a state from the largest magnitudes its four consumer waves
+// hold (an LDS array of four floats).
+__device__ __forceinline__ int state_exp_of(const float *wave_max4) {
+    const float4 m4 = *(const float4 *)wave_max4;
+    const float m = fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w));
+    return m > 0.f ? scale_exp(m) : kZeroState;
+}
+// A chunk's products are formed in the state's scale when the state
+// outweighs them by more than 2^kMaxShift (they then hold below 2^-kMaxShift
+// of the output).
+constexpr int kMaxShift = 60;
+
 // v of lane 63 - l (row_mirror within the row, then the row order reversed).
 __device__ __forceinline__ float reverse_lanes(float v) {
     return xor32_f(xor16_f(dpp_f<0x140>(v)));

@@ -176,8 +176,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         float off[2][TS];
         float carry[2]; // kSeq: 1 where the state carries over the chunk
         int mixed[2];   // kSeq: the chunk holds more than one id (C.B^T needs the id mask)
+        int qexp[2];    // ek: q holds q 2^-ek
+        int sexp[2];    // eN: T3 holds B dec q 2^-eN, the scale of the state leaving the chunk
     };
     __shared__ __attribute__((aligned(16))) ChunkTok s_tok;
+    __shared__ __attribute__((aligned(16))) float s_smax[4]; // |entering state| maximum per consumer wave
     auto &s_cs = s_tok.cs, &s_q = s_tok.q;
     auto &s_sid = s_tok.sid;
     auto &s_off = s_tok.off;
@@ -224,6 +227,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     const int rt = pt >> 4, c4 = (pt & 15) * 4;
     float4 xr[kDepth][4], br[kDepth][4];
     float dtr[kDepth];
+    int p_eS = kZeroState; // exponent of the state entering the chunk being staged
     int sidr[kDepth], sprv[kDepth]; // kSeq: id of token `lane`, id of the token before the chunk
     const int rowHP4 = (int)(rowHP * 4), rowGN4 = (int)(rowGN * 4); // token strides, bytes
     const int hr = h / prm.hdiv, Hr = H / prm.hdiv;                      // the real head
@@ -265,21 +269,21 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     auto p_stage = [&](int k, int s, auto slot_c) {
         constexpr int sl = decltype(slot_c)::value;
         const int tv = (int)min((int64_t)T, prm.L - (int64_t)k * T); // <= 0 past the end
-        float q = 0.f, a = 0.f;
-        if (lane < tv) {
-            q = discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
-            a = Ah2 * q;
-        }
-        const float cs = wave_inclusive_scan(a);
+        float q = 0.f;
+        if (lane < tv) q = discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
+        const float sq = wave_inclusive_scan(q); // prefix sums of q
+        const float cs = Ah2 * sq;               // log2 units
         const float cs_last = readlane_f(cs, T - 1);
+        const int ek = chunk_q_exp(readlane_f(sq, T - 1));
         // every member from one base the optimizer cannot split into
         // per-array address registers
         ChunkTok *tk = opaque_lds_t(&s_tok);
         if (w == 0) {
             tk->cs[s][lane] = cs;
-            tk->q[s][lane] = q;
+            tk->q[s][lane] = __builtin_amdgcn_ldexpf(q, -ek);
         }
         float dec = exp2_f(cs_last - cs);
+        bool cut = false; // kSeq: the state does not carry over the chunk
         if (kSeq) {
             // rows past the sequence end repeat its last token's id
             const int sid = sidr[sl], e_end = __shfl(sid, T - 1, kWave), e_prev = sprv[sl];
@@ -293,18 +297,32 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     tk->mixed[s] = mixed ? 1 : 0;
                 }
             }
+            cut = e_end != e_prev;
         }
+        // the state leaving the chunk is S 2^-eN (every producer wave runs
+        // the same recurrence as the consumers' eS)
+        const int eN = next_state_exp(p_eS, ek, cs_last, cut);
+        p_eS = eN;
+        if (w == 0 && lane == 0) {
+            tk->qexp[s] = ek;
+            tk->sexp[s] = eN;
+        }
+        const float qn = __builtin_amdgcn_ldexpf(q, -eN);
         const SplitTile t1 = T1(s), t2 = T2(s), t3 = T3(s);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = rt + 16 * j;
-            const float dr = __shfl(dec * q, row, kWave);
+            const float dr = __shfl(dec * qn, row, kWave);
             const float4 xv = xr[sl][j], bv = br[sl][j];
             put(t2, row, xv);
             put(t3, row, make_float4(bv.x * dr, bv.y * dr, bv.z * dr, bv.w * dr));
             if (!kStateOnly) put(t1, row, bv);
         }
     };
+
+    // the entering state can be nonzero: its magnitude sets its first scale,
+    // through one more barrier in both roles (wave-uniform)
+    const bool s0_nonzero = (!kStateOnly || kSave) && (sp.seg_in != nullptr || prm.init != nullptr);
 
     // ------------------------------------------------------------ producer role
     using S0 = std::integral_constant<int, 0>;
@@ -318,6 +336,10 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         p_load(kbeg, S0{});
         p_load(kbeg + 1, S1{});
         p_load(kbeg + 2, S2{});
+        if (s0_nonzero) {
+            lds_barrier(); // the consumers' maxima of the entering state
+            p_eS = state_exp_of(s_smax);
+        }
         p_stage(kbeg, 0, S0{});
         p_load(kbeg + 3, S0{});
         lds_barrier();
@@ -351,7 +373,10 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         constexpr int W = decltype(wave_c)::value;
         const int own = 16 * W + r16; // token row of this lane
         // state: Sr[pb][i] = S[p = 16 pb + l % 16][n = 16 W + 4 (l / 16) + i]
+        // 2^-eS (eS = kZeroState while the state is zero; every consumer wave
+        // forms the same eS, and the producers the same sequence)
         f32x4 Sr[4];
+        int eS = kZeroState;
         // C row `own` of the next two chunks: chunk k in cr[(k - kbeg) & 1],
         // loaded two chunks ahead
         float4 cr[2][4];
@@ -420,6 +445,24 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     }
                 }
             }
+            if (s0_nonzero) {
+                // the entering state's largest magnitude over the four
+                // consumer waves sets its scale (one more barrier, matched by
+                // the producers, which read the same maxima)
+                float m = 0.f;
+    #pragma unroll
+                for (int pb = 0; pb < 4; ++pb)
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(Sr[pb][i]));
+                m = wave_max(m);
+                if (lane == 0) s_smax[W] = m;
+                lds_barrier();
+                eS = state_exp_of(s_smax);
+    #pragma unroll
+                for (int pb = 0; pb < 4; ++pb)
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i) Sr[pb][i] = __builtin_amdgcn_ldexpf(Sr[pb][i], -eS);
+            }
             if (!kStateOnly) {
                 write_T4(0);
                 c_load(kbeg, C0{});
@@ -446,13 +489,18 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             const int tv = (int)min((int64_t)T, prm.L - t0);
             const float cs_last = s_cs[s][T - 1];
             log_decay_sum += cs_last;
+            // scales: q by 2^-ek, the state leaving the chunk by 2^-eN, the
+            // chunk's products of y by 2^-eo
+            const int ek = s_tok.qexp[s], eN = s_tok.sexp[s];
+            const int eo = max(ek, eS - kMaxShift);
             if (kSave) {
                 // saved for the backward: the state entering chunk k
                 float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * PNS + n0;
+                const float f = __builtin_amdgcn_ldexpf(1.f, eS);
     #pragma unroll
                 for (int pb = 0; pb < 4; ++pb)
                     *(float4 *)(cst + (16 * pb + r16) * NS + 16 * W + 4 * kq) =
-                        make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
+                        make_float4(Sr[pb][0] * f, Sr[pb][1] * f, Sr[pb][2] * f, Sr[pb][3] * f);
             }
             const SplitTile t2 = T2(s), t3 = T3(s);
             f32x4 U[4];
@@ -469,6 +517,10 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 c_load(k + 2, slot_c);
                 const SplitTile t1 = T1(s), t4 = T4(s);
                 const float cs_own = s_cs[s][own];
+                // W in the output's scale 2^-eo: q 2^-ek times 2^(ek - eo), an
+                // exact shift of the exponent argument (0 unless the state
+                // outweighs the chunk by 2^kMaxShift)
+                const float cs_w = cs_own + (float)(ek - eo);
 
                 // W^T tiles: C_t . B_s exp2(cs_t - cs_s), s <= t, t = own
                 Frag WT[2];
@@ -484,7 +536,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const int so = 16 * j + 4 * kq + i;
-                            const float e = (j <= W && so <= own) ? exp2_f(cs_own - s_cs[s][so]) * s_q[s][so] : 0.f;
+                            const float e = (j <= W && so <= own) ? exp2_f(cs_w - s_cs[s][so]) * s_q[s][so] : 0.f;
                             wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
                         }
                     }
@@ -504,7 +556,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     WT[0] = pack_frag(wv[0]);
                     WT[1] = pack_frag(wv[1]);
                 }
-                // y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] q_s x_s
+                // 2^-eo y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] q_s x_s (S held
+                // as S 2^-eS, W built in the scale 2^-eo)
                 f32x4 acc[4];
     #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) {
@@ -513,7 +566,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     for (int ks = 0; ks < 2; ++ks)
                         acc[pb] = mma3f(frag(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
                 }
-                const float ecs = kSeq ? exp2_f(cs_own) * s_off[s][own] : exp2_f(cs_own);
+                const float ecs = __builtin_amdgcn_ldexpf(kSeq ? exp2_f(cs_own) * s_off[s][own] : exp2_f(cs_own),
+                                                          eS - eo);
     #pragma unroll
                 for (int pb = 0; pb < 4; ++pb)
     #pragma unroll
@@ -528,6 +582,13 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         if (2 * m <= W) acc[pb] = mma3f(f2, WT[m], acc[pb]);
                         U[pb] = mma3f(a3, f2, U[pb]);
                     }
+                }
+                {
+                    const float f = __builtin_amdgcn_ldexpf(1.f, eo);
+    #pragma unroll
+                    for (int pb = 0; pb < 4; ++pb)
+    #pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[pb][i] *= f;
                 }
                 if (kFull || own < tv) {
                     const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P;
@@ -568,12 +629,15 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag_tp_s<kXS>(t2, m, 16 * pb), U[pb]);
                     }
                 }
-                const float alpha = kSeq ? exp2_f(cs_last) * s_carry[s] : exp2_f(cs_last);
+                // S' 2^-eN = exp2(cs_last) 2^(eS - eN) (S 2^-eS) + U 2^-eN (T3's scale)
+                const float alpha = __builtin_amdgcn_ldexpf(kSeq ? exp2_f(cs_last) * s_carry[s] : exp2_f(cs_last),
+                                                            eS - eN);
                 if (kSeq) seg_carry *= s_carry[s];
     #pragma unroll
                 for (int pb = 0; pb < 4; ++pb)
     #pragma unroll
                     for (int i = 0; i < 4; ++i) Sr[pb][i] = alpha * Sr[pb][i] + U[pb][i];
+                eS = eN;
             }
             if (!kStateOnly) write_T4(s ^ 1);
             lds_barrier(); // buffer s is free, buffer s ^ 1 and T4(s ^ 1) are complete
@@ -602,10 +666,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             dst = prm.final_state + ((int64_t)b * H + h) * PNS + n0;
         }
         if (dst) {
+            const float f = __builtin_amdgcn_ldexpf(1.f, eS);
     #pragma unroll
             for (int pb = 0; pb < 4; ++pb)
                 *(float4 *)(dst + (16 * pb + r16) * NS + 16 * W + 4 * kq) =
-                    make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]);
+                    make_float4(Sr[pb][0] * f, Sr[pb][1] * f, Sr[pb][2] * f, Sr[pb][3] * f);
         }
     };
     switch (w) {

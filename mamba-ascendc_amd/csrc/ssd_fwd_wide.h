@@ -140,8 +140,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         float off[2][TS];
         float carry[2];
         int mixed[2];
+        int qexp[2]; // ek: q holds q 2^-ek
+        int sexp[2]; // eN: T3 holds x dec q 2^-eN, the scale of the state leaving the chunk
     };
     __shared__ __attribute__((aligned(16))) ChunkTok s_tok;
+    __shared__ __attribute__((aligned(16))) float s_smax[4]; // |entering state| maximum per consumer wave
     auto &s_cs = s_tok.cs, &s_q = s_tok.q;
     auto &s_sid = s_tok.sid;
     auto &s_off = s_tok.off;
@@ -177,6 +180,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
     const int brow = pt >> 5, cb = (pt & 31) * 4;  // B: 32 threads per 128-column row
     float4 xr[kDepth][2], br[kDepth][8];
     float dtr[kDepth];
+    int p_eS = kZeroState; // exponent of the state entering the chunk being staged
     int sidr[kDepth], sprv[kDepth];
     const int rowHP4 = (int)((int64_t)H * P * 4), rowGN4 = (int)((int64_t)G * NS * 4); // token strides, bytes
     const int hr = h / prm.hdiv, Hr = H / prm.hdiv;
@@ -205,19 +209,19 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
     auto p_stage = [&](int k, int s, auto slot_c) {
         constexpr int sl = decltype(slot_c)::value;
         const int tv = (int)min((int64_t)T, prm.L - (int64_t)k * T);
-        float q = 0.f, a = 0.f;
-        if (lane < tv) {
-            q = discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
-            a = Ah2 * q;
-        }
-        const float cs = wave_inclusive_scan(a);
+        float q = 0.f;
+        if (lane < tv) q = discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
+        const float sq = wave_inclusive_scan(q); // prefix sums of q
+        const float cs = Ah2 * sq;               // log2 units
         const float cs_last = readlane_f(cs, T - 1);
+        const int ek = chunk_q_exp(readlane_f(sq, T - 1));
         ChunkTok *tk = opaque_lds_t(&s_tok);
         if (w == 0) {
             tk->cs[s][lane] = cs;
-            tk->q[s][lane] = q;
+            tk->q[s][lane] = __builtin_amdgcn_ldexpf(q, -ek);
         }
         float dec = exp2_f(cs_last - cs);
+        bool cut = false; // kSeq: the state does not carry over the chunk
         if (kSeq) {
             const int sid = sidr[sl], e_end = __shfl(sid, T - 1, kWave), e_prev = sprv[sl];
             if (sid != e_end || e_end < 0) dec = 0.f;
@@ -230,13 +234,23 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
                     tk->mixed[s] = mixed ? 1 : 0;
                 }
             }
+            cut = e_end != e_prev;
         }
+        // the state leaving the chunk is S 2^-eN (every producer wave runs
+        // the same recurrence as the consumers' eS)
+        const int eN = next_state_exp(p_eS, ek, cs_last, cut);
+        p_eS = eN;
+        if (w == 0 && lane == 0) {
+            tk->qexp[s] = ek;
+            tk->sexp[s] = eN;
+        }
+        const float qn = __builtin_amdgcn_ldexpf(q, -eN);
         _Float16 *lp = opaque_lds(lds);
         const SplitTile t1 = T1(lp, s), t2 = T2(lp, s), t3 = T3(lp, s);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int row = xrow + 32 * j;
-            const float dr = __shfl(dec * q, row, kWave);
+            const float dr = __shfl(dec * qn, row, kWave);
             const float4 xv = xr[sl][j];
             store_split4(t2, row * kS2 + cx, xv);
             store_split4(t3, row * kS2 + cx, make_float4(xv.x * dr, xv.y * dr, xv.z * dr, xv.w * dr));
@@ -249,10 +263,17 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
     static_assert(kDepth == 3, "the unrolled ring below assumes three slots");
+    // the entering state can be nonzero: its magnitude sets its first scale,
+    // through one more barrier in both roles (wave-uniform)
+    const bool s0_nonzero = sp.seg_in != nullptr || prm.init != nullptr;
     if (producer) {
         p_load(kbeg, S0{});
         p_load(kbeg + 1, S1{});
         p_load(kbeg + 2, S2{});
+        if (s0_nonzero) {
+            lds_barrier(); // the consumers' maxima of the entering state
+            p_eS = state_exp_of(s_smax);
+        }
         p_stage(kbeg, 0, S0{});
         p_load(kbeg + 3, S0{});
         lds_barrier();
@@ -278,7 +299,10 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         constexpr int W = decltype(wave_c)::value;
         const int own = 16 * W + r16; // token row of this lane
         // Sr[c][pb][i] = S[p0 + 16 pb + l % 16][n = 16 (W + 4 c) + 4 (l / 16) + i]
+        // 2^-eS (eS = kZeroState while the state is zero; every consumer wave
+        // forms the same eS, and the producers the same sequence)
         f32x4 Sr[2][2];
+        int eS = kZeroState;
         // C row `own` of the next chunk (128 columns: k-steps ks = 0..3, each
         // 8 (l / 16) + 0..7 of its 32 columns), loaded one chunk ahead; past
         // the segment end an empty-range read
@@ -355,6 +379,28 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
                         }
                     }
             }
+            if (s0_nonzero) {
+                // the entering state's largest magnitude over the four
+                // consumer waves sets its scale (one more barrier, matched by
+                // the producers, which read the same maxima)
+                float m = 0.f;
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(Sr[c][pb][i]));
+                m = wave_max(m);
+                if (lane == 0) s_smax[W] = m;
+                lds_barrier();
+                eS = state_exp_of(s_smax);
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) Sr[c][pb][i] = __builtin_amdgcn_ldexpf(Sr[c][pb][i], -eS);
+            }
             write_T4(0);
             c_load(kbeg);
             cb_load(kbeg);
@@ -372,14 +418,19 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             const int64_t t0 = (int64_t)k * T;
             const int tv = (int)min((int64_t)T, prm.L - t0);
             const float cs_last = s_cs[s][T - 1];
+            // scales: q by 2^-ek, the state leaving the chunk by 2^-eN, the
+            // chunk's products of y by 2^-eo
+            const int ek = s_tok.qexp[s], eN = s_tok.sexp[s];
+            const int eo = max(ek, eS - kMaxShift);
             if (kSave) {
                 float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * PNS;
+                const float f = __builtin_amdgcn_ldexpf(1.f, eS);
 #pragma unroll
                 for (int c = 0; c < 2; ++c)
 #pragma unroll
                     for (int pb = 0; pb < 2; ++pb)
                         *(float4 *)(cst + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq) =
-                            make_float4(Sr[c][pb][0], Sr[c][pb][1], Sr[c][pb][2], Sr[c][pb][3]);
+                            make_float4(Sr[c][pb][0] * f, Sr[c][pb][1] * f, Sr[c][pb][2] * f, Sr[c][pb][3] * f);
             }
             Frag Cown[4];
 #pragma unroll
@@ -396,6 +447,10 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             _Float16 *la = opaque_lds(lds);
             const SplitTile t1 = T1(la, s), t4 = T4(la, s);
             const float cs_own = s_cs[s][own];
+            // W in the output's scale 2^-eo: q 2^-ek times 2^(ek - eo), an exact
+            // shift of the exponent argument (0 unless the state outweighs the
+            // chunk by 2^kMaxShift)
+            const float cs_w = cs_own + (float)(ek - eo);
 
             // W^T tiles: C_t . B_s exp2(cs_t - cs_s) q_s, s <= t, t = own
             Frag WT[2];
@@ -414,7 +469,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int so = 16 * j + 4 * kq + i;
-                        const float e = (j <= W && so <= own) ? exp2_f(cs_own - s_cs[s][so]) * s_q[s][so] : 0.f;
+                        const float e = (j <= W && so <= own) ? exp2_f(cs_w - s_cs[s][so]) * s_q[s][so] : 0.f;
                         wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
                     }
                 }
@@ -432,7 +487,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
                 WT[0] = pack_frag(wv[0]);
                 WT[1] = pack_frag(wv[1]);
             }
-            // y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] q_s x_s, p in this half
+            // 2^-eo y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] q_s x_s, p in this
+            // half (S held as S 2^-eS, W built in the scale 2^-eo)
             f32x4 acc[2];
 #pragma unroll
             for (int pb = 0; pb < 2; ++pb) {
@@ -440,7 +496,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) acc[pb] = mma3f(frag_s<kS1>(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
             }
-            const float ecs = kSeq ? exp2_f(cs_own) * s_off[s][own] : exp2_f(cs_own);
+            const float ecs = __builtin_amdgcn_ldexpf(kSeq ? exp2_f(cs_own) * s_off[s][own] : exp2_f(cs_own),
+                                                      eS - eo);
 #pragma unroll
             for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
@@ -453,6 +510,13 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
 #pragma unroll
                     for (int pb = 0; pb < 2; ++pb)
                         acc[pb] = mma3f(frag_tp_s<kS2>(t2, m, 16 * pb), WT[m], acc[pb]);
+            }
+            {
+                const float f = __builtin_amdgcn_ldexpf(1.f, eo);
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[pb][i] *= f;
             }
             if (kFull || own < tv) {
                 const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P + p0;
@@ -498,13 +562,16 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
                     for (int pb = 0; pb < 2; ++pb) U[c][pb] = mma3f(a1, f3[pb], U[c][pb]);
                 }
             }
-            const float alpha = kSeq ? exp2_f(cs_last) * s_carry[s] : exp2_f(cs_last);
+            // S' 2^-eN = exp2(cs_last) 2^(eS - eN) (S 2^-eS) + U 2^-eN (T3's scale)
+            const float alpha = __builtin_amdgcn_ldexpf(kSeq ? exp2_f(cs_last) * s_carry[s] : exp2_f(cs_last),
+                                                        eS - eN);
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
                 for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) Sr[c][pb][i] = alpha * Sr[c][pb][i] + U[c][pb][i];
+            eS = eN;
             write_T4(s ^ 1);
             lds_barrier(); // buffer s is free, buffer s ^ 1 and T4(s ^ 1) are complete
         };
@@ -515,12 +582,13 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
 
         if (sp.write_final && sg == sp.nseg - 1 && prm.final_state) {
             float *dst = prm.final_state + ((int64_t)b * H + h) * PNS;
+            const float f = __builtin_amdgcn_ldexpf(1.f, eS);
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
                 for (int pb = 0; pb < 2; ++pb)
                     *(float4 *)(dst + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq) =
-                        make_float4(Sr[c][pb][0], Sr[c][pb][1], Sr[c][pb][2], Sr[c][pb][3]);
+                        make_float4(Sr[c][pb][0] * f, Sr[c][pb][1] * f, Sr[c][pb][2] * f, Sr[c][pb][3] * f);
         }
     };
     switch (w) {
