@@ -517,10 +517,18 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
                 xa[pb] = tile_row4(tile_at(le, par), own, 16 * pb + cq);
-                ga[pb] = tile_row4(tile_at(le, 2 + par), own, 16 * pb + cq);
-                // s_D holds D per channel (a scalar D repeated, 0 without D)
-                const float4 d4 = *(const float4 *)&s_D[par][16 * pb + cq];
-                Dv[pb] = f32x4{d4.x, d4.y, d4.z, d4.w};
+                ga[pb] = zero4();
+                Dv[pb] = zero4();
+            }
+            if (prm.has_D) {
+                // D gy joins dx (wave-uniform: without D neither is read)
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) {
+                    ga[pb] = tile_row4(tile_at(le, 2 + par), own, 16 * pb + cq);
+                    // s_D holds D per channel (a scalar D repeated)
+                    const float4 d4 = *(const float4 *)&s_D[par][16 * pb + cq];
+                    Dv[pb] = f32x4{d4.x, d4.y, d4.z, d4.w};
+                }
             }
             // da of token own: through this wave's LDS row (written and read
             // back by the same wave, so no barrier)
