@@ -486,6 +486,9 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         const int cq = 4 * kq;        // first of its 4 channels in each 16-channel block
         // dxa[pb][i] = dxdt[own][16 pb + cq + i]; dBa, dCa likewise over n
         f32x4 dBa[4], dCa[4], dxa[4];
+        // x[own][16 pb + cq + i] of the step, read in phase B and kept for the
+        // step's epilogue (at the start of the next step)
+        f32x4 xk[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             dBa[i] = zero4();
@@ -516,7 +519,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             __bf16 *le = opaque_lds_t(lds);
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
-                xa[pb] = tile_row4(tile_at(le, par), own, 16 * pb + cq);
+                xa[pb] = xk[pb];
                 ga[pb] = zero4();
                 Dv[pb] = zero4();
             }
@@ -724,11 +727,11 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                     f32x4 rm = zero4();
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) rm = mma3f(frag(Ut, 16 * pb + r16, ks), Bo[ks], rm);
-                    const f32x4 xv = tile_row4(xb, own, 16 * pb + cq);
+                    xk[pb] = tile_row4(xb, own, 16 * pb + cq);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         dxa[pb][i] += dte_o * rm[i];
-                        rpart += xv[i] * rm[i];
+                        rpart += xk[pb][i] * rm[i];
                     }
                 }
             }
