@@ -55,17 +55,25 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 // result equals converting that difference, in half the instructions of
 // convert-back, subtract and convert.  The compiler does not form these
 // itself, and it cannot see the register writes inside an asm block when it
-// spaces dependent instructions, so the block ends with the two wait states
+// spaces dependent instructions: kMfma ends the block with the two wait states
 // an MFMA reading a VALU result needs (the s_nop 1 the compiler puts between
-// its own conversions and such an MFMA).
+// its own conversions and such an MFMA), for operands packed straight into an
+// MFMA; values bound for LDS need none.
+template <bool kMfma = false>
 __device__ __forceinline__ void split2(float a, float b, half2v &hi, half2v &lo) {
     const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
     uint32_t l;
-    asm("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
-        "v_fma_mixhi_f16 %0, -%1, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-        "s_nop 1"
-        : "=&v"(l)
-        : "v"(h), "v"(a), "v"(b));
+    if (kMfma)
+        asm("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mixhi_f16 %0, -%1, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "s_nop 1"
+            : "=&v"(l)
+            : "v"(h), "v"(a), "v"(b));
+    else
+        asm("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mixhi_f16 %0, -%1, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "=&v"(l)
+            : "v"(h), "v"(a), "v"(b));
     hi = __builtin_bit_cast(half2v, h);
     lo = __builtin_bit_cast(half2v, l);
 }
@@ -331,7 +339,7 @@ __device__ __forceinline__ Frag pack_frag(const float (&v)[8]) {
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
         half2v h, l;
-        split2(v[i], v[i + 1], h, l);
+        split2<true>(v[i], v[i + 1], h, l);
         f.h[i] = h[0];
         f.h[i + 1] = h[1];
         f.l[i] = l[0];
@@ -406,8 +414,8 @@ __device__ __forceinline__ Frag frag_tp(SplitTile s, int m, int c0) { return fra
 
 // fp32 hi + lo of four split values: one mixed-precision FMA each
 // (hi * 1 + lo with both fp16 operands widened, exact, rounded once to fp32),
-// instead of two conversions and an add.  The block ends with the wait states
-// an MFMA reading a VALU result needs, as split2 does.
+// instead of two conversions and an add.  Its results feed VALU arithmetic
+// only (an MFMA or DPP reader would need the wait states split2<true> adds).
 __device__ __forceinline__ f32x4 join4(half4 h, half4 l) {
     typedef uint32_t u2 __attribute__((ext_vector_type(2)));
     const u2 hb = __builtin_bit_cast(u2, h), lb = __builtin_bit_cast(u2, l);
@@ -415,8 +423,7 @@ __device__ __forceinline__ f32x4 join4(half4 h, half4 l) {
     asm("v_fma_mix_f32 %0, %4, 1.0, %6 op_sel_hi:[1,0,1]\n\t"
         "v_fma_mix_f32 %1, %4, 1.0, %6 op_sel:[1,0,1] op_sel_hi:[1,0,1]\n\t"
         "v_fma_mix_f32 %2, %5, 1.0, %7 op_sel_hi:[1,0,1]\n\t"
-        "v_fma_mix_f32 %3, %5, 1.0, %7 op_sel:[1,0,1] op_sel_hi:[1,0,1]\n\t"
-        "s_nop 1"
+        "v_fma_mix_f32 %3, %5, 1.0, %7 op_sel:[1,0,1] op_sel_hi:[1,0,1]"
         : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d)
         : "v"(hb[0]), "v"(hb[1]), "v"(lb[0]), "v"(lb[1]));
     return f32x4{a, b, c, d};
