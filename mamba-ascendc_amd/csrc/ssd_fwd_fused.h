@@ -230,7 +230,14 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     int p_eS = kZeroState; // exponent of the state entering the chunk being staged
     int sidr[kDepth], sprv[kDepth]; // kSeq: id of token `lane`, id of the token before the chunk
     const int rowHP4 = (int)(rowHP * 4), rowGN4 = (int)(rowGN * 4); // token strides, bytes
+    int xrow_off[4], brow_off[4]; // byte offsets of rows rt + 16 j
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        xrow_off[j] = (rt + 16 * j) * rowHP4;
+        brow_off[j] = (rt + 16 * j) * rowGN4;
+    }
     const int hr = h / prm.hdiv, Hr = H / prm.hdiv;                      // the real head
+    const int dt_off = lane * Hr * 4;                                    // dt of token `lane`, bytes
     const float Ah2 = prm.A[hr] * kLog2e;                                // A in log2 units
     const float bias = prm.dt_bias ? prm.dt_bias[hr] : 0.f;
     // Loads are issued unconditionally, so the wait counts the compiler
@@ -245,13 +252,17 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         const int range = real ? 0x7fffffff : 0;
         const auto rx = buf_rsrc_n(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P, range);
         const auto rb = buf_rsrc_n(prm.B + (((int64_t)b * prm.L + t0) * G + g) * NS + n0, range);
+        // row offsets clamped to the last valid row: min of the lane's
+        // precomputed offsets and the chunk's last-row offset (no per-chunk
+        // multiplies)
+        const int xlast = (tv - 1) * rowHP4, blast = (tv - 1) * rowGN4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int row = min(rt + 16 * j, tv - 1);
-            xr[sl][j] = buf_load4(rx, row * rowHP4 + c4 * 4, 0);
-            br[sl][j] = buf_load4(rb, row * rowGN4 + c4 * 4, 0);
+            xr[sl][j] = buf_load4(rx, min(xrow_off[j], xlast) + c4 * 4, 0);
+            br[sl][j] = buf_load4(rb, min(brow_off[j], blast) + c4 * 4, 0);
         }
-        dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * Hr + hr];
+        const auto rdt = buf_rsrc(prm.dt + ((int64_t)b * prm.L + t0) * Hr + hr);
+        dtr[sl] = buf_load(rdt, min(dt_off, (tv - 1) * Hr * 4), 0);
         if (kSeq) {
             const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + t0;
             sidr[sl] = si[min(lane, tv - 1)];

@@ -184,6 +184,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
     int sidr[kDepth], sprv[kDepth];
     const int rowHP4 = (int)((int64_t)H * P * 4), rowGN4 = (int)((int64_t)G * NS * 4); // token strides, bytes
     const int hr = h / prm.hdiv, Hr = H / prm.hdiv;
+    const int xrow_off = xrow * rowHP4, brow_off = brow * rowGN4; // bytes
+    const int dt_off = lane * Hr * 4;                             // dt of token `lane`, bytes
     const float Ah2 = prm.A[hr] * kLog2e;
     const float bias = prm.dt_bias ? prm.dt_bias[hr] : 0.f;
     auto p_load = [&](int k, auto slot_c) {
@@ -194,11 +196,15 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         const int range = real ? 0x7fffffff : 0;
         const auto rx = buf_rsrc_n(prm.x + (((int64_t)b * prm.L + t0) * H + h) * P + p0, range);
         const auto rb = buf_rsrc_n(prm.B + (((int64_t)b * prm.L + t0) * G + g) * NS, range);
+        // row offsets clamped to the last valid row: min of the lane's
+        // precomputed offsets and the chunk's last-row offset
+        const int xlast = (tv - 1) * rowHP4, blast = (tv - 1) * rowGN4;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) xr[sl][j] = buf_load4(rx, min(xrow + 32 * j, tv - 1) * rowHP4 + cx * 4, 0);
+        for (int j = 0; j < 2; ++j) xr[sl][j] = buf_load4(rx, min(xrow_off + 32 * j * rowHP4, xlast) + cx * 4, 0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) br[sl][j] = buf_load4(rb, min(brow + 8 * j, tv - 1) * rowGN4 + cb * 4, 0);
-        dtr[sl] = prm.dt[((int64_t)b * prm.L + t0 + min(lane, tv - 1)) * Hr + hr];
+        for (int j = 0; j < 8; ++j) br[sl][j] = buf_load4(rb, min(brow_off + 8 * j * rowGN4, blast) + cb * 4, 0);
+        const auto rdt = buf_rsrc(prm.dt + ((int64_t)b * prm.L + t0) * Hr + hr);
+        dtr[sl] = buf_load(rdt, min(dt_off, (tv - 1) * Hr * 4), 0);
         if (kSeq) {
             const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + t0;
             sidr[sl] = si[min(lane, tv - 1)];
