@@ -85,15 +85,21 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     // Per-token (and per-channel D) values of a step written by the dt
     // prologue, double buffered by step parity; one struct, so the writing
     // wave addresses every member from one base (see the prologue).
+    // bT[t] = exp2(cs of the last token of t's 16-token block - cs_t) and
+    // bS[t] = exp2(cs_t - cs of the first token of its block): the decay
+    // masks of phase A's off-diagonal blocks factor through block bounds,
+    // one exp2 per block and lane instead of one per element (both factors
+    // have the sign of the whole exponent, so neither overflows where the
+    // product does not)
     struct StepTok {
-        float q[2][T], cs[2][T], dqdu[2][T], dte[2][T], ecs[2][T], D[2][P];
+        float q[2][T], cs[2][T], dqdu[2][T], dte[2][T], ecs[2][T], bT[2][T], bS[2][T], D[2][P];
         int sid[2][TS];  // kSeq: token ids
         float carry[2];  // kSeq: 1 where the state carries over
         float A[2];
     };
     __shared__ __attribute__((aligned(32))) StepTok s_tok;
     auto &s_q = s_tok.q, &s_cs = s_tok.cs, &s_dqdu = s_tok.dqdu, &s_dte = s_tok.dte, &s_ecs = s_tok.ecs,
-         &s_D = s_tok.D;
+         &s_D = s_tok.D, &s_bT = s_tok.bT, &s_bS = s_tok.bS;
     auto &s_sid = s_tok.sid;
     auto &s_carry = s_tok.carry, &s_A = s_tok.A;
     __shared__ __attribute__((aligned(32))) float s_dcs[2][T], s_rd[2][T];
@@ -310,6 +316,8 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 tk->dqdu[par][lane] = dq;
                 tk->dte[par][lane] = exp2_f(last - cs) * into;
                 tk->ecs[par][lane] = exp2_f(cs) * reads;
+                tk->bT[par][lane] = exp2_f(__shfl(cs, lane | 15, kWave) - cs);
+                tk->bS[par][lane] = exp2_f(cs - __shfl(cs, lane & ~15, kWave));
                 tk->D[par][lane] = prm.has_D ? Dr : 0.f;
                 if (lane == 0) tk->A[par] = Ahr;
             }
@@ -585,7 +593,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             const SplitTile Bt = tile_at(la, 6), Ct = tile_at(la, 7);
 
             // ---------------- phase A: x, gy, B, C
-            const float *q_ = s_q[par], *cs_ = s_cs[par];
+            const float *q_ = s_q[par], *cs_ = s_cs[par], *bT_ = s_bT[par], *bS_ = s_bS[par];
             Frag Bo[2];
             f32x4 ca[4];
             {
@@ -618,7 +626,10 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 #pragma unroll
                             for (int ks = 0; ks < 2; ++ks) dw = mma3f(frag(xt, 16 * j + r16, ks), Go[ks], dw);
                             const float4 qv = *(const float4 *)&q_[16 * j + 4 * kq];
-                            const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
+                            // exp2(cs_own - cs_s): per element on the diagonal block,
+                            // else exp2(cs_own - cs_end(j)) bT[s]
+                            const float4 cv = *(const float4 *)&(j < W ? bT_ : cs_)[16 * j + 4 * kq];
+                            const float aj = j < W ? exp2_f(cs_own - cs_[16 * j + 15]) : 0.f;
                             const float qa[4] = {qv.x, qv.y, qv.z, qv.w}, cva[4] = {cv.x, cv.y, cv.z, cv.w};
                             int sva[4] = {0, 0, 0, 0};
                             if (kSeq) {
@@ -628,7 +639,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 const bool in = (j < W || 4 * kq + i <= r16) && (!kSeq || sva[i] == sid_own);
-                                const float e = in ? exp2_f(cs_own - cva[i]) : 0.f;
+                                const float e = in ? (j < W ? aj * cva[i] : exp2_f(cs_own - cva[i])) : 0.f;
                                 const float dwv = dw[i] * qa[i];
                                 rows += dwv * cb[i] * e;
                                 dct[j >> 1][(j & 1) * 4 + i] = dwv * e;
@@ -657,7 +668,10 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                             const f32x4 cb = cbS[j];
 #pragma unroll
                             for (int ks = 0; ks < 2; ++ks) dw = mma3f(frag(gt, 16 * j + r16, ks), Xo[ks], dw);
-                            const float4 cv = *(const float4 *)&cs_[16 * j + 4 * kq];
+                            // exp2(cs_t - cs_own): per element on the diagonal block,
+                            // else exp2(cs_start(j) - cs_own) bS[t]
+                            const float4 cv = *(const float4 *)&(j > W ? bS_ : cs_)[16 * j + 4 * kq];
+                            const float aj = j > W ? exp2_f(cs_[16 * j] - cs_own) : 0.f;
                             const float cva[4] = {cv.x, cv.y, cv.z, cv.w};
                             int sva[4] = {0, 0, 0, 0};
                             if (kSeq) {
@@ -667,7 +681,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 const bool in = (j > W || r16 <= 4 * kq + i) && (!kSeq || sva[i] == sid_own);
-                                const float e = in ? exp2_f(cva[i] - cs_own) : 0.f;
+                                const float e = in ? (j > W ? aj * cva[i] : exp2_f(cva[i] - cs_own)) : 0.f;
                                 const float dwv = dw[i] * q_own, wsv = cb[i] * e;
                                 cols += dwv * wsv;
                                 ws[j >> 1][(j & 1) * 4 + i] = wsv;
