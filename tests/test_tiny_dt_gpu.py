@@ -93,13 +93,17 @@ def test_tiny_q_with_initial_states_and_features(shape):
 
 
 @pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[1], SHAPES[3]], ids=["one-seg", "segments", "n128"])
-@pytest.mark.parametrize("order", ["drop", "rise"])
-def test_q_jumps_inside_the_sequence(shape, order):
-    """q of ~1 on one half of every sequence and ~2e-9 on the other, with a
-    strongly decaying head among slow ones, so the state is carried across the
-    jump (drop: large-q history under tiny-q chunks; rise: the reverse)."""
+@pytest.mark.parametrize("order,offset", [("drop", -20.0), ("rise", -20.0), ("drop", -45.0)],
+                         ids=["drop", "rise", "deep-drop"])
+def test_q_jumps_inside_the_sequence(shape, order, offset):
+    """q of ~1 on one half of every sequence and ~2e-9 (offset -20) or ~3e-20
+    (-45) on the other, with a strongly decaying head among slow ones, so the
+    state is carried across the jump (drop: large-q history under tiny-q
+    chunks; rise: the reverse).  The deep drop puts the state more than 2^60
+    above the chunk's own terms, the case where W is formed in the state's
+    scale."""
     _need_gpu()
-    _say(f"q jump {order} {shape}")
+    _say(f"q jump {order} {offset} {shape}")
     inp = make_inputs(shape, seed=13)
     L = shape[1]
     tiny = torch.zeros(L, dtype=torch.bool)
@@ -107,7 +111,7 @@ def test_q_jumps_inside_the_sequence(shape, order):
         tiny[L // 2 + 7:] = True
     else:
         tiny[: L // 2 + 7] = True
-    inp["dt"] = torch.where(tiny[None, :, None], inp["dt"] - 20.0, inp["dt"])
+    inp["dt"] = torch.where(tiny[None, :, None], inp["dt"] + offset, inp["dt"])
     inp["A"][0] = -8.0
     _check(inp, shape[5], order)
 
