@@ -242,8 +242,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             }
             cut = e_end != e_prev;
         }
-        // the state leaving the chunk is S 2^-eN (every producer wave runs
-        // the same recurrence as the consumers' eS)
+        // the state leaving the chunk is held as S 2^-eN: every producer wave
+        // runs this recurrence, and the consumers take eN from LDS
         const int eN = next_state_exp(p_eS, ek, cs_last, cut);
         p_eS = eN;
         if (w == 0 && lane == 0) {
