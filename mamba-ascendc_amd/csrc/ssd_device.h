@@ -232,6 +232,22 @@ __device__ __forceinline__ int chunk_q_exp(float q_sum) { return max(scale_exp(q
 __device__ __forceinline__ int next_state_exp(int eS, int ek, float cs_last, bool cut) {
     return cut ? ek : min(max(ek, eS + (int)floorf(fmaxf(cs_last, -512.f))), 126);
 }
+// Packed sequences: a chunk that holds several ids scales each id's tokens
+// by its own sum (the sequences need not share a magnitude of q), so every
+// token of one id gets the same exponent, chunk_q_exp of the q sum over the
+// chunk's tokens of that id.  One pass per distinct id (wave-uniform).
+__device__ __forceinline__ int id_q_exp(int sid, float q) {
+    int e = 0;
+    uint64_t left = ~0ull;
+    while (left) {
+        const int id = __builtin_amdgcn_readlane(sid, __builtin_ctzll(left));
+        const bool mine = sid == id;
+        const float sum = wave_sum(mine ? q : 0.f);
+        if (mine) e = chunk_q_exp(sum);
+        left &= ~__ballot(mine);
+    }
+    return e;
+}
 
 // Exponent of a state known to be zero (any scale holds it exactly; far
 // below every exponent the rules above produce).

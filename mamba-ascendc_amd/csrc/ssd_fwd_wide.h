@@ -141,6 +141,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         float carry[2];
         int mixed[2];
         int qexp[2]; // ek: q holds q 2^-ek
+        int qe[2][TS]; // kSeq: q of token t holds q 2^-qe[t] (ek of its id)
         int sexp[2]; // eN: T3 holds x dec q 2^-eN, the scale of the state leaving the chunk
     };
     __shared__ __attribute__((aligned(16))) ChunkTok s_tok;
@@ -220,21 +221,24 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         const float sq = wave_inclusive_scan(q); // prefix sums of q
         const float cs = Ah2 * sq;               // log2 units
         const float cs_last = readlane_f(cs, T - 1);
-        const int ek = chunk_q_exp(readlane_f(sq, T - 1));
+        int ek = chunk_q_exp(readlane_f(sq, T - 1)); // kSeq: that of the id leaving the chunk
+        int ek_tok = ek; // exponent of the token's q (kSeq: that of its id)
         ChunkTok *tk = opaque_lds_t(&s_tok);
-        if (w == 0) {
-            tk->cs[s][lane] = cs;
-            tk->q[s][lane] = __builtin_amdgcn_ldexpf(q, -ek);
-        }
+        if (w == 0) tk->cs[s][lane] = cs;
         float dec = exp2_f(cs_last - cs);
         bool cut = false; // kSeq: the state does not carry over the chunk
         if (kSeq) {
             const int sid = sidr[sl], e_end = __shfl(sid, T - 1, kWave), e_prev = sprv[sl];
             if (sid != e_end || e_end < 0) dec = 0.f;
             const bool mixed = __ballot(sid != e_end) != 0;
+            if (mixed) { // wave-uniform
+                ek_tok = id_q_exp(sid, q);
+                ek = __builtin_amdgcn_readlane(ek_tok, T - 1);
+            }
             if (w == 0) {
                 tk->sid[s][lane] = sid;
                 tk->off[s][lane] = sid == e_prev ? 1.f : 0.f;
+                tk->qe[s][lane] = ek_tok;
                 if (lane == 0) {
                     tk->carry[s] = e_end == e_prev ? 1.f : 0.f;
                     tk->mixed[s] = mixed ? 1 : 0;
@@ -242,6 +246,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             }
             cut = e_end != e_prev;
         }
+        if (w == 0) tk->q[s][lane] = __builtin_amdgcn_ldexpf(q, -ek_tok);
         // the state leaving the chunk is held as S 2^-eN: every producer wave
         // runs this recurrence, and the consumers take eN from LDS
         const int eN = next_state_exp(p_eS, ek, cs_last, cut);
@@ -426,8 +431,12 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             const float cs_last = s_cs[s][T - 1];
             // scales: q by 2^-ek, the state leaving the chunk by 2^-eN, the
             // chunk's products of y by 2^-eo
-            const int ek = s_tok.qexp[s], eN = s_tok.sexp[s];
-            const int eo = max(ek, eS - kMaxShift);
+            const int eN = s_tok.sexp[s];
+            // kSeq: the exponents of the lane's own row; a row that does not
+            // read the entering state takes no part of its scale
+            const int ek = kSeq ? s_tok.qe[s][own] : s_tok.qexp[s];
+            int eo = max(ek, eS - kMaxShift);
+            if (kSeq && s_off[s][own] == 0.f) eo = ek;
             if (kSave) {
                 float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * PNS;
                 const float f = __builtin_amdgcn_ldexpf(1.f, eS);

@@ -156,3 +156,39 @@ def test_backward_with_tiny_q(shape):
         _say(f"  d{k:<15} maxabs {ma:.3e} relL2 {rl:.3e}")
         assert torch.isfinite(got[k]).all(), k
         assert rl <= 2e-4, (k, rl)
+
+
+@pytest.mark.parametrize("shape", [[2, 640, 8, 64, 64, 64, 2], [1, 640, 4, 64, 128, 64, 1]], ids=["n64", "n128"])
+def test_packed_sequences_alternating_tiny_q(shape):
+    """Packed sequences whose q alternates between ~1 and ~2e-9 from one
+    sequence to the next: where a sequence cuts the state its scale restarts
+    from that chunk's q, so a tiny-q sequence after a large-q one keeps full
+    relative precision.  Checked per sequence (a global rel-L2 would be
+    dominated by the large-q sequences)."""
+    import ascend_kernel
+
+    _need_gpu()
+    _say(f"packed tiny q {shape}")
+    inp = make_inputs(shape, seed=15)
+    b, l = shape[0], shape[1]
+    bounds = [0, 150, 290, 300, 470, l]  # sequences of 150, 140, 10, 170, 170 tokens
+    ids = torch.zeros(b, l, dtype=torch.int32)
+    for i in range(len(bounds) - 1):
+        ids[:, bounds[i]:bounds[i + 1]] = i
+        if i % 2 == 1:
+            inp["dt"][:, bounds[i]:bounds[i + 1]] -= 20.0
+    dev = {k: v.cuda() for k, v in inp.items()}
+    out, fin = ascend_kernel.mamba2_ssd_fwd(dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"], shape[5],
+                                            dt_softplus=True, return_final_state=True, seq_idx=ids.cuda())
+    torch.cuda.synchronize()
+    ref, ref_fin = ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], shape[5],
+                                      dt_softplus=True, return_final_state=True, seq_idx=ids)
+    out = out.cpu()
+    for i in range(len(bounds) - 1):
+        sl = slice(bounds[i], bounds[i + 1])
+        ma, rl = parity_metrics(out[:, sl], ref[:, sl])
+        _say(f"  sequence {i} ({'tiny' if i % 2 else 'normal'} q): |y| max "
+             f"{float(ref[:, sl].abs().max()):.2e} rel {rl:.2e} maxabs {ma:.2e}")
+        assert rl <= RELL2, (i, rl)
+    _, frl = parity_metrics(fin.cpu(), ref_fin)
+    assert frl <= RELL2, frl
