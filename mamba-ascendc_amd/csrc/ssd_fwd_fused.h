@@ -325,10 +325,16 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         }
         const float qn = __builtin_amdgcn_ldexpf(q, -eN);
         const SplitTile t1 = T1(s), t2 = T2(s), t3 = T3(s);
+        // the four permutes issued back to back, ahead of every tile write:
+        // one wait for all of them instead of one each
+        float drs[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) drs[j] = __shfl(dec * qn, rt + 16 * j, kWave);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = rt + 16 * j;
-            const float dr = __shfl(dec * qn, row, kWave);
+            const float dr = drs[j];
             const float4 xv = xr[sl][j], bv = br[sl][j];
             put(t2, row, xv);
             put(t3, row, make_float4(bv.x * dr, bv.y * dr, bv.z * dr, bv.w * dr));

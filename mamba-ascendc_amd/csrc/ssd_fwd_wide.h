@@ -258,10 +258,15 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         const float qn = __builtin_amdgcn_ldexpf(q, -eN);
         _Float16 *lp = opaque_lds(lds);
         const SplitTile t1 = T1(lp, s), t2 = T2(lp, s), t3 = T3(lp, s);
+        // both permutes issued ahead of every tile write: one wait for both
+        float drs[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) drs[j] = __shfl(dec * qn, xrow + 32 * j, kWave);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int row = xrow + 32 * j;
-            const float dr = __shfl(dec * qn, row, kWave);
+            const float dr = drs[j];
             const float4 xv = xr[sl][j];
             store_split4(t2, row * kS2 + cx, xv);
             store_split4(t3, row * kS2 + cx, make_float4(xv.x * dr, xv.y * dr, xv.z * dr, xv.w * dr));
