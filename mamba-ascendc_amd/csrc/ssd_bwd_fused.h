@@ -106,10 +106,10 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     __shared__ __attribute__((aligned(32))) float s_sdu[2][4];
     __shared__ __attribute__((aligned(32))) float s_da[4][T]; // epilogue: da of a step, per consumer wave
 
-    auto Xt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, par); };
-    auto Gt = [&](int par) __attribute__((always_inline)) { return tile_at(lds, 2 + par); };
-    const SplitTile St = tile_at(lds, 4), Ut = tile_at(lds, 5), Bt = tile_at(lds, 6),
-                    Ct = tile_at(lds, 7);
+    // tiles: x(par) = 0 + par, gy(par) = 2 + par, S 4, dU 5, B 6, C 7 (the
+    // roles address them through copies of `lds` the optimizer cannot see
+    // through)
+    const SplitTile St = tile_at(lds, 4), Ut = tile_at(lds, 5);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int r16 = lane & 15, kq = lane >> 4;
