@@ -316,8 +316,10 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 tk->dqdu[par][lane] = dq;
                 tk->dte[par][lane] = exp2_f(last - cs) * into;
                 tk->ecs[par][lane] = exp2_f(cs) * reads;
-                tk->bT[par][lane] = exp2_f(__shfl(cs, lane | 15, kWave) - cs);
-                tk->bS[par][lane] = exp2_f(cs - __shfl(cs, lane & ~15, kWave));
+                // cs of the last and the first lane of the lane's 16-lane
+                // block: DPP row_newbcast 15 and 0 (no LDS round trip)
+                tk->bT[par][lane] = exp2_f(dpp_f<0x15F>(cs) - cs);
+                tk->bS[par][lane] = exp2_f(cs - dpp_f<0x150>(cs));
                 tk->D[par][lane] = prm.has_D ? Dr : 0.f;
                 if (lane == 0) tk->A[par] = Ahr;
             }
@@ -947,11 +949,17 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
             }
             const float ecs = exp2_f(cs) * reads;
             const SplitTile ge = GE(s), ct = CT(s);
+            // the four permutes issued back to back, ahead of every tile
+            // write: one wait for all of them instead of one each
+            float es[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) es[j] = __shfl(ecs, rt + 16 * j, kWave);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = rt + 16 * j;
                 const bool ok = row < tv;
-                const float e = __shfl(ecs, row, kWave);
+                const float e = es[j];
                 float4 v = (ok && has_dout) ? gr[sl][j] : z4;
                 if (kHasZ) {
                     v.x *= silu_f(zr[sl][j].x);
