@@ -235,10 +235,11 @@ __device__ __forceinline__ int next_state_exp(int eS, int ek, float cs_last, boo
 // Packed sequences: a chunk that holds several ids scales each id's tokens
 // by its own sum (the sequences need not share a magnitude of q), so every
 // token of one id gets the same exponent, chunk_q_exp of the q sum over the
-// chunk's tokens of that id.  One pass per distinct id (wave-uniform).
+// chunk's tokens of that id.  One pass per distinct id (wave-uniform); the
+// loop starts from the active lanes, so it ends whatever the exec mask.
 __device__ __forceinline__ int id_q_exp(int sid, float q) {
     int e = 0;
-    uint64_t left = ~0ull;
+    uint64_t left = __ballot(1);
     while (left) {
         const int id = __builtin_amdgcn_readlane(sid, __builtin_ctzll(left));
         const bool mine = sid == id;
