@@ -113,8 +113,17 @@ __global__ __launch_bounds__(256) void k_ssu(SsuParams prm) {
                 *(float4 *)sp = ns;
                 part = ns.x * cv.x + ns.y * cv.y + ns.z * cv.z + ns.w * cv.w;
             }
-            // sum over the lpr lanes of the row (aligned groups of a power of two)
-            for (int o = lpr >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+            // sum over the lpr lanes of the row (aligned groups of a power of two):
+            // a 16-lane row (N = 64) or two (N = 128) through DPP and the lane
+            // swap, other widths through LDS permutes
+            if (lpr == 16) {
+                part = sum16(part);
+            } else if (lpr == 32) {
+                part = sum16(part);
+                part += xor16_f(part);
+            } else {
+                for (int o = lpr >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+            }
             if (active && n0 == 0) {
                 float y = part;
                 if (prm.has_D) y += x * prm.D[h * prm.D_h + (prm.d_per_channel ? p * prm.D_p : 0)];
