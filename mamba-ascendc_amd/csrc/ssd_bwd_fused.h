@@ -305,7 +305,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 // and spilled, and each reload waited for the prefetches)
                 StepTok *tk = opaque_lds_t(&s_tok);
                 if (kSeq) {
-                    const int e_end = __shfl(sidr, T - 1, kWave); // rows past the end repeat the last id
+                    const int e_end = __builtin_amdgcn_readlane(sidr, T - 1); // rows past the end repeat the last id
                     into = (sidr == e_end && e_end >= 0) ? 1.f : 0.f;
                     reads = sidr == sprv ? 1.f : 0.f;
                     tk->sid[par][lane] = sidr;
@@ -934,7 +934,7 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
             const float cs_last = readlane_f(cs, T - 1);
             float reads = 1.f, carry = 1.f;
             if (kSeq) {
-                const int e_end = __shfl(sidr[sl], T - 1, kWave);
+                const int e_end = __builtin_amdgcn_readlane(sidr[sl], T - 1);
                 reads = sidr[sl] == sprv[sl] ? 1.f : 0.f;
                 carry = e_end == sprv[sl] ? 1.f : 0.f;
             }

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dstate(BwdParams prm) {
             const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + t0;
             const int sid = si[min(lane, tv - 1)];
             const int prev = k > 0 ? si[-1] : 0;
-            const int last = __shfl(sid, T - 1, 64);
+            const int last = __builtin_amdgcn_readlane(sid, T - 1);
             if (sid != prev) e = 0.f;
             if (last != prev) ld = -INFINITY;
         }

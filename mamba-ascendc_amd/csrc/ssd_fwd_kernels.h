@@ -79,7 +79,7 @@ __global__ __launch_bounds__(kThreads) void k_chunk_state(FwdParams prm) {
 
     if (wave == 0) {
         const float cs = chunk_prologue(prm, b, h, t0, tv, s_q, s_cs);
-        const float last = __shfl(cs, T - 1, 64);
+        const float last = readlane_f(cs, T - 1);
         s_w[lane] = s_q[lane] * __expf(last - cs);
         if (lane == 0) prm.chunk_log_decay[((int64_t)b * prm.H + h) * prm.K + k] = last;
     }

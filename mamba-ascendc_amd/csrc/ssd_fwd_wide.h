@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         float dec = exp2_f(cs_last - cs);
         bool cut = false; // kSeq: the state does not carry over the chunk
         if (kSeq) {
-            const int sid = sidr[sl], e_end = __shfl(sid, T - 1, kWave), e_prev = sprv[sl];
+            const int sid = sidr[sl], e_end = __builtin_amdgcn_readlane(sid, T - 1), e_prev = sprv[sl];
             if (sid != e_end || e_end < 0) dec = 0.f;
             const bool mixed = __ballot(sid != e_end) != 0;
             if (mixed) { // wave-uniform
