@@ -25,7 +25,8 @@
  *                          (mamba2.py:1091-1658) reached from
  *                          _Mamba2SsdAutogradM1.backward (mamba2.py:1782-1838)
  *   mamba2_ssd_state_passing -- torch.ops.mamba_ascend.mamba2_ssd_state_passing
- *                          (register.cpp:89-90; op_host mamba2_ssd_state_passing.cpp:12-78)
+ *                          (register.cpp:89-90; op_host mamba2_ssd_state_passing.cpp:12-78),
+ *                          fp32 chunk states; mamba2_ssd_state_passing_f16 its fp16 form
  *   mamba2_selective_state_update -- the single-token decode step
  *                          selective_state_update of the reference's Triton port
  *                          (mamba_triton_ascend/mamba2/ops/triton/selective_state_update.py:134-213)
@@ -42,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MAMBA2_SSD_ABI_VERSION 4
+#define MAMBA2_SSD_ABI_VERSION 5
 
 /* status codes */
 #define MAMBA2_SSD_OK 0
@@ -197,6 +198,17 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
                              const float *initial_states, float *states_start,
                              float *final_state, int64_t batch, int64_t nheads,
                              int64_t nchunks, int64_t headdim, int64_t dstate, void *stream);
+
+/* The same with fp16 chunk_states (IEEE binary16, [B, H, K, P, N]); the log
+ * decays, initial_states, states_start and final_state stay fp32, and
+ * states_start must not overlap chunk_states.  Replaces the FP16 branch of the
+ * reference op (op_host mamba2_ssd_state_passing.cpp:19-23, chunkStatesHalf at
+ * :58), which takes FP16 or FP32 chunk states and returns FP32 states. */
+int mamba2_ssd_state_passing_f16(const void *chunk_states, const float *chunk_log_decay,
+                                 const float *initial_states, float *states_start,
+                                 float *final_state, int64_t batch, int64_t nheads,
+                                 int64_t nchunks, int64_t headdim, int64_t dstate,
+                                 void *stream);
 
 /* ---- decode step ---------------------------------------------------------- */
 

@@ -21,7 +21,7 @@ LIBRARY_NAME = "libmamba2_ssd.so"
 LIBRARY_PATH = os.environ.get("MAMBA2_SSD_LIBRARY", os.path.join(_PKG_ROOT, LIBRARY_NAME))
 TORCH_OPS_PATH = os.path.join(_PKG_ROOT, "libmamba2_ssd_torch.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DT_SOFTPLUS = 1 << 0
 HAS_D = 1 << 1
@@ -152,6 +152,10 @@ EXPORTS = {
         ctypes.c_int,
     ),
     "mamba2_ssd_state_passing": (
+        [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 5 + [ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "mamba2_ssd_state_passing_f16": (
         [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 5 + [ctypes.c_void_p],
         ctypes.c_int,
     ),

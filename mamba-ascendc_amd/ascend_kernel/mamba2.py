@@ -24,6 +24,7 @@ becomes RuntimeError.  There is no CPU path: CPU tensors are rejected.
 from __future__ import annotations
 
 import contextlib
+import contextvars
 import ctypes
 import dataclasses
 import math
@@ -293,16 +294,23 @@ class TrainingPolicy:
 
 
 _policy_lock = threading.Lock()
-_policy = TrainingPolicy()
+_policy = TrainingPolicy()  # the process-wide default
+# the policy of an enclosing training_policy() block in this thread / context
+_scoped_policy: contextvars.ContextVar = contextvars.ContextVar("mamba2_training_policy", default=None)
 
 
 def get_training_policy() -> TrainingPolicy:
-    """The policy new training calls use."""
-    return _policy
+    """The policy new training calls in this context use: that of the
+    innermost enclosing ``training_policy()`` block, else the process-wide
+    default."""
+    scoped = _scoped_policy.get()
+    return _policy if scoped is None else scoped
 
 
 def set_training_policy(policy: TrainingPolicy) -> TrainingPolicy:
-    """Make ``policy`` the default for new training calls; returns the old one."""
+    """Make ``policy`` the process-wide default for new training calls (calls
+    inside a ``training_policy()`` block keep that block's policy); returns the
+    old default."""
     global _policy
     if not isinstance(policy, TrainingPolicy):
         raise TypeError("set_training_policy expects a TrainingPolicy")
@@ -313,14 +321,17 @@ def set_training_policy(policy: TrainingPolicy) -> TrainingPolicy:
 
 @contextlib.contextmanager
 def training_policy(**fields) -> Iterator[TrainingPolicy]:
-    """``with training_policy(save_chunk_states=False): ...`` -- the policy with
-    the given fields changed, for the calls inside the block."""
-    new = dataclasses.replace(_policy, **fields)
-    old = set_training_policy(new)
+    """``with training_policy(save_chunk_states=False): ...`` -- the current
+    policy with the given fields changed, for the calls inside the block.  The
+    block's policy is held in a context variable: other threads (and asyncio
+    tasks) keep theirs, and overlapping blocks in different threads cannot
+    leave each other's policy behind."""
+    new = dataclasses.replace(get_training_policy(), **fields)
+    token = _scoped_policy.set(new)
     try:
         yield new
     finally:
-        set_training_policy(old)
+        _scoped_policy.reset(token)
 
 
 # ----------------------------------------------------------------------------- autograd
@@ -482,7 +493,7 @@ def mamba2_ssd_fwd(
                 "mamba2_ssd_fwd backward requires contiguous FP32 GPU tensors with "
                 "headdim == dstate == 64"
             )
-        save = _policy.save_chunk_states if save_chunk_states is None else bool(save_chunk_states)
+        save = get_training_policy().save_chunk_states if save_chunk_states is None else bool(save_chunk_states)
         out, final_state, varlen = _Mamba2SsdAutogradM1.apply(
             x, dt, A, B, C, chunk_size, D, z, dt_bias, dt_softplus, lo, hi, initial_states,
             seq32, cu32, save)

@@ -471,25 +471,21 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
 
     const int B = (int)s->batch;
     if (s->seqlen == 0) {
-        // no tokens: the final state is the initial state (or zero)
-        if (a->final_state) {
-            const size_t n = (size_t)s->batch * s->nheads * s->headdim * s->dstate * sizeof(float);
-            hipError_t e = a->initial_states
-                               ? hipMemcpyAsync(a->final_state, a->initial_states, n,
-                                                hipMemcpyDeviceToDevice, st)
-                               : hipMemsetAsync(a->final_state, 0, n, st);
-            if (e != hipSuccess)
-                return fail(MAMBA2_SSD_ERR_LAUNCH, "final-state copy failed: %s", hipGetErrorString(e));
-        }
-        if (varlen) {
-            // every sequence is empty: zero states
-            hipError_t e = hipMemsetAsync(a->varlen_states, 0,
-                                          (size_t)a->nseqs * s->nheads * s->headdim * s->dstate *
-                                              sizeof(float),
-                                          st);
-            if (e != hipSuccess)
-                return fail(MAMBA2_SSD_ERR_LAUNCH, "varlen-state clear failed: %s", hipGetErrorString(e));
-        }
+        // no tokens: the final state is the initial state (or zero), and
+        // every varlen state is zero; written by a kernel (no memset or
+        // memcpy, so a captured forward holds kernel nodes only)
+        auto fill = [&](const float *src, float *dst, int64_t n) {
+            const int64_t blocks = std::min<int64_t>((n + ssd::kPadThreads - 1) / ssd::kPadThreads, 4096);
+            hipLaunchKernelGGL(ssd::k_copy_or_zero, dim3((unsigned)std::max<int64_t>(blocks, 1)),
+                               dim3(ssd::kPadThreads), 0, st, src, dst, n);
+            return launch_status("k_copy_or_zero", tr, st);
+        };
+        if (int rc = record(tr, st, nullptr)) return rc;
+        if (a->final_state)
+            if (int rc = fill(a->initial_states, a->final_state, s->batch * s->nheads * s->headdim * s->dstate))
+                return rc;
+        if (varlen)
+            if (int rc = fill(nullptr, a->varlen_states, a->nseqs * s->nheads * s->headdim * s->dstate)) return rc;
         return ok();
     }
     // the fused kernels' view of the shape (heads of dim 64)
@@ -906,10 +902,15 @@ int mamba2_ssd_fwd_traced(const Mamba2SsdFwdArgs *a, void *workspace, size_t wor
     return rc;
 }
 
-int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_decay,
-                             const float *initial_states, float *states_start,
-                             float *final_state, int64_t batch, int64_t nheads, int64_t nchunks_,
-                             int64_t headdim, int64_t dstate, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks and launch shared by the fp32 and fp16 forms of the stage op.
+template <typename Tin>
+int state_passing_impl(const Tin *chunk_states, const float *chunk_log_decay, const float *initial_states,
+                       float *states_start, float *final_state, int64_t batch, int64_t nheads, int64_t nchunks_,
+                       int64_t headdim, int64_t dstate, void *stream) {
     if (!chunk_states || !chunk_log_decay || !states_start)
         return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
                     "chunk_states, chunk_log_decay and states_start must be non-NULL");
@@ -929,11 +930,43 @@ int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_d
                     (long long)PN, (long long)(0x7fffffff / (4 * ssd::kStateRing)),
                     (long long)nchunks_, (long long)(0x7fffffff / 4 - 2 * ssd::kStateRing));
     const dim3 grid((unsigned)((PN / 4 + ssd::kThreads - 1) / ssd::kThreads), (unsigned)(batch * nheads));
-    hipLaunchKernelGGL(ssd::k_state_pass, grid, dim3(ssd::kThreads), 0, (hipStream_t)stream,
-                       chunk_states, chunk_log_decay, initial_states, states_start, final_state,
-                       (int)nchunks_, (int)PN);
-    if (int rc = launch_status("k_state_pass")) return rc;
+    if constexpr (sizeof(Tin) == 2) {
+        // fp16 in, fp32 out: the output cannot share the input's memory
+        const char *in = (const char *)chunk_states, *out = (const char *)states_start;
+        const size_t in_bytes = (size_t)(batch * nheads * nchunks_ * PN) * 2, out_bytes = in_bytes * 2;
+        if (in < out + out_bytes && out < in + in_bytes)
+            return fail(MAMBA2_SSD_ERR_INVALID_ARGUMENT,
+                        "states_start (fp32) must not overlap the fp16 chunk_states");
+        hipLaunchKernelGGL(ssd::k_state_pass_f16, grid, dim3(ssd::kThreads), 0, (hipStream_t)stream,
+                           (const _Float16 *)chunk_states, chunk_log_decay, initial_states, states_start,
+                           final_state, (int)nchunks_, (int)PN);
+        if (int rc = launch_status("k_state_pass_f16")) return rc;
+    } else {
+        hipLaunchKernelGGL(ssd::k_state_pass, grid, dim3(ssd::kThreads), 0, (hipStream_t)stream, chunk_states,
+                           chunk_log_decay, initial_states, states_start, final_state, (int)nchunks_, (int)PN);
+        if (int rc = launch_status("k_state_pass")) return rc;
+    }
     return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int mamba2_ssd_state_passing(const float *chunk_states, const float *chunk_log_decay,
+                             const float *initial_states, float *states_start,
+                             float *final_state, int64_t batch, int64_t nheads, int64_t nchunks_,
+                             int64_t headdim, int64_t dstate, void *stream) {
+    return state_passing_impl(chunk_states, chunk_log_decay, initial_states, states_start, final_state, batch,
+                              nheads, nchunks_, headdim, dstate, stream);
+}
+
+int mamba2_ssd_state_passing_f16(const void *chunk_states, const float *chunk_log_decay,
+                                 const float *initial_states, float *states_start, float *final_state,
+                                 int64_t batch, int64_t nheads, int64_t nchunks_, int64_t headdim,
+                                 int64_t dstate, void *stream) {
+    return state_passing_impl((const _Float16 *)chunk_states, chunk_log_decay, initial_states, states_start,
+                              final_state, batch, nheads, nchunks_, headdim, dstate, stream);
 }
 
 int mamba2_selective_state_update(const Mamba2SsuArgs *a, void *stream) {

@@ -210,8 +210,10 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(v, xor32_f(v));
 }
 
-// Binary exponent e of v = m 2^e, m in [1, 2), clamped to [-126, 126] (0
-// for v = 0): 2^-e scales v into [1, 2), and 2^e and 2^-e are finite.
+// Binary exponent e of v = m 2^e, m in [1, 2), clamped to [-126, 126]:
+// 2^-e scales v into [1, 2), and 2^e and 2^-e are finite.  v = 0 gives -1
+// (frexp's exponent of zero is 0); callers that can see a zero either do not
+// care (any scale holds zero exactly) or test for it first.
 __device__ __forceinline__ int scale_exp(float v) {
     return min(max(__builtin_amdgcn_frexp_expf(v) - 1, -126), 126);
 }
@@ -220,22 +222,30 @@ __device__ __forceinline__ int scale_exp(float v) {
 // W and the state update, and the state scales with it, so for tiny q
 // (softplus of a very negative dt) those operands would fall into fp16's
 // subnormal range and lose their low bits.  A chunk's q is scaled by 2^-ek
-// with its sum in [8, 16) (mean in [1/8, 1/4), largest below 16), and the
-// state leaving it is held as S 2^-eN:
+// with its sum in [8, 16) (mean in [1/8, 1/4)), unless that would lift its
+// largest |q| to 1 or more: then ek puts the largest |q| in [1/2, 1).  Every
+// scaled |q| is therefore below 1, so a scaled operand (x or B times the
+// decayed, scaled q) never exceeds the magnitude of the raw x or B row that
+// fp16 must already hold (a chunk dominated by one token would otherwise lift
+// it to nearly 16 and overflow fp16 at |x| of a few thousand).  The state
+// leaving the chunk is held as S 2^-eN:
 //   eN = ek                                  where the state is cut (packed sequences),
 //   eN = min(max(ek, eS + floor(cs_last)), 126)  otherwise,
 // with eS the exponent of the state entering the chunk and cs_last its log2
 // decay, since |S'| <= 2^(eS + cs_last) |S 2^-eS| + 2^ek |U 2^-ek|.  All
-// scales are exact, so they change results only where fp16 would have lost
-// bits.
-__device__ __forceinline__ int chunk_q_exp(float q_sum) { return max(scale_exp(q_sum) - 3, -126); }
+// scales are exact powers of two and none raises an operand above its raw
+// magnitude, so they change results only where fp16 would have lost bits
+// (tiny q lifted out of the subnormal range) or overflowed.
+__device__ __forceinline__ int chunk_q_exp(float q_sum, float q_max) {
+    return max(max(scale_exp(q_sum) - 3, scale_exp(q_max) + 1), -126);
+}
 __device__ __forceinline__ int next_state_exp(int eS, int ek, float cs_last, bool cut) {
     return cut ? ek : min(max(ek, eS + (int)floorf(fmaxf(cs_last, -512.f))), 126);
 }
 // Packed sequences: a chunk that holds several ids scales each id's tokens
 // by its own sum (the sequences need not share a magnitude of q), so every
-// token of one id gets the same exponent, chunk_q_exp of the q sum over the
-// chunk's tokens of that id.  One pass per distinct id (wave-uniform); the
+// token of one id gets the same exponent, chunk_q_exp of the q sum and the
+// largest q over the chunk's tokens of that id.  One pass per distinct id (wave-uniform); the
 // loop starts from the active lanes, so it ends whatever the exec mask.
 __device__ __forceinline__ int id_q_exp(int sid, float q) {
     int e = 0;
@@ -243,8 +253,8 @@ __device__ __forceinline__ int id_q_exp(int sid, float q) {
     while (left) {
         const int id = __builtin_amdgcn_readlane(sid, __builtin_ctzll(left));
         const bool mine = sid == id;
-        const float sum = wave_sum(mine ? q : 0.f);
-        if (mine) e = chunk_q_exp(sum);
+        const float sum = wave_sum(mine ? q : 0.f), top = wave_max(mine ? fabsf(q) : 0.f);
+        if (mine) e = chunk_q_exp(sum, top);
         left &= ~__ballot(mine);
     }
     return e;

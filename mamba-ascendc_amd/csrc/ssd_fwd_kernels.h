@@ -161,16 +161,31 @@ __global__ __launch_bounds__(kThreads) void k_chunk_state(FwdParams prm) {
 // --------------------------------------------------------------------------
 constexpr int kStateRing = 16;  // chunks in flight per thread in k_state_pass (and _bwd)
 
-#ifndef SSD_KERNEL_TEMPLATES_ONLY
-__global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_states,
-                                                         const float *log_decay,
-                                                         const float *init, float *states_start,
-                                                         float *final_state, int K, int PN) {
+// Four consecutive chunk-state elements (element offset `elem`) as fp32: the
+// chunk states of the stage op come in fp32 or, as the reference's op also
+// takes them, in fp16 (8-byte loads, widened exactly).
+template <typename Tin>
+__device__ __forceinline__ float4 load_state4(__amdgpu_buffer_rsrc_t r, int elem) {
+    if constexpr (sizeof(Tin) == 2) {
+        typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+        const u2 v = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(r, elem * 2, 0, 0));
+        const half4 h = __builtin_bit_cast(half4, v);
+        return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+    } else {
+        return buf_load4(r, elem * 4, 0);
+    }
+}
+
+// S_start[k] = S ; S = exp(log_decay[k]) S + U[k] over the K chunks of one
+// (b, h) stream (blockIdx.y), four state elements per thread.
+template <typename Tin>
+__device__ __forceinline__ void state_pass_body(const Tin *chunk_states, const float *log_decay, const float *init,
+                                                float *states_start, float *final_state, int K, int PN) {
     constexpr int D = kStateRing;
     const int64_t bh = blockIdx.y;
     const int idx = (blockIdx.x * kThreads + threadIdx.x) * 4;
     if (idx >= PN) return;
-    const float *u = chunk_states + bh * K * (int64_t)PN;
+    const Tin *u = chunk_states + bh * K * (int64_t)PN;
     float *so = states_start + bh * K * (int64_t)PN + idx;
     const float *ld = log_decay + bh * K;
     float4 s = init ? *(const float4 *)(init + bh * PN + idx) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -180,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_stat
     // traffic), so every round issues the same loads and the wait counts
     // stay exact.
     auto rsrc_from = [&](int k) {
-        const int64_t left = (int64_t)(K - k) * PN * 4;
+        const int64_t left = (int64_t)(K - k) * PN * (int64_t)sizeof(Tin);
         return buf_rsrc_n(u + (int64_t)k * PN, (int)(left < 0 ? 0 : (left > 0x7fffffff ? 0x7fffffff : left)));
     };
     // the log decays ride in the same ring (every lane reads the chunk's one value)
@@ -191,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_stat
         const auto r = rsrc_from(0);
 #pragma unroll
         for (int i = 0; i < D; ++i) {
-            buf[i] = buf_load4(r, (i * PN + idx) * 4, 0);
+            buf[i] = load_state4<Tin>(r, i * PN + idx);
             lv[i] = buf_load(rl, 0, i * 4);
         }
     }
@@ -206,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_stat
             s.y = dec * s.y + buf[i].y;
             s.z = dec * s.z + buf[i].z;
             s.w = dec * s.w + buf[i].w;
-            buf[i] = buf_load4(r, (i * PN + idx) * 4, 0);
+            buf[i] = load_state4<Tin>(r, i * PN + idx);
             lv[i] = buf_load(rl, 0, (k0 + D + i) * 4);
         }
     }
@@ -222,6 +237,20 @@ __global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_stat
         }
     }
     if (final_state) *(float4 *)(final_state + bh * PN + idx) = s;
+}
+
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
+__global__ __launch_bounds__(kThreads) void k_state_pass(const float *chunk_states, const float *log_decay,
+                                                         const float *init, float *states_start,
+                                                         float *final_state, int K, int PN) {
+    state_pass_body(chunk_states, log_decay, init, states_start, final_state, K, PN);
+}
+
+// The same with fp16 chunk states (fp32 states out).
+__global__ __launch_bounds__(kThreads) void k_state_pass_f16(const _Float16 *chunk_states, const float *log_decay,
+                                                             const float *init, float *states_start,
+                                                             float *final_state, int K, int PN) {
+    state_pass_body(chunk_states, log_decay, init, states_start, final_state, K, PN);
 }
 #endif
 
@@ -243,6 +272,18 @@ __global__ __launch_bounds__(kPadThreads) void k_pad_copy(const float *src, int6
         const int64_t o = orow / rd;
         dst[i] = (r < rs && c < cs) ? src[(o * rs + r) * cs + c] : 0.f;
     }
+}
+#endif
+
+// --------------------------------------------------------------------------
+// dst[i] = src ? src[i] : 0 for i < n (grid-stride): the states of an empty
+// sequence (its initial state, or zero) written by a kernel, so the forward
+// issues no memset or memcpy nodes (a caller may capture it in a graph).
+// --------------------------------------------------------------------------
+#ifndef SSD_KERNEL_TEMPLATES_ONLY
+__global__ __launch_bounds__(kPadThreads) void k_copy_or_zero(const float *src, float *dst, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kPadThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kPadThreads)
+        dst[i] = src ? src[i] : 0.f;
 }
 #endif
 

@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         const float sq = wave_inclusive_scan(q); // prefix sums of q
         const float cs = Ah2 * sq;               // log2 units
         const float cs_last = readlane_f(cs, T - 1);
-        int ek = chunk_q_exp(readlane_f(sq, T - 1)); // kSeq: that of the id leaving the chunk
+        int ek = chunk_q_exp(readlane_f(sq, T - 1), wave_max(fabsf(q))); // kSeq: that of the id leaving the chunk
         int ek_tok = ek; // exponent of the token's q (kSeq: that of its id)
         ChunkTok *tk = opaque_lds_t(&s_tok);
         if (w == 0) tk->cs[s][lane] = cs;

@@ -279,7 +279,14 @@ Grads bwd(const Tensor &x, const Tensor &dt, const Tensor &A, const Tensor &B, c
 std::tuple<Tensor, Tensor> state_passing(const Tensor &chunk_states, const Tensor &dA_cumsum,
                                          const optional<Tensor> &init) {
     const char *op = "mamba2_ssd_state_passing";
-    check_tensor(op, "chunk_states", chunk_states);
+    // chunk_states in fp32 or fp16, the rest fp32, the states out in fp32
+    // (the reference op's dtypes: op_host mamba2_ssd_state_passing.cpp:19-23, 50-53)
+    const bool half = chunk_states.scalar_type() == at::kHalf;
+    TORCH_CHECK(chunk_states.device().is_cuda(), op, ": chunk_states must be a ROCm GPU tensor (got device ",
+                chunk_states.device().str(), ")");
+    TORCH_CHECK(half || chunk_states.scalar_type() == at::kFloat, op,
+                ": chunk_states must be float32 or float16 (got ", c10::toString(chunk_states.scalar_type()), ")");
+    TORCH_CHECK(chunk_states.is_contiguous(), op, ": chunk_states must be contiguous");
     check_tensor(op, "dA_cumsum", dA_cumsum);
     TORCH_CHECK(chunk_states.dim() == 5, op, ": chunk_states must have shape [B,H,K,P,N]");
     const int64_t b = chunk_states.size(0), h = chunk_states.size(1), k = chunk_states.size(2),
@@ -294,12 +301,20 @@ std::tuple<Tensor, Tensor> state_passing(const Tensor &chunk_states, const Tenso
     }
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(chunk_states.device());
     const Tensor log_decay = dA_cumsum.select(3, dA_cumsum.size(3) - 1).contiguous();
-    Tensor states = at::empty_like(chunk_states);
-    Tensor final_state = at::empty({b, h, p, n}, chunk_states.options());
+    const auto f32 = chunk_states.options().dtype(at::kFloat);
+    Tensor states = at::empty({b, h, k, p, n}, f32);
+    Tensor final_state = at::empty({b, h, p, n}, f32);
     const hipStream_t st = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(chunk_states.device().index()).stream();
-    check_status(mamba2_ssd_state_passing(chunk_states.data_ptr<float>(), log_decay.data_ptr<float>(), cptr(init),
-                                          states.data_ptr<float>(), final_state.data_ptr<float>(), b, h, k, p, n, st),
-                 op);
+    if (half)
+        check_status(mamba2_ssd_state_passing_f16(chunk_states.data_ptr(), log_decay.data_ptr<float>(), cptr(init),
+                                                  states.data_ptr<float>(), final_state.data_ptr<float>(), b, h, k,
+                                                  p, n, st),
+                     op);
+    else
+        check_status(mamba2_ssd_state_passing(chunk_states.data_ptr<float>(), log_decay.data_ptr<float>(),
+                                              cptr(init), states.data_ptr<float>(), final_state.data_ptr<float>(),
+                                              b, h, k, p, n, st),
+                     op);
     return {states, final_state};
 }
 
@@ -332,7 +347,8 @@ Grads bwd_meta(const Tensor &x, const Tensor &dt, const Tensor &A, const Tensor 
 }
 
 std::tuple<Tensor, Tensor> state_passing_meta(const Tensor &cs, const Tensor &, const optional<Tensor> &) {
-    return {at::empty_like(cs), at::empty({cs.size(0), cs.size(1), cs.size(3), cs.size(4)}, cs.options())};
+    const auto f32 = cs.options().dtype(at::kFloat);
+    return {at::empty(cs.sizes(), f32), at::empty({cs.size(0), cs.size(1), cs.size(3), cs.size(4)}, f32)};
 }
 
 }  // namespace

@@ -63,6 +63,7 @@ How each function is pinned (tests/test_oracle.py):
 
 from __future__ import annotations
 
+import math
 from typing import Tuple
 
 import torch
@@ -457,6 +458,20 @@ def make_inputs(shape, seed, device="cpu", dtype=torch.float32, features=()):
     if "init" in features:
         out["initial_states"] = torch.randn(bsz, nheads, headdim, dstate, generator=gen)
     return {k: v.to(device=device, dtype=dtype) for k, v in out.items()}
+
+
+def dominant_q_dt(bsz, seqlen, nheads, period, seed, q_big=0.99, q_small=1e-4):
+    """dt [B, L, H] whose softplus is q_big on one random token of every
+    ``period`` tokens (per batch row and head) and q_small elsewhere: chunks
+    whose q sum comes from a single token.  dt = log(expm1(q)) inverts
+    softplus."""
+    gen = torch.Generator("cpu").manual_seed(seed)
+    inv = lambda q: math.log(math.expm1(q))  # noqa: E731
+    dt = torch.full((bsz, seqlen, nheads), inv(q_small))
+    for t0 in range(0, seqlen, period):
+        pick = t0 + torch.randint(0, min(period, seqlen - t0), (bsz, 1, nheads), generator=gen)
+        dt.scatter_(1, pick, inv(q_big))
+    return dt
 
 
 def bench_seed(config_index: int) -> int:

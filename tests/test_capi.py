@@ -219,6 +219,21 @@ def test_fwd_rejects_null_and_flag_mismatch_without_gpu():
     assert lib.mamba2_ssd_fwd(None, None, 0, None) == -1
 
 
+def test_forward_issues_kernels_only():
+    """The forward (also the empty-sequence path, whose states a fill kernel
+    writes) enqueues no memset or memcpy, so a caller may capture it in a
+    graph: no library source calls them and the built library does not link
+    them."""
+    csrc = os.path.join(ROOT, "mamba-ascendc_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h")):
+            code = re.sub(r"//.*", "", open(os.path.join(csrc, name)).read())
+            assert not re.search(r"\bhipMem(set|cpy)\w*\s*\(", code), name
+    out = subprocess.run(["nm", "-D", "--undefined-only", rt.LIBRARY_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    assert not re.search(r"\bhipMem(set|cpy)", out), out
+
+
 def test_state_passing_rejects_bad_arguments():
     lib = rt.load_library()
     fake = ctypes.c_void_p(0x1000)
@@ -235,6 +250,12 @@ def test_state_passing_rejects_bad_arguments():
                                         64, 64, None) == -2
     assert lib.mamba2_ssd_state_passing(fake, fake, None, fake, None, 256, 256, 1, 64, 64,
                                         None) == -2
+    # the fp16 form: the same checks, and its fp32 output may not overlap the fp16 input
+    f16 = lib.mamba2_ssd_state_passing_f16
+    assert f16(None, fake, None, fake, None, 1, 1, 1, 64, 64, None) == -1
+    assert f16(fake, fake, None, fake, None, 1, 1, 1, 3, 3, None) == -2
+    assert f16(fake, fake, None, fake, None, 1, 1, 2, 64, 64, None) == -1
+    assert "overlap" in rt.last_error(lib)
 
 
 def test_decode_step_rejects_bad_arguments():
@@ -390,6 +411,11 @@ def test_meta_shape_inference():
     states, fin = torch.ops.mamba_ascend.mamba2_ssd_state_passing(
         torch.empty(2, 8, 4, 64, 64, device="meta"), torch.empty(2, 8, 4, 64, device="meta"), None)
     assert states.shape == (2, 8, 4, 64, 64) and fin.shape == (2, 8, 64, 64)
+    # fp16 chunk states give fp32 states (the reference op's output dtype)
+    states, fin = torch.ops.mamba_ascend.mamba2_ssd_state_passing(
+        torch.empty(2, 8, 4, 64, 64, device="meta", dtype=torch.float16), torch.empty(2, 8, 4, 64, device="meta"),
+        None)
+    assert states.dtype == torch.float32 and fin.dtype == torch.float32
 
 
 @pytest.mark.parametrize(
@@ -507,5 +533,27 @@ def test_training_policy_object():
     with pytest.raises(TypeError):
         with ascend_kernel.training_policy(no_such_field=True):
             pass
+    # a block affects its own thread only, and overlapping blocks in two
+    # threads each restore their own state
+    import threading
+
+    inside, release, seen = threading.Event(), threading.Event(), {}
+
+    def other():
+        with ascend_kernel.training_policy(save_chunk_states=False):
+            inside.set()
+            release.wait(10)
+            seen["other_in_block"] = ascend_kernel.get_training_policy().save_chunk_states
+        seen["other_after"] = ascend_kernel.get_training_policy().save_chunk_states
+
+    th = threading.Thread(target=other)
+    th.start()
+    assert inside.wait(10)
+    seen["main_during"] = ascend_kernel.get_training_policy().save_chunk_states
+    with ascend_kernel.training_policy(save_chunk_states=True):
+        release.set()
+        th.join(10)
+    assert seen == {"other_in_block": False, "other_after": True, "main_during": True}
+    assert ascend_kernel.get_training_policy().save_chunk_states is True
     sig = inspect.signature(ascend_kernel.mamba2_ssd_fwd)
     assert sig.parameters["save_chunk_states"].kind is inspect.Parameter.KEYWORD_ONLY

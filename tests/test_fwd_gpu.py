@@ -142,6 +142,33 @@ def test_state_passing_op():
     assert torch.allclose(fin.cpu(), S, atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("K,with_init", [(5, True), (37, False)], ids=["K5-init", "K37"])
+def test_state_passing_op_fp16_chunk_states(K, with_init):
+    """fp16 chunk states (the reference op's FP16 branch, op_host
+    mamba2_ssd_state_passing.cpp:19-23): fp32 states out, against the direct
+    recurrence over the same fp16 values widened to fp32; K = 37 runs past
+    the kernel's ring of 16 chunks in flight."""
+    _need_gpu()
+    g = torch.Generator().manual_seed(12)
+    U = torch.randn(2, 3, K, 64, 128, generator=g).half()
+    dA = -torch.rand(2, 3, K, 64, generator=g)
+    init = torch.randn(2, 3, 64, 128, generator=g) if with_init else None
+    states, fin = torch.ops.mamba_ascend.mamba2_ssd_state_passing(
+        U.cuda(), dA.cuda(), None if init is None else init.cuda())
+    assert states.dtype == torch.float32 and fin.dtype == torch.float32
+    S = torch.zeros(2, 3, 64, 128) if init is None else init.clone()
+    ref = []
+    for k in range(K):
+        ref.append(S.clone())
+        S = torch.exp(dA[:, :, k, -1])[..., None, None] * S + U[:, :, k].float()
+    assert torch.allclose(states.cpu(), torch.stack(ref, 2), atol=1e-5, rtol=1e-5)
+    assert torch.allclose(fin.cpu(), S, atol=1e-5, rtol=1e-5)
+    # the fp32 form on the widened values gives the same bits
+    s32, f32 = torch.ops.mamba_ascend.mamba2_ssd_state_passing(
+        U.float().cuda(), dA.cuda(), None if init is None else init.cuda())
+    assert torch.equal(s32, states) and torch.equal(f32, fin)
+
+
 def _slice_groups(inp, g0, g1, r):
     out = dict(inp)
     out["x"] = inp["x"][:, :, g0 * r:g1 * r].contiguous()

@@ -25,7 +25,7 @@ import pytest
 import torch
 
 from oracle.precision_emulation import ssd_forward_emulated
-from oracle.ssd_reference import bench_seed, make_inputs, parity_metrics, ssd_chunk_scan_ref
+from oracle.ssd_reference import bench_seed, dominant_q_dt, make_inputs, parity_metrics, ssd_chunk_scan_ref
 
 MAXABS = 2e-2
 
@@ -101,3 +101,38 @@ def test_emulation_rounding_is_live():
     d_single = float((single - exact).abs().max())
     d_split = float((split - exact).abs().max())
     assert d_single > 0 and d_split < d_single / 100
+
+
+
+def test_q_scale_keeps_dominated_chunks_in_fp16_range():
+    """A chunk whose q sum comes from one token: scaling the sum into
+    [8, 16) lifts that token's q to nearly 16, so the state update's operand
+    (decay q x, fp16) overflows at |x| of a few thousand; capping the scale so
+    the largest q stays below 1 keeps it finite and at the fp32 oracle's
+    precision.  On ordinary inputs the cap never binds: the C4 unit gets the
+    same exponents under both rules."""
+    from oracle.precision_emulation import chunk_q_exponent
+
+    b, l, h = 1, 256, 2
+    gen = torch.Generator().manual_seed(21)
+    x = torch.randn(b, l, h, 64, generator=gen) * 2e3
+    dt = dominant_q_dt(b, l, h, 64, seed=22)
+    A = -torch.rand(h, generator=gen)
+    B = torch.randn(b, l, 1, 64, generator=gen)
+    C = torch.randn(b, l, 1, 64, generator=gen)
+    ref, ref_fin = ssd_chunk_scan_ref(x, dt, A, B, C, 64, dt_softplus=True, return_final_state=True)
+    y_sum, _ = ssd_forward_emulated(x, dt, A, B, C, "split16", q_scale="sum")
+    y_cap, fin_cap = ssd_forward_emulated(x, dt, A, B, C, "split16", q_scale="sum_max")
+    assert not torch.isfinite(y_sum).all()  # the sum-only rule overflows fp16
+    assert torch.isfinite(y_cap).all()
+    assert parity_metrics(y_cap, ref)[1] < 1e-5 and parity_metrics(fin_cap, ref_fin)[1] < 1e-5
+    # the rules on the bench-distributed C4 unit: identical exponents
+    u = _unit(3, [4, 2048, 16, 64, 64, 64, 4])
+    qc = torch.nn.functional.softplus(u["dt"].double()).reshape(1, 32, 64, 4).permute(0, 1, 3, 2)
+    assert torch.equal(chunk_q_exponent(qc, "sum"), chunk_q_exponent(qc, "sum_max"))
+    # ... and on the dominated chunks the cap puts the largest q in [1/2, 1)
+    qd = torch.nn.functional.softplus(dt.double()).reshape(b, 4, 64, h).permute(0, 1, 3, 2)
+    top = qd.amax(-1) * torch.pow(2.0, -chunk_q_exponent(qd, "sum_max").double())
+    assert bool(((top >= 0.5) & (top < 1)).all())
+    top_sum = qd.amax(-1) * torch.pow(2.0, -chunk_q_exponent(qd, "sum").double())
+    assert bool((top_sum > 15).all())
