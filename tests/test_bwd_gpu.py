@@ -13,6 +13,7 @@ against the float64 oracle at the bound of the small cases; config 3 the same
 way on independent slices.
 """
 
+import functools
 import math
 import sys
 
@@ -189,48 +190,108 @@ def test_backward_baseline_config4():
         assert cos >= 0.999, (k, cos)
 
 
-def test_backward_baseline_config3_slices():
+def _c3_features(shape, seed):
+    """The benchmark's full feature set (reference mamba2_backward_bench.py:
+    159-165): D [H, P], z, dt_bias, initial states, with dt_limit (1e-3, 1);
+    drawn on the CPU with the distributions bench.py uses."""
+    b, l, h, p, n, _chunk, g = shape
+    gen = torch.Generator().manual_seed(seed + 1)
+    return {"D": torch.randn(h, p, generator=gen), "z": torch.randn(b, l, h, p, generator=gen),
+            "dt_bias": torch.randn(h, generator=gen) * 0.1,
+            "initial_states": torch.randn(b, h, p, n, generator=gen) / 5}
+
+
+def _packed_ids(shape, seed, lo=256, hi=2048):
+    """Every batch row cut into sequences of U[lo, hi) tokens (the last one
+    shortened to fit), as bench.py's packed-sequence timing does."""
+    b, l = shape[0], shape[1]
+    gen = torch.Generator().manual_seed(seed + 2)
+    rows = []
+    for _ in range(b):
+        lengths = []
+        while sum(lengths) < l:
+            lengths.append(int(torch.randint(lo, hi, (1,), generator=gen)))
+        lengths[-1] -= sum(lengths) - l
+        rows.append(torch.cat([torch.full((m,), i, dtype=torch.int32) for i, m in enumerate(lengths)]))
+    return torch.stack(rows)
+
+
+@functools.lru_cache(maxsize=1)
+def _c3_inputs():
+    """The config-3 inputs (drawing them takes a while on the CPU): shared by
+    the variants below, which copy the dict before adding to it."""
+    return make_inputs([8, 4096, 256, 64, 64, 64, 64], seed=bench_seed(2))
+
+
+@pytest.mark.parametrize("variant", ["plain", "full", "packed"])
+def test_backward_baseline_config3_slices(variant):
     """BASELINE config 3 [8,4096,256,64,64,64,64] trained at full size through
     autograd (the reverse fused backward: 512 (batch, group) streams, 64 chunks
-    each, 4 heads per group), loss mean(y^2) + mean(final^2).  (batch, group)
-    units share nothing but dA, so dx, ddt, dB and dC of a slice depend only on
-    that slice's inputs and upstream gradients: the oracle runs on batches 0
-    and 7, groups 0..3, with the GPU's own upstream gradients."""
+    each, 4 heads per group), loss mean(y^2) + mean(final^2); plain, with the
+    benchmark's full feature set (D [H,P], z, dt_bias, initial states,
+    dt_limit (1e-3, 1)), or with packed sequences (rows cut into sequences of
+    256..2047 tokens).  (batch, group) units share nothing but the per-head
+    sums (dA, dD, ddt_bias), so the forward outputs and dx, ddt, dB, dC, dz,
+    dinitial_states of a slice depend only on that slice's inputs and
+    upstream gradients: the oracle runs on batches 0 and 7 x groups 0..3, and
+    on group 0 across all 8 batches, which also gives the per-head sums of its
+    4 heads, each with the GPU's own upstream gradients."""
     _need_gpu()
     import ascend_kernel
 
     shape = [8, 4096, 256, 64, 64, 64, 64]
-    _say(f"config 3 backward {shape}")
-    inp = make_inputs(shape, seed=bench_seed(2))
+    _say(f"config 3 training {variant} {shape}")
+    inp = dict(_c3_inputs())
+    limit = (0.0, math.inf)
+    ids = None
+    if variant == "full":
+        inp.update(_c3_features(shape, bench_seed(2)))
+        limit = (1e-3, 1.0)
+    elif variant == "packed":
+        ids = _packed_ids(shape, bench_seed(2))
     leaves = {k: v.cuda().requires_grad_(True) for k, v in inp.items()}
-    out, fin = ascend_kernel.mamba2_ssd_fwd(leaves["x"], leaves["dt"], leaves["A"], leaves["B"],
-                                            leaves["C"], 64, dt_softplus=True,
-                                            return_final_state=True)
+    out, fin = ascend_kernel.mamba2_ssd_fwd(
+        leaves["x"], leaves["dt"], leaves["A"], leaves["B"], leaves["C"], 64, D=leaves.get("D"),
+        z=leaves.get("z"), dt_bias=leaves.get("dt_bias"), dt_softplus=True, dt_limit=limit,
+        initial_states=leaves.get("initial_states"), return_final_state=True,
+        seq_idx=None if ids is None else ids.cuda())
     gy = (out * (2.0 / out.numel())).detach()
     gf = (fin * (2.0 / fin.numel())).detach()
     torch.autograd.backward((out, fin), (gy, gf))
     torch.cuda.synchronize()
-    for k in ("x", "dt", "B", "C"):
+    for k in leaves:
         assert bool(torch.isfinite(leaves[k].grad).all()), k
-    r, groups = 4, 4
-    for bi in (0, 7):
-        hs = slice(0, groups * r)
-        sub = {"x": inp["x"][bi:bi + 1, :, hs], "dt": inp["dt"][bi:bi + 1, :, hs], "A": inp["A"][hs],
-               "B": inp["B"][bi:bi + 1, :, :groups], "C": inp["C"][bi:bi + 1, :, :groups]}
-        lv = {k: v.contiguous().clone().requires_grad_(True) for k, v in sub.items()}
-        ro, rf = ssd_chunk_scan_ref(lv["x"], lv["dt"], lv["A"], lv["B"], lv["C"], 64,
-                                    dt_softplus=True, return_final_state=True)
-        torch.autograd.backward((ro, rf), (gy[bi:bi + 1, :, hs].cpu(), gf[bi:bi + 1, hs].cpu()))
-        got = {"x": leaves["x"].grad[bi:bi + 1, :, hs], "dt": leaves["dt"].grad[bi:bi + 1, :, hs],
-               "B": leaves["B"].grad[bi:bi + 1, :, :groups], "C": leaves["C"].grad[bi:bi + 1, :, :groups]}
-        for k, g in got.items():
-            g = g.cpu()
+    r = 4
+    per_stream = ("x", "dt", "B", "C", "z", "initial_states")
+    for bs, gs in (((0, 1), (0, 4)), ((7, 8), (0, 4)), ((0, 8), (0, 1))):
+        b0, b1 = bs
+        hs, gsl = slice(gs[0] * r, gs[1] * r), slice(*gs)
+        sel = {"x": (slice(b0, b1), slice(None), hs), "dt": (slice(b0, b1), slice(None), hs), "A": (hs,),
+               "B": (slice(b0, b1), slice(None), gsl), "C": (slice(b0, b1), slice(None), gsl), "D": (hs,),
+               "z": (slice(b0, b1), slice(None), hs), "dt_bias": (hs,), "initial_states": (slice(b0, b1), hs)}
+        lv = {k: v[sel[k]].contiguous().clone().requires_grad_(True) for k, v in inp.items()}
+        sid = None if ids is None else ids[b0:b1].contiguous()
+        ro, rf = ssd_chunk_scan_ref(lv["x"], lv["dt"], lv["A"], lv["B"], lv["C"], 64, D=lv.get("D"),
+                                    z=lv.get("z"), dt_bias=lv.get("dt_bias"), dt_softplus=True, dt_limit=limit,
+                                    initial_states=lv.get("initial_states"), return_final_state=True,
+                                    seq_idx=sid)
+        label = f"batches {b0}..{b1 - 1} groups {gs[0]}..{gs[1] - 1}"
+        for name, got, want in (("out", out[b0:b1, :, hs], ro), ("final", fin[b0:b1, hs], rf)):
+            ma, rl = parity_metrics(got.detach().cpu(), want.detach())
+            _say(f"  {label} {name:<6} maxabs {ma:.3e} relL2 {rl:.3e}")
+            assert ma <= 2e-2 and rl <= 5e-3, (label, name, ma, rl)
+        torch.autograd.backward((ro, rf), (gy[b0:b1, :, hs].cpu(), gf[b0:b1, hs].cpu()))
+        # per-head sums are complete only over all batches
+        names = [k for k in lv if k in per_stream or b1 - b0 == 8]
+        for k in names:
+            g = leaves[k].grad[sel[k]].cpu()
             ma, rl = parity_metrics(g, lv[k].grad)
             cos = _cos(g, lv[k].grad)
-            _say(f"  batch {bi} d{k:<3} maxabs {ma:.3e} (max |want| {lv[k].grad.abs().max():.3e}) "
+            _say(f"  {label} d{k:<15} maxabs {ma:.3e} (max |want| {lv[k].grad.abs().max():.3e}) "
                  f"relL2 {rl:.3e} cos {cos:.9f}")
-            assert rl <= 5e-3 and ma <= 2e-2 and cos >= 0.999, (bi, k, ma, rl, cos)
-            assert rl <= TIGHT_REL, (bi, k, rl)
+            assert rl <= 5e-3 and ma <= 2e-2 and cos >= 0.999, (label, k, ma, rl, cos)
+            if variant == "plain":
+                assert rl <= TIGHT_REL, (label, k, rl)
 
 
 def test_forward_chunk_states_are_prefix_final_states():
