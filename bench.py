@@ -3,8 +3,9 @@
 
 Workload: the headline configuration [B,L,H,P,N,chunk,G] = [8,4096,256,64,64,64,64]
 (x, dt, A, B, C; dt_softplus=True, return_final_state=True; fp32 public tensors),
-synthetic inputs drawn on the GPU with the benchmark distributions (x, B, C ~ N(0,1),
-dt ~ U[0,1), A = -U[0,1)).  A "step" is one forward call over that batch; when the
+synthetic inputs drawn on the CPU with torch.Generator("cpu").manual_seed(20260806 +
+config index) in the order x = randn, dt = rand, A = -rand, B = randn, C = randn, then
+copied to the GPU, so the GPU and the CPU baseline see bit-identical tensors.  A "step" is one forward call over that batch; when the
 backward is available the fwd+bwd time (loss mean(y^2) + mean(final^2)) is reported
 beside it.
 
@@ -15,9 +16,10 @@ durations used for the roofline come from the timed region itself.  The wall-clo
 time of the K steps, bracketed by device synchronisation, gives ms_per_step.
 
 CPU baseline: the repository's fp32 CPU oracle (oracle/ssd_reference.py, a restatement
-of the reference's mamba_torch/ssd_reference.py) timed on a bounded sample of the same
-workload (batch 0, the first few groups) on this host's cores, scaled to the full
-configuration by the number of independent (batch, group) units.
+of the reference's mamba_torch/ssd_reference.py) timed on this host's cores on the same
+CPU tensors, for every BASELINE config: the forward (C1, C2, C3, C5) and the forward plus
+autograd backward of mean(y^2) + mean(final^2) (C4), time.perf_counter_ns around each call,
+median of warmup 1 / repeat 3 at C3 and warmup 3 / repeat 10 elsewhere.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -182,6 +184,11 @@ def fwd_kernel_model(name: str, shape) -> dict:
     elif name == "k_fwd_seg_state":
         per = f4 * (T * p + T + T * n / r)
         fl = 2 * T * p * n
+    elif name == "k_fwd_seg_state_save":
+        # the backward's recompute of the chunk-start states: x, dt, B in,
+        # the state entering every chunk out
+        per = f4 * (T * p + T + T * n / r + p * n)
+        fl = 2 * T * p * n
     elif name == "k_bwd_dstate_rev":
         # dout, dt, C in; dU (state gradient leaving each chunk) out
         per = f4 * (T * p + T + T * n / r + p * n)
@@ -236,17 +243,42 @@ def op_work(shape):
 
 # ----------------------------------------------------------------------------- GPU runs
 
-def make_gpu_inputs(torch, shape, seed):
+def make_cpu_inputs(torch, shape, seed):
+    """The BASELINE inputs: one CPU generator seeded with `seed`, drawn in the
+    order x = randn, dt = rand, A = -rand, B = randn, C = randn (fp32)."""
     b, l, h, p, n, _chunk, g = shape
-    gen = torch.Generator(device="cuda").manual_seed(seed)
-    kw = dict(device="cuda", dtype=torch.float32, generator=gen)
+    gen = torch.Generator("cpu").manual_seed(seed)
     return {
-        "x": torch.randn(b, l, h, p, **kw),
-        "dt": torch.rand(b, l, h, **kw),
-        "A": -torch.rand(h, **kw),
-        "B": torch.randn(b, l, g, n, **kw),
-        "C": torch.randn(b, l, g, n, **kw),
+        "x": torch.randn(b, l, h, p, generator=gen),
+        "dt": torch.rand(b, l, h, generator=gen),
+        "A": -torch.rand(h, generator=gen),
+        "B": torch.randn(b, l, g, n, generator=gen),
+        "C": torch.randn(b, l, g, n, generator=gen),
     }
+
+
+def to_gpu(torch, cpu):
+    gpu = {k: v.cuda() for k, v in cpu.items()}
+    torch.cuda.synchronize()
+    return gpu
+
+
+def summarize(samples):
+    """Tail statistics of per-call times (the reference bench's summary,
+    benchmarks/mamba2_backward_bench.py:380-389)."""
+    vals = list(samples)
+    ordered = sorted(vals)
+    return {"median_ms": round(statistics.median(vals), 6), "mean_ms": round(statistics.fmean(vals), 6),
+            "p90_ms": round(ordered[min(len(ordered) - 1, math.ceil(0.9 * len(ordered)) - 1)], 6),
+            "min_ms": round(min(vals), 6), "max_ms": round(max(vals), 6), "n": len(vals)}
+
+
+def checksums(torch, tensors):
+    """Sum of every tensor (float64 accumulation), and their total: the
+    reference bench's gradient checksums (mamba2_backward_bench.py:569-579)."""
+    sums = {k: float(v.double().sum()) for k, v in tensors.items()}
+    total = sum(sums.values())
+    return {k: (v if math.isfinite(v) else None) for k, v in sums.items()}, (total if math.isfinite(total) else None)
 
 
 def run_traced(torch, lib, rt, hip, call, nsteps, max_kernels=16):
@@ -303,7 +335,7 @@ def bench_forward(torch, lib, rt, api, hip, inp, shape, steps, warmup):
 PARITY_MAXABS, PARITY_RELL2 = 2e-2, 5e-3  # the contract: max-abs and relative-L2 vs the fp32 oracle
 
 
-def parity_slices(torch, inp, out, final, shape, slices):
+def parity_slices(torch, cpu_inp, out, final, shape, slices):
     """Same-run parity gate: the CPU oracle on slices (batch, head0, head1) of the
     timed inputs against the same slices of the GPU output.  Heads share nothing
     but their group's B and C, so a slice of heads of one group is an
@@ -316,10 +348,10 @@ def parity_slices(torch, inp, out, final, shape, slices):
     for bi, h0, h1 in slices:
         gi = h0 // r
         assert (h1 - 1) // r == gi, "a parity slice stays within one group"
-        sub = {"x": inp["x"][bi:bi + 1, :, h0:h1], "dt": inp["dt"][bi:bi + 1, :, h0:h1],
-               "A": inp["A"][h0:h1], "B": inp["B"][bi:bi + 1, :, gi:gi + 1],
-               "C": inp["C"][bi:bi + 1, :, gi:gi + 1]}
-        sub = {k: v.contiguous().cpu() for k, v in sub.items()}
+        sub = {"x": cpu_inp["x"][bi:bi + 1, :, h0:h1], "dt": cpu_inp["dt"][bi:bi + 1, :, h0:h1],
+               "A": cpu_inp["A"][h0:h1], "B": cpu_inp["B"][bi:bi + 1, :, gi:gi + 1],
+               "C": cpu_inp["C"][bi:bi + 1, :, gi:gi + 1]}
+        sub = {k: v.contiguous() for k, v in sub.items()}
         with torch.no_grad():
             ref, ref_fin = ssd_chunk_scan_ref(sub["x"], sub["dt"], sub["A"], sub["B"], sub["C"], chunk,
                                               dt_softplus=True, return_final_state=True)
@@ -358,53 +390,67 @@ def summarize_kernels(res, names, shape):
     return kern
 
 
-def bench_config(torch, lib, rt, api, hip, cfg, steps, warmup):
+def bench_config(torch, lib, rt, api, hip, cfg, steps, warmup, cpu=True):
     """One BASELINE config besides the headline: the forward (dt_softplus, final
     state) timed with the reference protocol, its per-kernel durations, the
     op-level algorithmic GB/s and HBM fraction, and a same-run parity slice; for
-    config 4 (the M1 backward config) also the training forward + backward."""
+    config 4 (the M1 backward config) also the training forward + backward;
+    and the CPU oracle on the same inputs (forward; config 4 forward plus
+    autograd backward)."""
     shape = CONFIGS[cfg]
     seed = 20260806 + (cfg - 1)
-    inp = make_gpu_inputs(torch, shape, seed)
-    torch.cuda.synchronize()
+    cpu_inp = make_cpu_inputs(torch, shape, seed)
+    inp = to_gpu(torch, cpu_inp)
     res, names, _wall, finite, ws_bytes, out, final = bench_forward(
         torch, lib, rt, api, hip, inp, shape, steps, warmup)
     fwd_ms = statistics.median(r[0] for r in res)
     flops, nbytes = op_work(shape)
-    row = {"shape": shape, "seed": seed, "fwd_ms": round(fwd_ms, 5),
+    row = {"shape": shape, "seed": seed, "fwd_ms": round(fwd_ms, 5), "fwd": summarize(r[0] for r in res),
            "fwd_kernels": summarize_kernels(res, names, shape),
            "op_GB_s": round(nbytes / (fwd_ms * 1e-3) / 1e9, 1),
            "op_TFLOP_s": round(flops / (fwd_ms * 1e-3) / 1e12, 2),
            "hbm_roofline_frac": round(nbytes / (fwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            "op_bytes": nbytes, "workspace_bytes": ws_bytes, "finite": finite,
-           "parity": parity_slices(torch, inp, out, final, shape, PARITY_SLICES[cfg])}
+           "output_checksums": checksums(torch, {"out": out, "final": final})[0],
+           "parity": parity_slices(torch, cpu_inp, out, final, shape, PARITY_SLICES[cfg])}
     del out, final
     row["api_fwd_ms"] = round(bench_api(torch, api, inp, shape[5], max(5, steps // 3), 3), 5)
     row["api_host_us"] = round(api_host_cost(torch, api, inp, shape[5]), 1)
-    if shape[3] == 64 and shape[4] == 64:
+    train = shape[3] == 64 and shape[4] == 64
+    if train:
         tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup)
         if tr is not None:
             fres, bres, bnames, bfinite = tr[:4]
             row["fwd_train_ms"] = round(statistics.median(r[0] for r in fres), 5)
             row["bwd_ms"] = round(statistics.median(r[0] for r in bres), 5)
             row["fwd_bwd_ms"] = round(statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres)), 5)
+            row["fwd_train"] = summarize(r[0] for r in fres)
+            row["bwd"] = summarize(r[0] for r in bres)
+            row["fwd_bwd"] = summarize(f[0] + bk[0] for f, bk in zip(fres, bres))
             row["bwd_kernels"] = summarize_kernels(bres, bnames, shape)
             row["grads_finite"] = bool(bfinite)
+            row["gradient_checksums"], row["gradient_checksum"] = tr[6]
     del inp
     torch.cuda.empty_cache()
+    if cpu:
+        row["cpu_baseline"] = cpu_oracle_baseline(torch, cpu_inp, shape, seed, with_bwd=train)
+        log(f"config C{cfg} cpu baseline {row['cpu_baseline']['value']:.2f} ms "
+            f"({row['cpu_baseline']['cores']} threads)")
+    del cpu_inp
     return row
 
 
 def full_features(torch, shape, seed):
     """The reference benchmark's "full" feature set (mamba2_backward_bench.py:
     159-165, 219-241): D [H, P], z, dt_bias, initial states, softplus and
-    dt_limit (1e-3, 1); seeded GPU tensors of those shapes."""
+    dt_limit (1e-3, 1); drawn on a CPU generator seeded with seed + 1 and
+    copied to the GPU (tests/test_bwd_gpu.py checks this set at C3)."""
     b, l, h, p, n, _chunk, g = shape
-    gen = torch.Generator(device="cuda").manual_seed(seed + 1)
-    kw = dict(device="cuda", dtype=torch.float32, generator=gen)
-    return {"D": torch.randn(h, p, **kw), "z": torch.randn(b, l, h, p, **kw),
-            "dt_bias": torch.randn(h, **kw) * 0.1,
-            "initial_states": torch.randn(b, h, p, n, **kw) / 5, "dt_limit": (1e-3, 1.0)}
+    gen = torch.Generator("cpu").manual_seed(seed + 1)
+    feats = {"D": torch.randn(h, p, generator=gen), "z": torch.randn(b, l, h, p, generator=gen),
+             "dt_bias": torch.randn(h, generator=gen) * 0.1,
+             "initial_states": torch.randn(b, h, p, n, generator=gen) / 5}
+    return {**to_gpu(torch, feats), "dt_limit": (1e-3, 1.0)}
 
 
 def feature_flags(rt, feats):
@@ -462,14 +508,16 @@ def bench_fwd_features(torch, lib, rt, inp, shape, feats, steps, warmup, seq=Non
         e0.record()
         e0.synchronize()
         samples.append(s0.elapsed_time(e0))
-    return statistics.median(samples)
+    return summarize(samples)
 
 
 def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup, feats=None, seq=None):
     """Training forward (saving the chunk-start states) + M1 bwd through the C
     ABI with per-kernel events; upstream gradients of the loss mean(y^2) +
     mean(final^2).  `feats`: optional full-feature tensors (full_features);
-    `seq`: optional packed-sequence ids.  None if unsupported."""
+    `seq`: optional packed-sequence ids.  None if unsupported; else (forward
+    steps, backward steps, backward kernel names, gradients finite, workspace
+    bytes, forward kernel names, (gradient checksums, their total))."""
     x, dt, A, B, C = (inp[k] for k in ("x", "dt", "A", "B", "C"))
     b, l, h, p, n, chunk, g = shape
     shp = rt.Mamba2SsdShape(b, l, h, p, g, n, chunk)
@@ -522,7 +570,9 @@ def bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, steps, warmup, feats=N
     fres, fnames, _ = run_traced(torch, lib, rt, hip, call_f, steps)
     bres, bnames, _ = run_traced(torch, lib, rt, hip, call_b, steps)
     ok = all(bool(torch.isfinite(v).all()) for v in grads.values())
-    return fres, bres, bnames, ok, ws.numel(), fnames
+    sums = checksums(torch, {("d" + k if not k.startswith("d") or k == "dt" else k): v
+                             for k, v in grads.items()})
+    return fres, bres, bnames, ok, ws.numel(), fnames, sums
 
 
 def copy_calibration(torch, nbytes):
@@ -797,36 +847,47 @@ def host_info():
     return {"cpu_model": model, "sockets": max(1, len(sockets)), "logical_cpus": os.cpu_count()}
 
 
-def cpu_baseline(torch, shape, seed, budget_s):
-    """Oracle forward on batch 0 and the first `gs` groups; scaled to the full config."""
-    from oracle.ssd_reference import make_inputs, ssd_chunk_scan_ref
+def cpu_oracle_baseline(torch, cpu_inp, shape, seed, with_bwd=False, warmup=None, repeat=None):
+    """The fp32 CPU oracle on the whole configuration, on the same CPU tensors
+    the GPU copies came from: the forward (dt_softplus, final state), or with
+    `with_bwd` the forward plus the autograd backward of mean(y^2) +
+    mean(final^2) (BASELINE.md's plan; C4).  time.perf_counter_ns around each
+    call (benchmarks/mamba2_backward_bench.py:373-376), median; warmup 1 /
+    repeat 3 for the 8.6 GB config 3, warmup 3 / repeat 10 otherwise."""
+    from oracle.ssd_reference import ssd_chunk_scan_ref
 
-    b, l, h, p, n, chunk, g = shape
-    r = h // g
+    chunk = shape[5]
+    big = shape == CONFIGS[3]
+    warmup = (1 if big else 3) if warmup is None else warmup
+    repeat = (3 if big else 10) if repeat is None else repeat
     torch.set_num_threads(os.cpu_count() or 1)
 
-    def sample(gs):
-        sub = [1, l, gs * r, p, n, chunk, gs]
-        inp = make_inputs(sub, seed)
-        t0 = time.perf_counter_ns()
-        with torch.no_grad():
-            ssd_chunk_scan_ref(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], chunk,
-                               dt_softplus=True, return_final_state=True)
+    def call():
+        if with_bwd:
+            lv = {k: v.clone().requires_grad_(True) for k, v in cpu_inp.items()}
+            t0 = time.perf_counter_ns()
+            out, fin = ssd_chunk_scan_ref(lv["x"], lv["dt"], lv["A"], lv["B"], lv["C"], chunk,
+                                          dt_softplus=True, return_final_state=True)
+            (out.pow(2).mean() + fin.pow(2).mean()).backward()
+        else:
+            t0 = time.perf_counter_ns()
+            with torch.no_grad():
+                ssd_chunk_scan_ref(cpu_inp["x"], cpu_inp["dt"], cpu_inp["A"], cpu_inp["B"], cpu_inp["C"], chunk,
+                                   dt_softplus=True, return_final_state=True)
         return (time.perf_counter_ns() - t0) / 1e6
 
-    one = sample(1)  # also the warmup
-    gs = int(max(1, min(g, (budget_s / 3 * 1e3) // max(one, 1e-3))))
-    times = [sample(gs) for _ in range(3)]
-    med = statistics.median(times)
-    scale = (b * g) / gs
+    for _ in range(warmup):
+        call()
+    times = [call() for _ in range(repeat)]
+    what = "forward + autograd backward (loss mean(y^2) + mean(final^2))" if with_bwd else "forward"
     return {
-        "value": med * scale,
+        "value": round(statistics.median(times), 4),
         "unit": "ms",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"oracle fp32 forward on batch 0, groups 0..{gs - 1} ({gs * r} heads, "
-                   f"L={l}) of the workload: median of 3 = {med:.1f} ms, x{scale:g} "
-                   f"(independent (batch, group) units) to the full config"),
+        "sample": (f"oracle fp32 {what} on the whole config {shape} (seed {seed}, the GPU's inputs), "
+                   f"median of {repeat} after {warmup} warmup"),
+        "stats": summarize(times),
         "host": host_info(),
         "torch": torch.__version__,
     }
@@ -843,8 +904,9 @@ def _short(name: str) -> str:
 def model_key(short: str) -> str:
     """Kernel-model / trace name of a (templated) kernel.
 
-    k_fwd_seg<state only, save states, z gate, packed sequences>: <true, ...>
-    is k_fwd_seg_state, <false, true, ...> k_fwd_seg_save, <false, false, ...>
+    k_fwd_seg<state only, save states, z gate, packed sequences>: <true, false,
+    ...> is k_fwd_seg_state, <true, true, ...> k_fwd_seg_state_save (the
+    backward's recompute of the chunk states), <false, true, ...> k_fwd_seg_save, <false, false, ...>
     k_fwd_seg, with a "_gate" suffix for the z-gated form and "_seq" for
     packed sequences.  k_bwd_ws<has z, heads per group, packed sequences>: a
     group size above 0 is the reverse fused k_bwd_ws_rev ("_z" with z, "_seq"
@@ -858,7 +920,8 @@ def model_key(short: str) -> str:
         args = [a.strip() for a in short[len("k_fwd_seg<"):-1].split(",")]
         seq = "_seq" if len(args) > 3 and args[3] == "true" else ""
         if args[0] == "true":
-            return "k_fwd_seg_state" + seq
+            save = "_save" if len(args) > 1 and args[1] == "true" else ""
+            return "k_fwd_seg_state" + save + seq
         key = "k_fwd_seg_save" if len(args) > 1 and args[1] == "true" else "k_fwd_seg"
         return (key + "_gate" if len(args) > 2 and args[2] == "true" else key) + seq
     base = short.split("<")[0]
@@ -982,8 +1045,6 @@ def main(argv=None):
                     help="skip the full-feature (D, z, dt_bias, initial states, dt_limit) timings")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run 3 plain 1 GiB device copies (counter calibration for rocprofv3 --pmc)")
-    ap.add_argument("--cpu-budget", type=float, default=20.0,
-                    help="approximate seconds of CPU-oracle work for the baseline")
     ap.add_argument("--summarize-profile", nargs=3, metavar=("TRACE_DIR", "FETCH_DIR", "WRITE_DIR"),
                     help="print a markdown summary of rocprofv3 csv output and exit (no GPU)")
     ap.add_argument("--traffic-json", help="with --summarize-profile: also write per-kernel traffic")
@@ -1024,9 +1085,9 @@ def main(argv=None):
     log(f"device {dev.name} ({getattr(dev, 'gcnArchName', '?')}), config C{args.config} {shape}, "
         f"seed {seed}")
 
-    inp = make_gpu_inputs(torch, shape, seed)
-    torch.cuda.synchronize()
-    log("inputs ready; forward warmup + timed steps")
+    cpu_inp = make_cpu_inputs(torch, shape, seed)
+    inp = to_gpu(torch, cpu_inp)
+    log("inputs ready (CPU generator, copied to the GPU); forward warmup + timed steps")
     res, names, wall_ms, finite, ws_bytes, out, final = bench_forward(
         torch, lib, rt, api, hip, inp, shape, args.steps, args.warmup)
     step_ms = [r[0] for r in res]
@@ -1047,7 +1108,9 @@ def main(argv=None):
         log(f"  {name:<16} avg {avg:8.4f} ms  {kern[name]['GB_s']:8.1f} GB/s  "
             f"{kern[name]['TFLOP_s']:7.2f} TFLOP/s")
     log(f"forward median {fwd_ms:.4f} ms (wall {wall_ms / args.steps:.4f} ms/step), finite={finite}")
-    parity = parity_slices(torch, inp, out, final, shape, PARITY_SLICES[args.config])
+    fwd_stats = summarize(step_ms)
+    out_sums = checksums(torch, {"out": out, "final": final})[0]
+    parity = parity_slices(torch, cpu_inp, out, final, shape, PARITY_SLICES[args.config])
     log(f"same-run parity vs the CPU oracle on {parity['slices']}: out maxabs {parity['out_maxabs']:.3e} "
         f"relL2 {parity['out_relL2']:.3e}, final maxabs {parity['final_maxabs']:.3e} relL2 "
         f"{parity['final_relL2']:.3e} -> {'pass' if parity['pass'] else 'FAIL'}")
@@ -1059,6 +1122,7 @@ def main(argv=None):
     fwd_bwd_ms, bwd_note, api_fwd_bwd_ms, bwd_kern, bwd_ms = None, "skipped (--no-bwd)", None, {}, None
     memory = None
     fwd_train_ms = None
+    train_stats, grad_sums = {}, None
     if not args.no_bwd:
         tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, args.steps, args.warmup)
         if tr is None:
@@ -1068,6 +1132,9 @@ def main(argv=None):
             bwd_ms = statistics.median(r[0] for r in bres)
             fwd_train_ms = statistics.median(r[0] for r in fres)
             fwd_bwd_ms = statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres))
+            train_stats = {"fwd_train": summarize(r[0] for r in fres), "bwd": summarize(r[0] for r in bres),
+                           "fwd_bwd": summarize(f[0] + bk[0] for f, bk in zip(fres, bres))}
+            grad_sums = {"gradient_checksums": tr[6][0], "gradient_checksum": tr[6][1]}
             bwd_note = ("C-ABI training fwd (saves chunk-start states) + M1 bwd, loss "
                         f"mean(y^2)+mean(final^2), grads finite={bfinite}")
             log(f"training forward (saving chunk states) median {fwd_train_ms:.4f} ms")
@@ -1113,12 +1180,13 @@ def main(argv=None):
         # the same call path without ids, timed back to back with the packed
         # calls, so the pair shows the masks' cost under the same conditions
         plain = bench_fwd_features(torch, lib, rt, inp, shape, None, nfs, 3)
+        pk = bench_fwd_features(torch, lib, rt, inp, shape, None, nfs, 3, seq=seq)
         packed = {"ids": "every row cut into sequences of U[256, 2048) tokens",
                   "nseqs": int((seq[:, 1:] != seq[:, :-1]).sum().item()) + shape[0],
-                  "fwd_ms": round(bench_fwd_features(torch, lib, rt, inp, shape, None, nfs, 3, seq=seq), 5),
-                  "fwd_ms_without_ids": round(plain, 5)}
+                  "fwd_ms": pk["median_ms"], "fwd": pk,
+                  "fwd_ms_without_ids": plain["median_ms"], "fwd_without_ids": plain}
         log(f"packed sequences ({packed['nseqs']}): forward median {packed['fwd_ms']:.4f} ms "
-            f"(same path without ids {plain:.4f} ms)")
+            f"(same path without ids {plain['median_ms']:.4f} ms)")
         if not args.no_bwd:
             tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, nfs, 3, seq=seq)
             if tr is not None:
@@ -1126,7 +1194,11 @@ def main(argv=None):
                 packed["fwd_train_ms"] = round(statistics.median(r[0] for r in fres), 5)
                 packed["bwd_ms"] = round(statistics.median(r[0] for r in bres), 5)
                 packed["fwd_bwd_ms"] = round(statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres)), 5)
+                packed["fwd_train"] = summarize(r[0] for r in fres)
+                packed["bwd"] = summarize(r[0] for r in bres)
+                packed["fwd_bwd"] = summarize(f[0] + bk[0] for f, bk in zip(fres, bres))
                 packed["grads_finite"] = bool(tr[3])
+                packed["gradient_checksums"], packed["gradient_checksum"] = tr[6]
                 log(f"packed sequences: training forward {packed['fwd_train_ms']:.4f} ms, bwd "
                     f"{packed['bwd_ms']:.4f} ms, fwd+bwd {packed['fwd_bwd_ms']:.4f} ms")
         del seq
@@ -1136,8 +1208,9 @@ def main(argv=None):
         # the reference's headline feature set on the same shape
         feats = full_features(torch, shape, seed)
         nfs = max(5, args.steps // 3)
+        ff = bench_fwd_features(torch, lib, rt, inp, shape, feats, nfs, 3)
         full = {"features": "D [H,P], z, dt_bias, initial_states, softplus, dt_limit (1e-3, 1)",
-                "fwd_ms": round(bench_fwd_features(torch, lib, rt, inp, shape, feats, nfs, 3), 5)}
+                "fwd_ms": ff["median_ms"], "fwd": ff}
         log(f"full features: forward median {full['fwd_ms']:.4f} ms")
         if not args.no_bwd:
             tr = bench_fwd_bwd_traced(torch, lib, rt, hip, inp, shape, nfs, 3, feats)
@@ -1146,7 +1219,11 @@ def main(argv=None):
                 full["fwd_train_ms"] = round(statistics.median(r[0] for r in fres), 5)
                 full["bwd_ms"] = round(statistics.median(r[0] for r in bres), 5)
                 full["fwd_bwd_ms"] = round(statistics.median(f[0] + bk[0] for f, bk in zip(fres, bres)), 5)
+                full["fwd_train"] = summarize(r[0] for r in fres)
+                full["bwd"] = summarize(r[0] for r in bres)
+                full["fwd_bwd"] = summarize(f[0] + bk[0] for f, bk in zip(fres, bres))
                 full["grads_finite"] = bool(tr[3])
+                full["gradient_checksums"], full["gradient_checksum"] = tr[6]
                 log(f"full features: training forward {full['fwd_train_ms']:.4f} ms, bwd "
                     f"{full['bwd_ms']:.4f} ms, fwd+bwd {full['fwd_bwd_ms']:.4f} ms")
         del feats
@@ -1175,7 +1252,7 @@ def main(argv=None):
         for cfg in sorted(CONFIGS):
             if cfg == args.config:
                 continue
-            row = bench_config(torch, lib, rt, api, hip, cfg, args.steps, args.warmup)
+            row = bench_config(torch, lib, rt, api, hip, cfg, args.steps, args.warmup, cpu=not args.no_cpu)
             others[f"C{cfg}"] = row
             log(f"config C{cfg} {row['shape']}: forward {row['fwd_ms']:.4f} ms (public API "
                 f"{row['api_fwd_ms']:.4f} ms per call, {row['api_host_us']:.0f} us of host work per call), "
@@ -1201,9 +1278,10 @@ def main(argv=None):
 
     cpu = None
     if not args.no_cpu:
-        log("CPU oracle baseline (bounded sample)")
-        cpu = cpu_baseline(torch, shape, seed, args.cpu_budget)
-        log(f"cpu baseline {cpu['value']:.1f} ms (scaled), {cpu['cores']} threads")
+        log(f"CPU oracle baseline: the whole C{args.config} forward on the same inputs")
+        cpu = cpu_oracle_baseline(torch, cpu_inp, shape, seed)
+        log(f"cpu baseline {cpu['value']:.1f} ms (median of {cpu['stats']['n']}), {cpu['cores']} threads")
+    del cpu_inp
 
     line = {
         "metric": METRIC,
@@ -1217,13 +1295,18 @@ def main(argv=None):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded GPU generator; x,B,C~N(0,1), dt~U[0,1), A=-U[0,1))",
+        "data": ("synthetic (seeded CPU generator, copied to the GPU; x,B,C~N(0,1), dt~U[0,1), "
+                 "A=-U[0,1))"),
         "config": {
             "workload": f"C{args.config} SSD forward [B,L,H,P,N,chunk,G]={shape}, dt_softplus, "
                         "final state, fp32 public tensors, split-fp16 MFMA operands",
             "shape": shape,
             "seed": seed,
         },
+        "fwd": fwd_stats,
+        "output_checksums": out_sums,
+        **train_stats,
+        **(grad_sums or {}),
         "fwd_bwd_ms": None if fwd_bwd_ms is None else round(fwd_bwd_ms, 5),
         "fwd_train_ms": None if fwd_train_ms is None else round(fwd_train_ms, 5),
         "bwd_ms": None if bwd_ms is None else round(bwd_ms, 5),

@@ -36,6 +36,8 @@ def test_traced_names_map_to_distinct_models():
     assert key("k_fwd_seg<false, false, true, false>") == "k_fwd_seg_gate"
     assert key("k_fwd_seg<false, true, true, true>") == "k_fwd_seg_save_gate_seq"
     assert key("k_fwd_seg<true, false, false, true>") == "k_fwd_seg_state_seq"
+    # the backward's recompute pass writes the chunk states: its own model
+    assert key("k_fwd_seg<true, true, false, false>") == "k_fwd_seg_state_save"
     assert key("k_bwd_ws<false, 4, false>") == "k_bwd_ws_rev"
     assert key("k_bwd_ws<true, 2, false>") == "k_bwd_ws_rev_z"
     assert key("k_bwd_ws<false, 4, true>") == "k_bwd_ws_rev_seq"
@@ -50,3 +52,20 @@ def test_traced_names_map_to_distinct_models():
     for name in ("k_fwd_seg_gate", "k_fwd_seg_save_gate", "k_bwd_ws_rev", "k_bwd_ws_rev_z", "k_fwd_wide",
                  "k_fwd_wide_gate"):
         assert not math.isnan(bench.fwd_kernel_model(name, shape)["bytes"]), name
+
+
+def test_recompute_pass_model_counts_the_state_writes():
+    """k_fwd_seg<state only, save> reads x, dt and B and writes the state
+    entering every chunk: 4 (T P + T + T N / R + P N) bytes per unit (4.87 GB
+    at C3, of which 2.15 GB are the states)."""
+    shape = bench.CONFIGS[3]
+    st = bench.fwd_kernel_model("k_fwd_seg_state", shape)
+    sv = bench.fwd_kernel_model("k_fwd_seg_state_save", shape)
+    assert sv["bytes"] - st["bytes"] == 4 * 64 * 64 * sv["units"]
+    assert math.isclose(sv["bytes"] / 1e9, 4.865, rel_tol=1e-3)
+
+
+def test_summary_statistics():
+    s = bench.summarize([5.0, 1.0, 3.0, 2.0, 4.0, 6.0, 7.0, 8.0, 9.0, 10.0])
+    assert s["median_ms"] == 5.5 and s["min_ms"] == 1.0 and s["max_ms"] == 10.0
+    assert s["p90_ms"] == 9.0 and s["n"] == 10 and s["mean_ms"] == 5.5
