@@ -518,6 +518,12 @@ __device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int lane_b
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, uniform_bytes, 0));
 }
 
+// The same marked non-temporal (cache-policy bit nt): data read once, which
+// should not displace lines other workgroups still read from L2.
+__device__ __forceinline__ float4 buf_load4_nt(__amdgpu_buffer_rsrc_t r, int lane_bytes, int uniform_bytes) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, uniform_bytes, 2));
+}
+
 // The wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 

@@ -259,7 +259,12 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         const int xlast = (tv - 1) * rowHP4, blast = (tv - 1) * rowGN4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            xr[sl][j] = buf_load4(rx, min(xrow_off[j], xlast) + c4 * 4, 0);
+            // the backward's recompute pass (two workgroups per CU, four
+            // rounds at C3) reads x non-temporally, so the B rows the group's
+            // other heads read stay in L2 (2 % faster there; the segment
+            // pre-passes of few streams ran 10 % slower with it)
+            const int xo = min(xrow_off[j], xlast) + c4 * 4;
+            xr[sl][j] = (kStateOnly && kSave) ? buf_load4_nt(rx, xo, 0) : buf_load4(rx, xo, 0);
             br[sl][j] = buf_load4(rb, min(brow_off[j], blast) + c4 * 4, 0);
         }
         const auto rdt = buf_rsrc(prm.dt + ((int64_t)b * prm.L + t0) * Hr + hr);
@@ -554,16 +559,27 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     float wv[2][8];
     #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        f32x4 cb = zero4();
-                        if (j <= W)
+                        if (j > W) { // above the diagonal: zero (compile-time)
     #pragma unroll
-                            for (int ks = 0; ks < 2; ++ks)
-                                cb = mma3f(frag_s<kXS>(t1, 16 * j + r16, ks), Cown[ks], cb);
+                            for (int i = 0; i < 4; ++i) wv[j >> 1][(j & 1) * 4 + i] = 0.f;
+                            continue;
+                        }
+                        f32x4 cb = zero4();
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ++ks)
+                            cb = mma3f(frag_s<kXS>(t1, 16 * j + r16, ks), Cown[ks], cb);
+                        // cs and q of tokens 16 j + 4 kq .. + 3, read
+                        // unconditionally (two 16-byte reads) and the causal
+                        // zeros of the diagonal block selected per lane: a
+                        // conditional read would become a divergent branch
+                        // that drains every LDS read in flight
+                        const float4 csv = *(const float4 *)&s_cs[s][16 * j + 4 * kq];
+                        const float4 qv = *(const float4 *)&s_q[s][16 * j + 4 * kq];
+                        const float csa[4] = {csv.x, csv.y, csv.z, csv.w}, qa[4] = {qv.x, qv.y, qv.z, qv.w};
     #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const int so = 16 * j + 4 * kq + i;
-                            const float e = (j <= W && so <= own) ? exp2_f(cs_w - s_cs[s][so]) * s_q[s][so] : 0.f;
-                            wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
+                            const float e = exp2_f(cs_w - csa[i]) * qa[i];
+                            wv[j >> 1][(j & 1) * 4 + i] = (j < W || 4 * kq + i <= r16) ? cb[i] * e : 0.f;
                         }
                     }
                     // packed sequences: C_t . B_s only between equal ids, applied
@@ -582,6 +598,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     WT[0] = pack_frag(wv[0]);
                     WT[1] = pack_frag(wv[1]);
                 }
+                // the mask chain (C.B^T, exponentials, W^T split) is scheduled
+                // as a phase of its own, ahead of the C.S, W.x and U products:
+                // interleaving them in one block ran the C3 forward 5 % slower,
+                // this fence 1.3 % faster than the branchy mask it replaces
+                __builtin_amdgcn_sched_barrier(0);
                 // 2^-eo y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] q_s x_s (S held
                 // as S 2^-eS, W built in the scale 2^-eo)
                 f32x4 acc[4];
@@ -618,28 +639,41 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 }
                 if (kFull || own < tv) {
                     const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P;
+                    // one wave-uniform branch per feature for the whole row
+                    // (not one per 16-channel block, which splits the step
+                    // into small blocks the scheduler cannot overlap)
+                    f32x4 v[4];
+    #pragma unroll
+                    for (int pb = 0; pb < 4; ++pb) v[pb] = acc[pb];
+                    if (prm.has_D) {
+    #pragma unroll
+                        for (int pb = 0; pb < 4; ++pb) {
+                            const int p = 16 * pb + 4 * kq;
+                            const f32x4 xa = tile_row4_s<kXS>(t2, own, p); // x from the staged tile
+                            const float4 d = *(const float4 *)&s_Dv[p];
+                            v[pb][0] += d.x * xa[0];
+                            v[pb][1] += d.y * xa[1];
+                            v[pb][2] += d.z * xa[2];
+                            v[pb][3] += d.w * xa[3];
+                        }
+                    }
+                    if (prm.pre_gate) {
+    #pragma unroll
+                        for (int pb = 0; pb < 4; ++pb)
+                            *(float4 *)(prm.pre_gate + row + 16 * pb + 4 * kq) =
+                                make_float4(v[pb][0], v[pb][1], v[pb][2], v[pb][3]);
+                    }
     #pragma unroll
                     for (int pb = 0; pb < 4; ++pb) {
-                        const int p = 16 * pb + 4 * kq;
-                        float4 v = make_float4(acc[pb][0], acc[pb][1], acc[pb][2], acc[pb][3]);
-                        if (prm.has_D) {
-                            const f32x4 xa = tile_row4_s<kXS>(t2, own, p); // x from the staged tile
-                            const float4 xv = make_float4(xa[0], xa[1], xa[2], xa[3]);
-                            const float4 d = *(const float4 *)&s_Dv[p];
-                            v.x += d.x * xv.x;
-                            v.y += d.y * xv.y;
-                            v.z += d.z * xv.z;
-                            v.w += d.w * xv.w;
-                        }
-                        if (prm.pre_gate) *(float4 *)(prm.pre_gate + row + p) = v;
                         if (kGate) {
                             const float4 zv = zr[pb];
-                            v.x *= silu_f(zv.x);
-                            v.y *= silu_f(zv.y);
-                            v.z *= silu_f(zv.z);
-                            v.w *= silu_f(zv.w);
+                            v[pb][0] *= silu_f(zv.x);
+                            v[pb][1] *= silu_f(zv.y);
+                            v[pb][2] *= silu_f(zv.z);
+                            v[pb][3] *= silu_f(zv.w);
                         }
-                        *(float4 *)(prm.out + row + p) = v;
+                        *(float4 *)(prm.out + row + 16 * pb + 4 * kq) =
+                            make_float4(v[pb][0], v[pb][1], v[pb][2], v[pb][3]);
                     }
                 }
                 z_load(k + 1);

@@ -478,19 +478,30 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
                 float wv[2][8];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
+                    if (j > W) { // above the diagonal: zero (compile-time)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) wv[j >> 1][(j & 1) * 4 + i] = 0.f;
+                        continue;
+                    }
                     f32x4 cb = zero4();
                     if (kCB) {
-                        if (j <= W) cb = f32x4{cbv[j].x, cbv[j].y, cbv[j].z, cbv[j].w};
-                    } else if (j <= W) {
+                        cb = f32x4{cbv[j].x, cbv[j].y, cbv[j].z, cbv[j].w};
+                    } else {
 #pragma unroll
                         for (int ks = 0; ks < 4; ++ks)
                             cb = mma3f(frag_s<kS1>(t1, 16 * j + r16, ks), Cown[ks], cb);
                     }
+                    // cs and q of tokens 16 j + 4 kq .. + 3 read unconditionally
+                    // and the diagonal block's causal zeros selected per lane
+                    // (a conditional read becomes a divergent branch that drains
+                    // every LDS read in flight)
+                    const float4 csv = *(const float4 *)&s_cs[s][16 * j + 4 * kq];
+                    const float4 qv = *(const float4 *)&s_q[s][16 * j + 4 * kq];
+                    const float csa[4] = {csv.x, csv.y, csv.z, csv.w}, qa[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int so = 16 * j + 4 * kq + i;
-                        const float e = (j <= W && so <= own) ? exp2_f(cs_w - s_cs[s][so]) * s_q[s][so] : 0.f;
-                        wv[j >> 1][(j & 1) * 4 + i] = cb[i] * e;
+                        const float e = exp2_f(cs_w - csa[i]) * qa[i];
+                        wv[j >> 1][(j & 1) * 4 + i] = (j < W || 4 * kq + i <= r16) ? cb[i] * e : 0.f;
                     }
                 }
                 if (kSeq && s_mixed[s]) {
@@ -540,27 +551,37 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             }
             if (kFull || own < tv) {
                 const int64_t row = (((int64_t)b * prm.L + t0 + own) * H + h) * P + p0;
+                // one wave-uniform branch per feature for the whole row
+                f32x4 v[2] = {acc[0], acc[1]};
+                if (prm.has_D) {
 #pragma unroll
-                for (int pb = 0; pb < 2; ++pb) {
-                    const int p = 16 * pb + 4 * kq;
-                    float4 v = make_float4(acc[pb][0], acc[pb][1], acc[pb][2], acc[pb][3]);
-                    if (prm.has_D) {
+                    for (int pb = 0; pb < 2; ++pb) {
+                        const int p = 16 * pb + 4 * kq;
                         const f32x4 xa = tile_row4_s<kS2>(t2, own, p);
                         const float4 d = *(const float4 *)&s_Dv[p];
-                        v.x += d.x * xa[0];
-                        v.y += d.y * xa[1];
-                        v.z += d.z * xa[2];
-                        v.w += d.w * xa[3];
+                        v[pb][0] += d.x * xa[0];
+                        v[pb][1] += d.y * xa[1];
+                        v[pb][2] += d.z * xa[2];
+                        v[pb][3] += d.w * xa[3];
                     }
-                    if (prm.pre_gate) *(float4 *)(prm.pre_gate + row + p) = v;
+                }
+                if (prm.pre_gate) {
+#pragma unroll
+                    for (int pb = 0; pb < 2; ++pb)
+                        *(float4 *)(prm.pre_gate + row + 16 * pb + 4 * kq) =
+                            make_float4(v[pb][0], v[pb][1], v[pb][2], v[pb][3]);
+                }
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb) {
                     if (kGate) {
                         const float4 zv = zr[pb];
-                        v.x *= silu_f(zv.x);
-                        v.y *= silu_f(zv.y);
-                        v.z *= silu_f(zv.z);
-                        v.w *= silu_f(zv.w);
+                        v[pb][0] *= silu_f(zv.x);
+                        v[pb][1] *= silu_f(zv.y);
+                        v[pb][2] *= silu_f(zv.z);
+                        v[pb][3] *= silu_f(zv.w);
                     }
-                    *(float4 *)(prm.out + row + p) = v;
+                    *(float4 *)(prm.out + row + 16 * pb + 4 * kq) =
+                        make_float4(v[pb][0], v[pb][1], v[pb][2], v[pb][3]);
                 }
             }
             z_load(k + 1);
