@@ -102,6 +102,52 @@ __device__ __forceinline__ int xcd_unit(int id, int total, int R) {
 
 constexpr int kWsThreads = 512; // 4 producer + 4 consumer waves
 
+// Ownership of the state in the full pass: the 16 tiles (16 x 16 blocks,
+// n-block nb, p-block pb) of S, and with them the U products, the state
+// update and the T4 staging, over the four consumer waves.  Wave W also forms
+// the causal C.B^T blocks j <= W of its token rows, so the later waves carry
+// more of the mask work; a split (c0, c1, c2, c3) other than (4, 4, 4, 4)
+// hands tiles of the later waves' n-blocks to the earlier waves.  Measured
+// at C3 (plain forward, one box, A/B): 4444 1.342 ms, 5533 1.335, 5542 1.329,
+// 6532 1.326; at C4 0.0330 -> 0.0325 ms.  A phase-timestamp probe of one
+// workgroup put wave 3's mask phase at 2.5x wave 0's and wave 0 idle at the
+// barrier for a quarter of the step, but moving tiles gains far less than
+// that imbalance: the waves also contend for the CU's LDS, VALU issue and
+// vector-memory paths (each 20-40 % busy).  The z-gate and packed-sequence
+// variants keep 4444 (6532 spills 12-24 bytes there).
+struct TileMap {
+    int n[4];
+    int nb[4][8], pb[4][8];
+};
+constexpr TileMap make_tiles(int c0, int c1, int c2, int c3) {
+    TileMap m{};
+    const int want[4] = {c0, c1, c2, c3};
+    int snb[16] = {}, spb[16] = {}, ns = 0;
+    for (int w = 0; w < 4; ++w)
+        for (int p = 0; p < 4; ++p) {
+            if (p < want[w]) {
+                m.nb[w][m.n[w]] = w;
+                m.pb[w][m.n[w]] = p;
+                ++m.n[w];
+            } else {
+                snb[ns] = w;
+                spb[ns] = p;
+                ++ns;
+            }
+        }
+    int t = 0;
+    for (int w = 0; w < 4; ++w)
+        while (m.n[w] < want[w] && t < ns) {
+            m.nb[w][m.n[w]] = snb[t];
+            m.pb[w][m.n[w]] = spb[t];
+            ++m.n[w];
+            ++t;
+        }
+    return m;
+}
+constexpr TileMap kTilesEven = make_tiles(4, 4, 4, 4);
+constexpr TileMap kTilesShifted = make_tiles(6, 5, 3, 2);
+
 // State entering segment sg when the segment recurrence is folded into the
 // full pass (sp.seg_in_log_decay non-NULL): with U_j the contribution of
 // pre-segment j (from a zero state) and ld_j its log decay,
@@ -399,10 +445,17 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     auto consumer = [&](auto wave_c) {
         constexpr int W = decltype(wave_c)::value;
         const int own = 16 * W + r16; // token row of this lane
-        // state: Sr[pb][i] = S[p = 16 pb + l % 16][n = 16 W + 4 (l / 16) + i]
-        // 2^-eS (eS = kZeroState while the state is zero; every consumer wave
-        // forms the same eS, and the producers the same sequence)
-        f32x4 Sr[4];
+        // state: Sr[i][r] = S[p = 16 tpb(i) + l % 16][n = 16 tnb(i) + 4 (l / 16) + r]
+        // 2^-eS for this wave's NT tiles (eS = kZeroState while the state is
+        // zero; every consumer wave forms the same eS, and the producers the
+        // same sequence).  The state-only pass keeps n-block W.
+        constexpr TileMap tm = (kGate || kSeq) ? kTilesEven : kTilesShifted;
+        constexpr int NT = kStateOnly ? 4 : tm.n[W];
+        auto tnb = [](int i) { return kStateOnly ? W : tm.nb[W][i]; };
+        auto tpb = [](int i) { return kStateOnly ? i : tm.pb[W][i]; };
+        // offset of tile i's four values within a [P, NS] state
+        auto toff = [&](int i) { return (16 * tpb(i) + r16) * NS + 16 * tnb(i) + 4 * kq; };
+        f32x4 Sr[NT];
         int eS = kZeroState;
         // C row `own` of the next two chunks: chunk k in cr[(k - kbeg) & 1],
         // loaded two chunks ahead
@@ -440,11 +493,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         auto write_T4 = [&](int s) {
             const SplitTile t4 = T4(s);
     #pragma unroll
-            for (int pb = 0; pb < 4; ++pb) {
+            for (int i = 0; i < NT; ++i) {
                 half4 hh, ll;
-                split4(make_float4(Sr[pb][0], Sr[pb][1], Sr[pb][2], Sr[pb][3]), hh, ll);
-                *(half4 *)&t4.hi[(16 * pb + r16) * kTS + 16 * W + 4 * kq] = hh;
-                *(half4 *)&t4.lo[(16 * pb + r16) * kTS + 16 * W + 4 * kq] = ll;
+                split4(make_float4(Sr[i][0], Sr[i][1], Sr[i][2], Sr[i][3]), hh, ll);
+                *(half4 *)&t4.hi[(16 * tpb(i) + r16) * kTS + 16 * tnb(i) + 4 * kq] = hh;
+                *(half4 *)&t4.lo[(16 * tpb(i) + r16) * kTS + 16 * tnb(i) + 4 * kq] = ll;
             }
         };
 
@@ -453,8 +506,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             const int64_t bh = (int64_t)b * H + h;
             if ((!kStateOnly || kSave) && sp.seg_in && sp.seg_in_log_decay) {
                 fold_entry(Sr, sp.seg_in + bh * sp.seg_in_n * PNS + n0, sp.seg_in_log_decay + bh * sp.seg_in_n,
-                           sg * sp.in_mult, PNS, prm.init ? prm.init + bh * PNS + n0 : nullptr,
-                           [&](int pb) { return (16 * pb + r16) * NS + 16 * W + 4 * kq; });
+                           sg * sp.in_mult, PNS, prm.init ? prm.init + bh * PNS + n0 : nullptr, toff);
             } else {
                 if (!kStateOnly || kSave) {
                     if (sp.seg_in)
@@ -463,12 +515,12 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                         s0 = prm.init + bh * PNS + n0;
                 }
     #pragma unroll
-                for (int pb = 0; pb < 4; ++pb) {
+                for (int i = 0; i < NT; ++i) {
                     if (s0) {
-                        const float4 v = *(const float4 *)(s0 + (16 * pb + r16) * NS + 16 * W + 4 * kq);
-                        Sr[pb] = f32x4{v.x, v.y, v.z, v.w};
+                        const float4 v = *(const float4 *)(s0 + toff(i));
+                        Sr[i] = f32x4{v.x, v.y, v.z, v.w};
                     } else {
-                        Sr[pb] = zero4();
+                        Sr[i] = zero4();
                     }
                 }
             }
@@ -478,17 +530,17 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 // the producers, which read the same maxima)
                 float m = 0.f;
     #pragma unroll
-                for (int pb = 0; pb < 4; ++pb)
+                for (int i = 0; i < NT; ++i)
     #pragma unroll
-                    for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(Sr[pb][i]));
+                    for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(Sr[i][r]));
                 m = wave_max(m);
                 if (lane == 0) s_smax[W] = m;
                 lds_barrier();
                 eS = state_exp_of(s_smax);
     #pragma unroll
-                for (int pb = 0; pb < 4; ++pb)
+                for (int i = 0; i < NT; ++i)
     #pragma unroll
-                    for (int i = 0; i < 4; ++i) Sr[pb][i] = __builtin_amdgcn_ldexpf(Sr[pb][i], -eS);
+                    for (int r = 0; r < 4; ++r) Sr[i][r] = __builtin_amdgcn_ldexpf(Sr[i][r], -eS);
             }
             if (!kStateOnly) {
                 write_T4(0);
@@ -529,14 +581,13 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * PNS + n0;
                 const float f = __builtin_amdgcn_ldexpf(1.f, eS);
     #pragma unroll
-                for (int pb = 0; pb < 4; ++pb)
-                    *(float4 *)(cst + (16 * pb + r16) * NS + 16 * W + 4 * kq) =
-                        make_float4(Sr[pb][0] * f, Sr[pb][1] * f, Sr[pb][2] * f, Sr[pb][3] * f);
+                for (int i = 0; i < NT; ++i)
+                    *(float4 *)(cst + toff(i)) = make_float4(Sr[i][0] * f, Sr[i][1] * f, Sr[i][2] * f, Sr[i][3] * f);
             }
             const SplitTile t2 = T2(s), t3 = T3(s);
-            f32x4 U[4];
+            f32x4 U[NT];
     #pragma unroll
-            for (int pb = 0; pb < 4; ++pb) U[pb] = zero4();
+            for (int i = 0; i < NT; ++i) U[i] = zero4();
             if (!kStateOnly) {
                 Frag Cown[2];
     #pragma unroll
@@ -619,15 +670,20 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                 for (int pb = 0; pb < 4; ++pb)
     #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[pb][i] *= ecs;
-                // each x fragment feeds both y^T (W part) and U^T
+                // each x fragment feeds both y^T (W part) and U^T; the
+                // decayed-B fragment of every n-block this wave's tiles use
     #pragma unroll
                 for (int m = 0; m < 2; ++m) {
-                    const Frag a3 = frag_tp_s<kXS>(t3, m, 16 * W);
+                    Frag a3[4];
+    #pragma unroll
+                    for (int i = 0; i < NT; ++i) a3[tnb(i)] = frag_tp_s<kXS>(t3, m, 16 * tnb(i));
     #pragma unroll
                     for (int pb = 0; pb < 4; ++pb) {
                         const Frag f2 = frag_tp_s<kXS>(t2, m, 16 * pb);
                         if (2 * m <= W) acc[pb] = mma3f(f2, WT[m], acc[pb]);
-                        U[pb] = mma3f(a3, f2, U[pb]);
+    #pragma unroll
+                        for (int i = 0; i < NT; ++i)
+                            if (tpb(i) == pb) U[i] = mma3f(a3[tnb(i)], f2, U[i]);
                     }
                 }
                 {
@@ -686,7 +742,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     for (int m = 0; m < 2; ++m) {
                         const Frag a3 = frag_tp_s<kXS>(t3, m, 16 * W);
     #pragma unroll
-                        for (int pb = 0; pb < 4; ++pb) U[pb] = mma3f(a3, frag_tp_s<kXS>(t2, m, 16 * pb), U[pb]);
+                        for (int i = 0; i < NT; ++i) U[i] = mma3f(a3, frag_tp_s<kXS>(t2, m, 16 * tpb(i)), U[i]);
                     }
                 }
                 // S' 2^-eN = exp2(cs_last) 2^(eS - eN) (S 2^-eS) + U 2^-eN (T3's scale)
@@ -694,9 +750,9 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                                                             eS - eN);
                 if (kSeq) seg_carry *= s_carry[s];
     #pragma unroll
-                for (int pb = 0; pb < 4; ++pb)
+                for (int i = 0; i < NT; ++i)
     #pragma unroll
-                    for (int i = 0; i < 4; ++i) Sr[pb][i] = alpha * Sr[pb][i] + U[pb][i];
+                    for (int r = 0; r < 4; ++r) Sr[i][r] = alpha * Sr[i][r] + U[i][r];
                 eS = eN;
             }
             if (!kStateOnly) write_T4(s ^ 1);
@@ -728,9 +784,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
         if (dst) {
             const float f = __builtin_amdgcn_ldexpf(1.f, eS);
     #pragma unroll
-            for (int pb = 0; pb < 4; ++pb)
-                *(float4 *)(dst + (16 * pb + r16) * NS + 16 * W + 4 * kq) =
-                    make_float4(Sr[pb][0] * f, Sr[pb][1] * f, Sr[pb][2] * f, Sr[pb][3] * f);
+            for (int i = 0; i < NT; ++i)
+                *(float4 *)(dst + toff(i)) = make_float4(Sr[i][0] * f, Sr[i][1] * f, Sr[i][2] * f, Sr[i][3] * f);
         }
     };
     switch (w) {
