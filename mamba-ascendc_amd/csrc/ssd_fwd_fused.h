@@ -217,6 +217,10 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     // from one base (see the prologue).
     struct ChunkTok {
         float cs[2][T], q[2][T];
+        // q_s 2^-ek exp2(cs_e - cs_s), e the last token of s's 16-token block:
+        // the blocks below the diagonal take exp2(cs_t - cs_s) q_s as
+        // exp2(cs_t - cs_e) times this (both factors <= 1)
+        float gq[2][T];
         // kSeq: token ids, 1 where the token reads the entering state
         int sid[2][TS];
         float off[2][TS];
@@ -365,7 +369,11 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
             }
             cut = e_end != e_prev;
         }
-        if (w == 0) tk->q[s][lane] = __builtin_amdgcn_ldexpf(q, -ek_tok);
+        if (w == 0) {
+            const float qs = __builtin_amdgcn_ldexpf(q, -ek_tok);
+            tk->q[s][lane] = qs;
+            if (!kStateOnly) tk->gq[s][lane] = exp2_f(dpp_f<0x15F>(cs) - cs) * qs;
+        }
         // the state leaving the chunk is held as S 2^-eN: every producer wave
         // runs this recurrence, and the consumers take eN from LDS
         const int eN = next_state_exp(p_eS, ek, cs_last, cut);
@@ -619,9 +627,19 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     #pragma unroll
                         for (int ks = 0; ks < 2; ++ks)
                             cb = mma3f(frag_s<kXS>(t1, 16 * j + r16, ks), Cown[ks], cb);
-                        // cs and q of tokens 16 j + 4 kq .. + 3, read
-                        // unconditionally (two 16-byte reads) and the causal
-                        // zeros of the diagonal block selected per lane: a
+                        if (j < W) {
+                            // below the diagonal: one exponential per block
+                            // (the decay from the block's last token to t)
+                            const float fe = exp2_f(cs_w - s_cs[s][16 * j + 15]);
+                            const float4 gv = *(const float4 *)&s_tok.gq[s][16 * j + 4 * kq];
+                            const float ga[4] = {gv.x, gv.y, gv.z, gv.w};
+    #pragma unroll
+                            for (int i = 0; i < 4; ++i) wv[j >> 1][(j & 1) * 4 + i] = cb[i] * (fe * ga[i]);
+                            continue;
+                        }
+                        // the diagonal block: cs and q of tokens 16 j + 4 kq
+                        // .. + 3, read unconditionally (two 16-byte reads),
+                        // and the causal zeros selected per lane: a
                         // conditional read would become a divergent branch
                         // that drains every LDS read in flight
                         const float4 csv = *(const float4 *)&s_cs[s][16 * j + 4 * kq];
@@ -630,7 +648,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
     #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const float e = exp2_f(cs_w - csa[i]) * qa[i];
-                            wv[j >> 1][(j & 1) * 4 + i] = (j < W || 4 * kq + i <= r16) ? cb[i] * e : 0.f;
+                            wv[j >> 1][(j & 1) * 4 + i] = (4 * kq + i <= r16) ? cb[i] * e : 0.f;
                         }
                     }
                     // packed sequences: C_t . B_s only between equal ids, applied
