@@ -614,8 +614,29 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
 
                 // W^T tiles: C_t . B_s exp2(cs_t - cs_s), s <= t, t = own
                 Frag WT[2];
+                f32x4 acc[4];
                 {
                     float wv[2][8];
+                    f32x4 cbs[4];
+    #pragma unroll
+                    for (int j = 0; j <= W; ++j) {
+                        cbs[j] = zero4();
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ++ks)
+                            cbs[j] = mma3f(frag_s<kXS>(t1, 16 * j + r16, ks), Cown[ks], cbs[j]);
+                    }
+                    // the C.S products issued between C.B^T and the mask
+                    // arithmetic, a scheduling phase of their own (C3 0.7 %
+                    // faster; without this fence the scheduler interleaves
+                    // them with the mask, C3 3.5 % slower)
+                    __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                    for (int pb = 0; pb < 4; ++pb) {
+                        acc[pb] = zero4();
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ++ks)
+                            acc[pb] = mma3f(frag(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
+                    }
     #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         if (j > W) { // above the diagonal: zero (compile-time)
@@ -623,10 +644,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                             for (int i = 0; i < 4; ++i) wv[j >> 1][(j & 1) * 4 + i] = 0.f;
                             continue;
                         }
-                        f32x4 cb = zero4();
-    #pragma unroll
-                        for (int ks = 0; ks < 2; ++ks)
-                            cb = mma3f(frag_s<kXS>(t1, 16 * j + r16, ks), Cown[ks], cb);
+                        const f32x4 cb = cbs[j];
                         if (j < W) {
                             // below the diagonal: one exponential per block
                             // (the decay from the block's last token to t)
@@ -667,21 +685,13 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     WT[0] = pack_frag(wv[0]);
                     WT[1] = pack_frag(wv[1]);
                 }
-                // the mask chain (C.B^T, exponentials, W^T split) is scheduled
-                // as a phase of its own, ahead of the C.S, W.x and U products:
-                // interleaving them in one block ran the C3 forward 5 % slower,
-                // this fence 1.3 % faster than the branchy mask it replaces
+                // the mask chain (C.B^T, C.S, exponentials, W^T split) is
+                // scheduled as a phase of its own, ahead of the W.x and U
+                // products: interleaving them in one block ran the C3 forward
+                // 5 % slower, this fence 1.3 % faster than a branchy mask
                 __builtin_amdgcn_sched_barrier(0);
                 // 2^-eo y^T[p][t]: exp2(cs_t) S C_t + sum_s W[t][s] q_s x_s (S held
-                // as S 2^-eS, W built in the scale 2^-eo)
-                f32x4 acc[4];
-    #pragma unroll
-                for (int pb = 0; pb < 4; ++pb) {
-                    acc[pb] = zero4();
-    #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks)
-                        acc[pb] = mma3f(frag(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
-                }
+                // as S 2^-eS, W built in the scale 2^-eo; acc holds S C_t)
                 const float ecs = __builtin_amdgcn_ldexpf(kSeq ? exp2_f(cs_own) * s_off[s][own] : exp2_f(cs_own),
                                                           eS - eo);
     #pragma unroll
