@@ -102,6 +102,19 @@ class HipEvents:
 
 # ----------------------------------------------------------------------------- work model
 
+def bwd_runs(shape):
+    """Runs per (b, h) stream of the reverse fused backward (mamba2_ssd.hip
+    bwd_rev_plan): with fewer than 256 (b, g) streams each is cut into about
+    256 / (B G) runs of equal length, whose own contributions the run
+    pre-pass forms."""
+    b, l, h, _p, _n, _chunk, g = shape
+    k = math.ceil(l / EXEC_CHUNK)
+    bg = b * g
+    nseg = min(-(-256 // bg), k)
+    m = math.ceil(k / nseg)
+    return math.ceil(k / m)
+
+
 def fwd_segments(shape):
     """(nseg, nseg_pre, nsplit) of the fused forward's plan (mamba2_ssd.hip
     fwd_plan): dstate 128 runs two workgroups per head; with fewer than 256
@@ -189,6 +202,12 @@ def fwd_kernel_model(name: str, shape) -> dict:
         # the state entering every chunk out
         per = f4 * (T * p + T + T * n / r + p * n)
         fl = 2 * T * p * n
+    elif name == "k_bwd_run_grad":
+        # dout, dt, C in; one state-sized contribution and log decay per run out
+        runs = b * h * bwd_runs(shape)
+        per = f4 * (T * p + T + T * n / r)
+        return {"bytes": units * per + runs * f4 * (p * n + 1), "flops": units * 2 * T * p * n,
+                "units": units, "bytes_per_unit": per}
     elif name == "k_bwd_dstate_rev":
         # dout, dt, C in; dU (state gradient leaving each chunk) out
         per = f4 * (T * p + T + T * n / r + p * n)
@@ -931,7 +950,7 @@ def model_key(short: str) -> str:
         if len(args) > 1 and args[1] != "0":
             return ("k_bwd_ws_rev_z" if args[0] == "true" else "k_bwd_ws_rev") + seq
         return "k_bwd_ws" + seq
-    return base if base in ("k_bwd_dstate_rev", "k_chunk_cb") else short
+    return base if base in ("k_bwd_dstate_rev", "k_bwd_run_grad", "k_chunk_cb") else short
 
 
 SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs

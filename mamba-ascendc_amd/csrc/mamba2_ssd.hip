@@ -581,8 +581,8 @@ constexpr int64_t kBwdUnits = 256;
 // gradients of the group's R heads in registers.  With at least kBwdUnits
 // (b, g) streams each stream is one run; with fewer, each is cut into about
 // kBwdUnits / (B G) runs of M chunks, and the gradient entering every run
-// from the right comes from a pre-pass over the same runs (k_bwd_dstate_rev
-// in segment mode: each run's own contribution and log decay) and the reverse
+// from the right comes from a pre-pass over the same runs (k_bwd_run_grad:
+// each run's own contribution and log decay) and the reverse
 // recurrence over runs (k_state_pass_bwd).  nseg = 0: other R, the split path
 // (per-chunk dU through HBM).
 struct RevPlan {
@@ -831,10 +831,9 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
             rs.M = (int)lay.rev.M;
             rs.seg_carry = (float *)(ws + lay.rev_carry);
             rs.seg_log_decay = (float *)(ws + lay.rev_decay);
-            // all R heads of a (b, g) run in one workgroup (R = 1, 2 or 4 here)
-            ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, bp.R, dim3((unsigned)(bg * nseg)), st, bp,
-                                       nullptr, nullptr, rs);
-            if (int rc = launch_status("k_bwd_dstate_rev_seg", tr, st)) return rc;
+            // each run's own contribution and log decay, one workgroup per (b, h, run)
+            ssd::launch_bwd_run_grad(bp.has_z != 0, seq, dim3((unsigned)(B * H * nseg)), st, bp, rs);
+            if (int rc = launch_status("k_bwd_run_grad", tr, st)) return rc;
             // in place: run s's slot becomes the gradient entering it from the right
             hipLaunchKernelGGL(ssd::k_state_pass_bwd, state_grid, dim3(ssd::kThreads), 0, st, rs.seg_carry,
                                rs.seg_log_decay, a->dfinal_state, (float *)nullptr, nseg, PN);
@@ -852,11 +851,8 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
     }
     // state gradients dU_k (and dinitial_states)
     if ((int64_t)B * H >= kMinRevStreams) {
-        ssd::RevSeg one{};
-        one.nseg = 1;
-        one.M = K;
-        ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, 1, dim3((unsigned)(B * H)), st, bp,
-                                   a->dfinal_state, a->dinitial_states, one);
+        ssd::launch_bwd_dstate_rev(bp.has_z != 0, seq, dim3((unsigned)(B * H)), st, bp, a->dfinal_state,
+                                   a->dinitial_states);
         if (int rc = launch_status("k_bwd_dstate_rev", tr, st)) return rc;
     } else {
         hipLaunchKernelGGL(ssd::bwd::k_bwd_dstate, chunk_grid, dim3(ssd::kThreads), 0, st, bp);

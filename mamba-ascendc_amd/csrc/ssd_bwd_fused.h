@@ -59,8 +59,8 @@ namespace bwd {
 //   dU_k = g;   g <- dSoff_k + exp(cs_last_k) g,   dSoff_k = (gy exp(cs))^T C,
 // starting from dfinal_state and ending at dinitial_states.  With nseg > 1
 // runs per stream, run sg starts from prm.carry_in (the gradient entering it
-// from the right, given by the segment pre-pass and recurrence) and only run 0
-// writes dinitial_states.
+// from the right, given by the run pre-pass k_bwd_run_grad and the recurrence
+// over runs) and only run 0 writes dinitial_states.
 //
 // kSeq: packed sequences (prm.seq_idx), the forward's masks in adjoint form:
 // W (and so dW, dCB and their dcs terms) only between equal ids, the state
@@ -823,35 +823,22 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     }
 }
 
-// Reverse state-gradient pass: each workgroup walks a run of chunks from last
-// to first with the state gradient g of kHeads heads (of one group) in
-// registers:
+// Reverse state-gradient pass: one workgroup per (b, h) walks the stream's
+// chunks from last to first with the state gradient g in registers:
 //   dU_k = g;   g <- dSoff_k + exp(cs_last_k) g,   dSoff_k = (gy exp(cs))^T C
-// Step i handles chunk kend - 1 - i / kHeads, head h0 + i % kHeads, so the
-// heads of a chunk follow each other and share its C rows (read once from
-// HBM, then from L2).  Producer waves stage gy exp(cs) and C of the next step
+// starting from g = dfinal_state; dU_k goes to prm.dstates and the final g is
+// dinitial_states (the per-chunk dS_off never reaches HBM).  Step i handles
+// chunk K - 1 - i; the R heads of a group sit on one XCD, so C of a chunk is
+// read from HBM once into its L2.  Producer waves stage gy exp(cs) and C of the next step
 // (token-major, split bf16) while the consumer waves run the product
 // dSoff^T[n][p] = sum_t C[t][n] (gy exp(cs))[t][p], read transposed from LDS.
 // The recurrence is that of mamba_ascendc/csrc/ops/mamba2_ssd_state_passing_bwd
 // (state_passing_bwd/design.md:44-61) with the dS_off product fused in.
 // kSeq: packed sequences, exp(cs_t) only for tokens that read the entering
 // state and the carry only where the state is not cut (as in k_bwd_ws).
-//
-// Whole streams (rs.seg_carry NULL, kHeads = 1): one workgroup per (b, h),
-// starting from g = dfinal_state; dU_k goes to prm.dstates and the final g is
-// dinitial_states.  The per-chunk dS_off never reaches HBM.
-//
-// Runs (rs.seg_carry non-NULL): one workgroup per (b, heads h0 .. h0 + kHeads
-// - 1, run of rs.M chunks), starting from a zero gradient and writing no
-// per-chunk dU; it leaves each head's run contribution to the gradient
-// entering the run from the right in rs.seg_carry [B, H, nseg, P, N] and the
-// run's total log decay (natural units; -inf where a packed sequence cuts the
-// state) in rs.seg_log_decay [B, H, nseg]: the pre-pass of the segmented
-// reverse fused backward.
-template <bool kHasZ, bool kSeq, int kHeads>
+template <bool kHasZ, bool kSeq>
 __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, const float *dfinal,
-                                                                float *dinit, RevSeg rs) {
-    static_assert(kHeads == 1 || kHeads == 2 || kHeads == 4, "heads per workgroup");
+                                                                float *dinit) {
     constexpr int T = 64, P = 64, N = 64;
     __shared__ __attribute__((aligned(16))) __bf16 lds[8 * kTile]; // GE(s), CT(s), s = 0, 1
     __shared__ float s_alpha[2];
@@ -860,15 +847,12 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
     const int w = wave & 3, r16 = lane & 15, kq = lane >> 4;
     auto GE = [&](int s) { return tile_at(lds, 2 * s); };
     auto CT = [&](int s) { return tile_at(lds, 2 * s + 1); };
-    // unit = ((b * G + g) * nseg + sg) * (R / kHeads) + head block
-    const int nhb = prm.R / kHeads;
-    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, nhb);
-    const int hb = u % nhb, sg = (u / nhb) % rs.nseg, bg = u / (nhb * rs.nseg);
-    const int g = bg % prm.G, b = bg / prm.G, h0 = g * prm.R + hb * kHeads;
+    // unit = (b * G + g) * R + r
+    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, prm.R);
+    const int bg = u / prm.R;
+    const int g = bg % prm.G, b = bg / prm.G, h = g * prm.R + u % prm.R;
     const int H = prm.H, G = prm.G, K = prm.K;
-    const int kbeg = sg * rs.M, kend = min(kbeg + rs.M, K);
-    const int nsteps = (kend - kbeg) * kHeads;
-    const bool segmented = rs.seg_carry != nullptr;
+    const int nsteps = K;
     const int rowHP4 = H * P * 4, rowGN4 = G * N * 4;
     auto tvalid = [&](int k) { return (int)min((int64_t)T, prm.L - (int64_t)k * T); };
 
@@ -884,13 +868,12 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         float dtr[kDepth];
         int sidr[kDepth], sprv[kDepth]; // kSeq: id of token `lane`, id of the token before the chunk
         // unconditional loads (exact wait counts): rows past the sequence end
-        // re-read its last row (zeroed when staged), steps past the run read
+        // re-read its last row (zeroed when staged), steps past chunk 0 read
         // through an empty-range resource (zeros, no traffic)
         auto p_load = [&](int i, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
             const bool real = i < nsteps;
-            const int k = real ? kend - 1 - i / kHeads : kbeg, tv = tvalid(k);
-            const int h = h0 + (real ? i % kHeads : 0);
+            const int k = real ? K - 1 - i : 0, tv = tvalid(k);
             const int range = real ? 0x7fffffff : 0;
             const int64_t t0 = (int64_t)k * T;
             const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
@@ -913,21 +896,12 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
             }
         };
         auto put = [&](SplitTile d, int row, float4 v) { store_split4(d, row * kTS + c4, v); };
-        // each head's run log2 decay and cut flag (lane 0 of producer wave 0)
-        float ld_sum[kHeads];
-        bool cut[kHeads];
-#pragma unroll
-        for (int rr = 0; rr < kHeads; ++rr) {
-            ld_sum[rr] = 0.f;
-            cut[rr] = false;
-        }
         auto p_stage = [&](int i, int s, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
             const bool real = i < nsteps;
-            const int hi = real ? i % kHeads : 0;
-            const int tv = real ? tvalid(kend - 1 - i / kHeads) : 0; // nothing valid past the run
-            const float Ah2 = prm.A[h0 + hi] * kLog2e;
-            const float bias = prm.dt_bias ? prm.dt_bias[h0 + hi] : 0.f;
+            const int tv = real ? tvalid(K - 1 - i) : 0; // nothing valid past chunk 0
+            const float Ah2 = prm.A[h] * kLog2e;
+            const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
             float a = 0.f;
             if (lane < tv) a = Ah2 * discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
             const float cs = wave_inclusive_scan(a); // log2 units
@@ -938,15 +912,7 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
                 reads = sidr[sl] == sprv[sl] ? 1.f : 0.f;
                 carry = e_end == sprv[sl] ? 1.f : 0.f;
             }
-            if (w == 0 && lane == 0) {
-                s_alpha[s] = exp2_f(cs_last) * carry;
-#pragma unroll
-                for (int rr = 0; rr < kHeads; ++rr)
-                    if (real && hi == rr) {
-                        ld_sum[rr] += cs_last;
-                        cut[rr] = cut[rr] || carry == 0.f;
-                    }
-            }
+            if (w == 0 && lane == 0) s_alpha[s] = exp2_f(cs_last) * carry;
             const float ecs = exp2_f(cs) * reads;
             const SplitTile ge = GE(s), ct = CT(s);
             // the four permutes issued back to back, ahead of every tile
@@ -996,40 +962,29 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
         }
         if (i0 < nsteps) p_iter(i0, S1{});
         if (i0 + 1 < nsteps) p_iter(i0 + 1, S2{});
-        if (segmented && w == 0 && lane == 0) {
-#pragma unroll
-            for (int rr = 0; rr < kHeads; ++rr)
-                rs.seg_log_decay[((int64_t)b * H + h0 + rr) * rs.nseg + sg] =
-                    cut[rr] ? -INFINITY : ld_sum[rr] * kLn2;
-        }
         return;
     }
 
     // -------------------------------------------------------------- consumers
-    // g[p = 16 pb + l % 16][n = 16 w + 4 (l / 16) + i] of head rr in gs[rr][pb][i]
-    f32x4 gs[kHeads][4];
+    // g[p = 16 pb + l % 16][n = 16 w + 4 (l / 16) + i] in gs[pb][i]
+    f32x4 gs[4];
     const int goff = (r16 * N + 16 * w + 4 * kq); // + 16 pb N
+    const int64_t bh = (int64_t)b * H + h;
 #pragma unroll
-    for (int rr = 0; rr < kHeads; ++rr)
-#pragma unroll
-        for (int pb = 0; pb < 4; ++pb) {
-            gs[rr][pb] = zero4();
-            if (dfinal && !segmented) {
-                const float4 v = *(const float4 *)(dfinal + ((int64_t)b * H + h0 + rr) * (P * N) + goff + 16 * pb * N);
-                gs[rr][pb] = f32x4{v.x, v.y, v.z, v.w};
-            }
+    for (int pb = 0; pb < 4; ++pb) {
+        gs[pb] = zero4();
+        if (dfinal) {
+            const float4 v = *(const float4 *)(dfinal + bh * (P * N) + goff + 16 * pb * N);
+            gs[pb] = f32x4{v.x, v.y, v.z, v.w};
         }
+    }
     lds_barrier();
-    auto c_step = [&](int i, auto rr_c) __attribute__((always_inline)) {
-        constexpr int rr = decltype(rr_c)::value;
-        const int k = kend - 1 - i / kHeads, s = i & 1;
-        if (!segmented) {
-            float *du = prm.dstates + ((((int64_t)b * H + h0 + rr) * K + k) * (P * N));
+    for (int i = 0; i < nsteps; ++i) {
+        const int k = K - 1 - i, s = i & 1;
+        float *du = prm.dstates + ((bh * K + k) * (P * N));
 #pragma unroll
-            for (int pb = 0; pb < 4; ++pb)
-                *(float4 *)(du + goff + 16 * pb * N) =
-                    make_float4(gs[rr][pb][0], gs[rr][pb][1], gs[rr][pb][2], gs[rr][pb][3]);
-        }
+        for (int pb = 0; pb < 4; ++pb)
+            *(float4 *)(du + goff + 16 * pb * N) = make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
         const SplitTile ge = GE(s), ct = CT(s);
         f32x4 U[4];
 #pragma unroll
@@ -1044,33 +999,168 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
 #pragma unroll
         for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) gs[rr][pb][ii] = alpha * gs[rr][pb][ii] + U[pb][ii];
+            for (int ii = 0; ii < 4; ++ii) gs[pb][ii] = alpha * gs[pb][ii] + U[pb][ii];
         lds_barrier(); // buffer s is free, buffer s ^ 1 is staged
+    }
+    if (dinit) {
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+            *(float4 *)(dinit + bh * (P * N) + goff + 16 * pb * N) =
+                make_float4(gs[pb][0], gs[pb][1], gs[pb][2], gs[pb][3]);
+    }
+}
+
+// Segment pre-pass of the reverse fused backward, one workgroup per (b, h,
+// run of M chunks): the gradient the run's own tokens send to the state
+// entering it, and the run's log decay,
+//   c[p][n] = sum_t exp2(CS_t) gy_t[p] C_t[n],   CS_t = log2 decay from the
+//   run's start through token t,
+// the closed form of k_bwd_dstate_rev's recurrence g <- dSoff_k +
+// exp2(cs_last_k) g over the run (from its last chunk, g = 0) with the
+// decays folded into the staged operand.  Chunks go in pairs, both staged at
+// once by all eight waves (the loads of the whole pair in flight together,
+// the next pair's issued before this pair's products), so a run of one or two
+// chunks is a single pass: the recurrence's chunk-by-chunk steps through a
+// register ring are latency-bound at one or two chunks per head.  The 16
+// output tiles go two to a wave (n-block wave % 4, p-blocks 2 (wave / 4) and
+// 2 (wave / 4) + 1); the same operands, fragments and split-bf16 products
+// as the recurrence's.
+template <bool kHasZ, bool kSeq>
+__global__ __launch_bounds__(kWsThreads, 2) void k_bwd_run_grad(BwdParams prm, RevSeg rs) {
+    constexpr int T = 64, P = 64, N = 64;
+    __shared__ __attribute__((aligned(16))) __bf16 lds[8 * kTile]; // GE(c), CT(c) of the pair's chunk c
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int r16 = lane & 15, kq = lane >> 4;
+    auto GE = [&](int c) { return tile_at(lds, 2 * c); };
+    auto CT = [&](int c) { return tile_at(lds, 2 * c + 1); };
+    // unit = ((b * G + g) * nseg + sg) * R + r: the R heads of a group's run
+    // on one XCD, so C of the run reaches one L2
+    const int R = prm.R;
+    const int u = xcd_unit(blockIdx.x, (int)gridDim.x, R);
+    const int r = u % R, sg = (u / R) % rs.nseg, bg = u / (R * rs.nseg);
+    const int g = bg % prm.G, b = bg / prm.G, h = g * R + r;
+    const int H = prm.H, G = prm.G, K = prm.K;
+    const int kbeg = sg * rs.M, kend = min(kbeg + rs.M, K);
+    const int rowHP4 = H * P * 4, rowGN4 = G * N * 4;
+    const bool has_dout = prm.dout != nullptr;
+    const float Ah2 = prm.A[h] * kLog2e;
+    const float bias = prm.dt_bias ? prm.dt_bias[h] : 0.f;
+    // staging: this thread's chunk of the pair, rows rt + 16 j, columns c4 .. c4 + 3
+    const int cpair = tid >> 8, pt = tid & 255;
+    const int rt = pt >> 4, c4 = (pt & 15) * 4;
+    auto tvalid = [&](int k) { return k < kend ? (int)min((int64_t)T, prm.L - (int64_t)k * T) : 0; };
+
+    float4 gr[4], zr[4], cr[4];
+    float dtr[2];
+    int sidr[2], sprv[2];
+    // unconditional loads (exact wait counts): rows past the sequence end
+    // re-read its last row and chunks past the run read through an
+    // empty-range resource (zeros); both are zeroed when staged
+    auto load = [&](int k0) {
+        const int k = k0 + cpair;
+        const bool real = k < kend;
+        const int kk = real ? k : kbeg, tv = (int)min((int64_t)T, prm.L - (int64_t)kk * T);
+        const int range = real ? 0x7fffffff : 0;
+        const int64_t t0 = (int64_t)kk * T;
+        const int64_t xo = (((int64_t)b * prm.L + t0) * H + h) * P;
+        const auto rd = buf_rsrc_n(has_dout ? prm.dout + xo : prm.x + xo, range);
+        const auto rz = buf_rsrc_n(kHasZ ? prm.z + xo : prm.x + xo, range);
+        const auto rc = buf_rsrc_n(prm.C + (((int64_t)b * prm.L + t0) * G + g) * N, range);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = min(rt + 16 * j, tv - 1);
+            gr[j] = buf_load4(rd, row * rowHP4 + c4 * 4, 0);
+            if (kHasZ) zr[j] = buf_load4(rz, row * rowHP4 + c4 * 4, 0);
+            cr[j] = buf_load4(rc, row * rowGN4 + c4 * 4, 0);
+        }
+        // dt (and ids) of token `lane` of both chunks, for every wave's scans
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int kc = k0 + c < kend ? k0 + c : kbeg;
+            const int64_t tc = (int64_t)kc * T;
+            const int tvc = (int)min((int64_t)T, prm.L - tc);
+            dtr[c] = prm.dt[((int64_t)b * prm.L + tc + min(lane, tvc - 1)) * H + h];
+            if (kSeq) {
+                const int32_t *si = prm.seq_idx + (int64_t)b * prm.L + tc;
+                sidr[c] = si[min(lane, tvc - 1)];
+                const int pv = si[tc > 0 ? -1 : 0]; // read unconditionally, 0 before the first chunk
+                sprv[c] = tc > 0 ? pv : 0;
+            }
+        }
     };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
-    for (int i = 0; i < nsteps; i += kHeads) {
-        c_step(i, I0{});
-        if constexpr (kHeads >= 2) c_step(i + 1, I1{});
-        if constexpr (kHeads == 4) {
-            c_step(i + 2, I2{});
-            c_step(i + 3, I3{});
-        }
-    }
+
+    // output tiles g[p = 16 pb + l % 16][n = 16 nb + 4 (l / 16) + i]
+    const int nb = wave & 3, pb0 = 2 * (wave >> 2);
+    f32x4 acc[2] = {zero4(), zero4()};
+    float off = 0.f;   // log2 decay from the run's start to the pair's first token
+    float keep = 1.f;  // kSeq: 0 once the state is cut inside the run
+    bool cut = false;
+    load(kbeg);
+    for (int k0 = kbeg; k0 < kend; k0 += 2) {
+        // per-token log2 decays of both chunks (every wave, lane = token)
+        float cs[2], last[2], reads[2] = {1.f, 1.f}, carry[2] = {1.f, 1.f};
 #pragma unroll
-    for (int rr = 0; rr < kHeads; ++rr) {
-        const int64_t bh = (int64_t)b * H + h0 + rr;
-        float *dst = segmented ? rs.seg_carry + (bh * rs.nseg + sg) * (P * N)
-                               : (dinit ? dinit + bh * (P * N) : nullptr);
-        if (dst) {
-#pragma unroll
-            for (int pb = 0; pb < 4; ++pb)
-                *(float4 *)(dst + goff + 16 * pb * N) =
-                    make_float4(gs[rr][pb][0], gs[rr][pb][1], gs[rr][pb][2], gs[rr][pb][3]);
+        for (int c = 0; c < 2; ++c) {
+            const int tv = tvalid(k0 + c);
+            float a = 0.f;
+            if (lane < tv) a = Ah2 * discretize_dt(dtr[c], bias, prm.softplus != 0, prm.lo, prm.hi);
+            cs[c] = wave_inclusive_scan(a);
+            last[c] = readlane_f(cs[c], T - 1);
+            if (kSeq && k0 + c < kend) {
+                const int e_end = __builtin_amdgcn_readlane(sidr[c], T - 1);
+                reads[c] = sidr[c] == sprv[c] ? 1.f : 0.f;
+                carry[c] = e_end == sprv[c] ? 1.f : 0.f;
+            }
         }
+        // exp2(CS_t) of this thread's chunk, times the kSeq masks
+        const float base = cpair ? off + last[0] : off;
+        const float mask = kSeq ? (cpair ? keep * carry[0] : keep) * (cpair ? reads[1] : reads[0]) : 1.f;
+        const float ecs = exp2_f(base + (cpair ? cs[1] : cs[0])) * mask;
+        float es[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) es[j] = __shfl(ecs, rt + 16 * j, kWave);
+        __builtin_amdgcn_sched_barrier(0);
+        const int tv = tvalid(k0 + cpair);
+        const SplitTile ge = GE(cpair), ct = CT(cpair);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = rt + 16 * j;
+            const bool ok = row < tv;
+            const float e = es[j];
+            float4 v = (ok && has_dout) ? gr[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (kHasZ) {
+                v.x *= silu_f(zr[j].x);
+                v.y *= silu_f(zr[j].y);
+                v.z *= silu_f(zr[j].z);
+                v.w *= silu_f(zr[j].w);
+            }
+            store_split4(ge, row * kTS + c4, make_float4(v.x * e, v.y * e, v.z * e, v.w * e));
+            store_split4(ct, row * kTS + c4, ok ? cr[j] : make_float4(0.f, 0.f, 0.f, 0.f));
+        }
+        off += last[0] + last[1];
+        if (kSeq) {
+            keep *= carry[0] * carry[1];
+            cut = cut || carry[0] == 0.f || carry[1] == 0.f;
+        }
+        // the next pair's loads fly under this pair's products
+        if (k0 + 2 < kend) load(k0 + 2);
+        lds_barrier();
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const Frag a = frag_tn(CT(c), ks, 16 * nb);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) acc[i] = mma3f(a, frag_tn(GE(c), ks, 16 * (pb0 + i)), acc[i]);
+            }
+        lds_barrier(); // the tiles are free for the next pair
     }
+    const int64_t bh = (int64_t)b * H + h;
+    float *dst = rs.seg_carry + (bh * rs.nseg + sg) * (P * N);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        *(float4 *)(dst + (16 * (pb0 + i) + r16) * N + 16 * nb + 4 * kq) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    if (tid == 0) rs.seg_log_decay[bh * rs.nseg + sg] = cut ? -INFINITY : off * kLn2;
 }
 
 }  // namespace bwd

@@ -48,8 +48,10 @@ struct BwdParams {
     float lo, hi;
 };
 
-// Segments of the reverse state-gradient pre-pass (k_bwd_dstate_rev): nseg
-// runs of M chunks per (b, h); seg_carry NULL = one run over all chunks.
+// Runs of the reverse fused backward: nseg runs of M chunks per (b, h), whose
+// own contributions to the gradient entering each run (seg_carry [B, H, nseg,
+// P, N]) and log decays (seg_log_decay [B, H, nseg]) the run pre-pass
+// k_bwd_run_grad forms.
 struct RevSeg {
     int nseg, M;
     float *seg_carry, *seg_log_decay;

@@ -1,5 +1,6 @@
-// Variants of the chunk backward k_bwd_ws and the reverse state-gradient pass
-// k_bwd_dstate_rev for one value of the z gate, and their launchers (declared
+// Variants of the chunk backward k_bwd_ws, the reverse state-gradient pass
+// k_bwd_dstate_rev and the run pre-pass k_bwd_run_grad for one value of the z
+// gate, and their launchers (declared
 // in ssd_launch.h).  Built twice, with SSD_BWD_Z=0 and SSD_BWD_Z=1, so the two
 // halves compile in parallel.
 #define SSD_KERNEL_TEMPLATES_ONLY
@@ -23,11 +24,14 @@ void run_ws(dim3 grid, hipStream_t st, const BwdParams &bp, int nseg, int M) {
     hipLaunchKernelGGL((bwd::k_bwd_ws<kZ, kR, kSeq>), grid, dim3(kBwsThreads), 0, st, bp, nseg, M);
 }
 
-template <bool kSeq, int kHeads>
-void run_rev(dim3 grid, hipStream_t st, const BwdParams &bp, const float *dfinal, float *dinit,
-             const RevSeg &rs) {
-    hipLaunchKernelGGL((bwd::k_bwd_dstate_rev<kZ, kSeq, kHeads>), grid, dim3(kWsThreads), 0, st, bp,
-                       dfinal, dinit, rs);
+template <bool kSeq>
+void run_rev(dim3 grid, hipStream_t st, const BwdParams &bp, const float *dfinal, float *dinit) {
+    hipLaunchKernelGGL((bwd::k_bwd_dstate_rev<kZ, kSeq>), grid, dim3(kWsThreads), 0, st, bp, dfinal, dinit);
+}
+
+template <bool kSeq>
+void run_grad(dim3 grid, hipStream_t st, const BwdParams &bp, const RevSeg &rs) {
+    hipLaunchKernelGGL((bwd::k_bwd_run_grad<kZ, kSeq>), grid, dim3(kWsThreads), 0, st, bp, rs);
 }
 
 }  // namespace
@@ -42,14 +46,14 @@ void SSD_CAT(launch_bwd_ws_z, SSD_BWD_Z)(int rev_r, bool seq, dim3 grid, hipStre
     }
 }
 
-void SSD_CAT(launch_bwd_dstate_rev_z, SSD_BWD_Z)(bool seq, int heads, dim3 grid, hipStream_t st,
-                                                  const BwdParams &bp, const float *dfinal,
-                                                  float *dinit, const RevSeg &rs) {
-    switch (heads) {
-    case 4: (seq ? run_rev<true, 4> : run_rev<false, 4>)(grid, st, bp, dfinal, dinit, rs); break;
-    case 2: (seq ? run_rev<true, 2> : run_rev<false, 2>)(grid, st, bp, dfinal, dinit, rs); break;
-    default: (seq ? run_rev<true, 1> : run_rev<false, 1>)(grid, st, bp, dfinal, dinit, rs); break;
-    }
+void SSD_CAT(launch_bwd_dstate_rev_z, SSD_BWD_Z)(bool seq, dim3 grid, hipStream_t st, const BwdParams &bp,
+                                                  const float *dfinal, float *dinit) {
+    (seq ? run_rev<true> : run_rev<false>)(grid, st, bp, dfinal, dinit);
+}
+
+void SSD_CAT(launch_bwd_run_grad_z, SSD_BWD_Z)(bool seq, dim3 grid, hipStream_t st, const BwdParams &bp,
+                                               const RevSeg &rs) {
+    (seq ? run_grad<true> : run_grad<false>)(grid, st, bp, rs);
 }
 
 }  // namespace ssd

@@ -29,10 +29,12 @@ void launch_bwd_ws_z0(int rev_r, bool seq, dim3 grid, hipStream_t st, const BwdP
                       int M);
 void launch_bwd_ws_z1(int rev_r, bool seq, dim3 grid, hipStream_t st, const BwdParams &bp, int nseg,
                       int M);
-void launch_bwd_dstate_rev_z0(bool seq, int heads, dim3 grid, hipStream_t st, const BwdParams &bp,
-                              const float *dfinal, float *dinit, const RevSeg &rs);
-void launch_bwd_dstate_rev_z1(bool seq, int heads, dim3 grid, hipStream_t st, const BwdParams &bp,
-                              const float *dfinal, float *dinit, const RevSeg &rs);
+void launch_bwd_dstate_rev_z0(bool seq, dim3 grid, hipStream_t st, const BwdParams &bp, const float *dfinal,
+                              float *dinit);
+void launch_bwd_dstate_rev_z1(bool seq, dim3 grid, hipStream_t st, const BwdParams &bp, const float *dfinal,
+                              float *dinit);
+void launch_bwd_run_grad_z0(bool seq, dim3 grid, hipStream_t st, const BwdParams &bp, const RevSeg &rs);
+void launch_bwd_run_grad_z1(bool seq, dim3 grid, hipStream_t st, const BwdParams &bp, const RevSeg &rs);
 
 // k_bwd_ws<has_z, rev_r, seq> (rev_r 0, 1, 2 or 4)
 inline void launch_bwd_ws(bool has_z, int rev_r, bool seq, dim3 grid, hipStream_t st,
@@ -41,12 +43,18 @@ inline void launch_bwd_ws(bool has_z, int rev_r, bool seq, dim3 grid, hipStream_
     else launch_bwd_ws_z0(rev_r, seq, grid, st, bp, nseg, M);
 }
 
-// k_bwd_dstate_rev<has_z, seq, heads> (heads per workgroup: 1, 2 or 4, dividing R)
-inline void launch_bwd_dstate_rev(bool has_z, bool seq, int heads, dim3 grid, hipStream_t st,
-                                  const BwdParams &bp, const float *dfinal, float *dinit,
-                                  const RevSeg &rs) {
-    if (has_z) launch_bwd_dstate_rev_z1(seq, heads, grid, st, bp, dfinal, dinit, rs);
-    else launch_bwd_dstate_rev_z0(seq, heads, grid, st, bp, dfinal, dinit, rs);
+// k_bwd_dstate_rev<has_z, seq>, one workgroup per (b, h)
+inline void launch_bwd_dstate_rev(bool has_z, bool seq, dim3 grid, hipStream_t st, const BwdParams &bp,
+                                  const float *dfinal, float *dinit) {
+    if (has_z) launch_bwd_dstate_rev_z1(seq, grid, st, bp, dfinal, dinit);
+    else launch_bwd_dstate_rev_z0(seq, grid, st, bp, dfinal, dinit);
+}
+
+// k_bwd_run_grad<has_z, seq>, one workgroup per (b, h, run)
+inline void launch_bwd_run_grad(bool has_z, bool seq, dim3 grid, hipStream_t st, const BwdParams &bp,
+                                const RevSeg &rs) {
+    if (has_z) launch_bwd_run_grad_z1(seq, grid, st, bp, rs);
+    else launch_bwd_run_grad_z0(seq, grid, st, bp, rs);
 }
 
 }  // namespace ssd

@@ -90,6 +90,10 @@ CASES = [
     # gradient entering each run from a pre-pass and the recurrence over runs
     ([4, 1700, 8, 64, 64, 64, 4], ("D", "z", "init"), True, (0.0, math.inf), "both"),
     ([2, 2600, 4, 64, 64, 64, 4], ("D2", "bias"), True, (0.0, math.inf), "final"),
+    # runs of 3 and 5 chunks: the run pre-pass walks pairs of chunks, the
+    # last pair of a run with one chunk
+    ([4, 2900, 8, 64, 64, 64, 4], ("z", "bias"), True, (0.0, math.inf), "both"),
+    ([4, 4500, 4, 64, 64, 64, 4], ("D", "init"), True, (0.0, math.inf), "both"),
     # >= 512 (b, h) streams: the fused reverse state-gradient pass
     ([2, 200, 256, 64, 64, 64, 64], ("D2", "z", "bias", "init"), True, (0.0, math.inf), "both"),
     ([1, 192, 512, 64, 64, 64, 128], (), True, (0.0, math.inf), "final"),

@@ -239,6 +239,7 @@ BWD = [
     ([2, 200, 4, 64, 64, 64, 2], ("D", "z", "bias", "init"), "mixed"),      # reverse runs of 1 chunk
     ([2, 330, 8, 64, 64, 256, 8], ("D2", "bias", "init"), "packed"),         # reverse runs, R = 1
     ([4, 1100, 8, 64, 64, 64, 4], ("D", "z", "init"), "packed"),             # reverse runs of 2 chunks
+    ([4, 2900, 8, 64, 64, 64, 4], ("z", "init"), "packed"),                  # reverse runs of 3 chunks
     ([2, 200, 8, 64, 64, 64, 1], ("D", "z", "init"), "mixed"),               # R = 8: chunk-parallel dSoff
     ([2, 130, 256, 64, 64, 64, 32], ("z", "init"), "mixed"),                 # reverse dstate pass
     ([2, 200, 256, 64, 64, 64, 128], ("D2", "z", "bias", "init"), "mixed"),  # fused reverse, R = 2
