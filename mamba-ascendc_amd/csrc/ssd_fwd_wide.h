@@ -124,6 +124,59 @@ __global__ __launch_bounds__(kCbThreads) void k_chunk_cb(const float *C, const f
     }
 }
 
+// Ownership of a workgroup's 32 x 128 state (16 tiles of 16 x 16: p-block
+// pb = 0, 1, n-block nb = 0..7) over the four consumer waves.  Wave W forms
+// the causal C . B^T blocks j <= W of its token rows (over 128 columns), so
+// the later waves carry more of the mask work; its own tiles are n-blocks W
+// and W + 4, and a split (c0, c1, c2, c3) other than (4, 4, 4, 4) hands tiles
+// of the later waves to the earlier ones (with them their U products, state
+// update and T4 staging).  Measured (A/B, three interleaved runs, k_fwd_wide
+// average): C2 4444 0.0540 ms, 6532 0.0523, 7531 0.0523, 5533 0.0534; C5
+// (C . B^T precomputed, so less to balance) 0.1716, 0.1731, 0.1744, 0.1730.
+struct WideTileMap {
+    int n[4];
+    int nb[4][8], pb[4][8];
+    int nd[4], dnb[4][8], tix[4][8]; // distinct n-blocks of a wave, and each tile's index among them
+};
+constexpr WideTileMap make_wide_tiles(int c0, int c1, int c2, int c3) {
+    WideTileMap m{};
+    const int want[4] = {c0, c1, c2, c3};
+    int snb[16] = {}, spb[16] = {}, ns = 0;
+    for (int w = 0; w < 4; ++w)
+        for (int i = 0; i < 4; ++i) {
+            const int nb = w + 4 * (i >> 1), pb = i & 1;
+            if (i < want[w]) {
+                m.nb[w][m.n[w]] = nb;
+                m.pb[w][m.n[w]] = pb;
+                ++m.n[w];
+            } else {
+                snb[ns] = nb;
+                spb[ns] = pb;
+                ++ns;
+            }
+        }
+    int t = 0;
+    for (int w = 0; w < 4; ++w)
+        while (m.n[w] < want[w] && t < ns) {
+            m.nb[w][m.n[w]] = snb[t];
+            m.pb[w][m.n[w]] = spb[t];
+            ++m.n[w];
+            ++t;
+        }
+    for (int w = 0; w < 4; ++w)
+        for (int i = 0; i < m.n[w]; ++i) {
+            int j = 0;
+            while (j < m.nd[w] && m.dnb[w][j] != m.nb[w][i]) ++j;
+            if (j == m.nd[w]) m.dnb[w][m.nd[w]++] = m.nb[w][i];
+            m.tix[w][i] = j;
+        }
+    return m;
+}
+#ifndef SSD_WIDE_TILES
+#define SSD_WIDE_TILES 6, 5, 3, 2
+#endif
+constexpr WideTileMap kWideTiles = make_wide_tiles(SSD_WIDE_TILES);
+
 // kSave: also write the state entering every chunk to prm.chunk_states (the
 // varlen states read them).  kGate: the z gate.  kSeq: packed sequences.
 // kCB: C . B^T of each chunk comes from prm.cb (k_chunk_cb) instead of
@@ -322,10 +375,16 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
     auto consumer = [&](auto wave_c) {
         constexpr int W = decltype(wave_c)::value;
         const int own = 16 * W + r16; // token row of this lane
-        // Sr[c][pb][i] = S[p0 + 16 pb + l % 16][n = 16 (W + 4 c) + 4 (l / 16) + i]
-        // 2^-eS (eS = kZeroState while the state is zero; every consumer wave
-        // forms the same eS, and the producers the same sequence)
-        f32x4 Sr[2][2];
+        // Sr[i][r] = S[p0 + 16 tpb(i) + l % 16][n = 16 tnb(i) + 4 (l / 16) + r]
+        // 2^-eS for this wave's NT tiles (eS = kZeroState while the state is
+        // zero; every consumer wave forms the same eS, and the producers the
+        // same sequence)
+        constexpr int NT = kWideTiles.n[W];
+        auto tnb = [](int i) { return kWideTiles.nb[W][i]; };
+        auto tpb = [](int i) { return kWideTiles.pb[W][i]; };
+        // offset of tile i's four values within a [P, NS] state
+        auto toff = [&](int i) { return (p0 + 16 * tpb(i) + r16) * NS + 16 * tnb(i) + 4 * kq; };
+        f32x4 Sr[NT];
         int eS = kZeroState;
         // C row `own` of the next chunk (128 columns: k-steps ks = 0..3, each
         // 8 (l / 16) + 0..7 of its 32 columns), loaded one chunk ahead; past
@@ -366,42 +425,31 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         auto write_T4 = [&](int s) {
             const SplitTile t4 = T4(opaque_lds(lds), s);
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
-#pragma unroll
-                for (int pb = 0; pb < 2; ++pb)
-                    store_split4(t4, (16 * pb + r16) * kS1 + 16 * (W + 4 * c) + 4 * kq,
-                                 make_float4(Sr[c][pb][0], Sr[c][pb][1], Sr[c][pb][2], Sr[c][pb][3]));
+            for (int i = 0; i < NT; ++i)
+                store_split4(t4, (16 * tpb(i) + r16) * kS1 + 16 * tnb(i) + 4 * kq,
+                             make_float4(Sr[i][0], Sr[i][1], Sr[i][2], Sr[i][3]));
         };
 
         {
             const float *s0 = nullptr;
             const int64_t bh = (int64_t)b * H + h;
             if (sp.seg_in && sp.seg_in_log_decay) {
-                f32x4 acc[4];
-                fold_entry(acc, sp.seg_in + bh * sp.seg_in_n * PNS, sp.seg_in_log_decay + bh * sp.seg_in_n,
-                           sg * sp.in_mult, PNS, prm.init ? prm.init + bh * PNS : nullptr, [&](int i) {
-                               return (p0 + 16 * (i & 1) + r16) * NS + 16 * (W + 4 * (i >> 1)) + 4 * kq;
-                           });
-#pragma unroll
-                for (int c = 0; c < 2; ++c)
-#pragma unroll
-                    for (int pb = 0; pb < 2; ++pb) Sr[c][pb] = acc[2 * c + pb];
+                fold_entry(Sr, sp.seg_in + bh * sp.seg_in_n * PNS, sp.seg_in_log_decay + bh * sp.seg_in_n,
+                           sg * sp.in_mult, PNS, prm.init ? prm.init + bh * PNS : nullptr, toff);
             } else {
                 if (sp.seg_in)
                     s0 = sp.seg_in + (bh * sp.seg_in_n + sg * sp.in_mult) * PNS;
                 else if (prm.init)
                     s0 = prm.init + bh * PNS;
 #pragma unroll
-                for (int c = 0; c < 2; ++c)
-#pragma unroll
-                    for (int pb = 0; pb < 2; ++pb) {
-                        if (s0) {
-                            const float4 v = *(const float4 *)(s0 + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq);
-                            Sr[c][pb] = f32x4{v.x, v.y, v.z, v.w};
-                        } else {
-                            Sr[c][pb] = zero4();
-                        }
+                for (int i = 0; i < NT; ++i) {
+                    if (s0) {
+                        const float4 v = *(const float4 *)(s0 + toff(i));
+                        Sr[i] = f32x4{v.x, v.y, v.z, v.w};
+                    } else {
+                        Sr[i] = zero4();
                     }
+                }
             }
             if (s0_nonzero) {
                 // the entering state's largest magnitude over the four
@@ -409,21 +457,17 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
                 // the producers, which read the same maxima)
                 float m = 0.f;
 #pragma unroll
-                for (int c = 0; c < 2; ++c)
+                for (int i = 0; i < NT; ++i)
 #pragma unroll
-                    for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(Sr[c][pb][i]));
+                    for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(Sr[i][r]));
                 m = wave_max(m);
                 if (lane == 0) s_smax[W] = m;
                 lds_barrier();
                 eS = state_exp_of(s_smax);
 #pragma unroll
-                for (int c = 0; c < 2; ++c)
+                for (int i = 0; i < NT; ++i)
 #pragma unroll
-                    for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) Sr[c][pb][i] = __builtin_amdgcn_ldexpf(Sr[c][pb][i], -eS);
+                    for (int r = 0; r < 4; ++r) Sr[i][r] = __builtin_amdgcn_ldexpf(Sr[i][r], -eS);
             }
             write_T4(0);
             c_load(kbeg);
@@ -454,11 +498,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
                 float *cst = prm.chunk_states + (((int64_t)b * H + h) * prm.K + k) * PNS;
                 const float f = __builtin_amdgcn_ldexpf(1.f, eS);
 #pragma unroll
-                for (int c = 0; c < 2; ++c)
-#pragma unroll
-                    for (int pb = 0; pb < 2; ++pb)
-                        *(float4 *)(cst + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq) =
-                            make_float4(Sr[c][pb][0] * f, Sr[c][pb][1] * f, Sr[c][pb][2] * f, Sr[c][pb][3] * f);
+                for (int i = 0; i < NT; ++i)
+                    *(float4 *)(cst + toff(i)) = make_float4(Sr[i][0] * f, Sr[i][1] * f, Sr[i][2] * f, Sr[i][3] * f);
             }
             Frag Cown[4];
 #pragma unroll
@@ -604,32 +645,29 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             }
             z_load(k + 1);
             // U^T[n][p] = sum_t B[t][n] (decay q x)[t][p]; S <- exp2(cs_last) S + U
-            f32x4 U[2][2];
+            f32x4 U[NT];
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
-#pragma unroll
-                for (int pb = 0; pb < 2; ++pb) U[c][pb] = zero4();
+            for (int i = 0; i < NT; ++i) U[i] = zero4();
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
                 Frag f3[2];
 #pragma unroll
                 for (int pb = 0; pb < 2; ++pb) f3[pb] = frag_tp_s<kS2>(t3, m, 16 * pb);
+                // the B operand of each n-block this wave's tiles use
+                constexpr int ND = kWideTiles.nd[W];
+                Frag a1[ND];
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const Frag a1 = frag_tp_s<kS1>(t1b, m, 16 * (W + 4 * c));
+                for (int j = 0; j < ND; ++j) a1[j] = frag_tp_s<kS1>(t1b, m, 16 * kWideTiles.dnb[W][j]);
 #pragma unroll
-                    for (int pb = 0; pb < 2; ++pb) U[c][pb] = mma3f(a1, f3[pb], U[c][pb]);
-                }
+                for (int i = 0; i < NT; ++i) U[i] = mma3f(a1[kWideTiles.tix[W][i]], f3[tpb(i)], U[i]);
             }
             // S' 2^-eN = exp2(cs_last) 2^(eS - eN) (S 2^-eS) + U 2^-eN (T3's scale)
             const float alpha = __builtin_amdgcn_ldexpf(kSeq ? exp2_f(cs_last) * s_carry[s] : exp2_f(cs_last),
                                                         eS - eN);
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
+            for (int i = 0; i < NT; ++i)
 #pragma unroll
-                for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) Sr[c][pb][i] = alpha * Sr[c][pb][i] + U[c][pb][i];
+                for (int r = 0; r < 4; ++r) Sr[i][r] = alpha * Sr[i][r] + U[i][r];
             eS = eN;
             write_T4(s ^ 1);
             lds_barrier(); // buffer s is free, buffer s ^ 1 and T4(s ^ 1) are complete
@@ -643,11 +681,8 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
             float *dst = prm.final_state + ((int64_t)b * H + h) * PNS;
             const float f = __builtin_amdgcn_ldexpf(1.f, eS);
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
-#pragma unroll
-                for (int pb = 0; pb < 2; ++pb)
-                    *(float4 *)(dst + (p0 + 16 * pb + r16) * NS + 16 * (W + 4 * c) + 4 * kq) =
-                        make_float4(Sr[c][pb][0] * f, Sr[c][pb][1] * f, Sr[c][pb][2] * f, Sr[c][pb][3] * f);
+            for (int i = 0; i < NT; ++i)
+                *(float4 *)(dst + toff(i)) = make_float4(Sr[i][0] * f, Sr[i][1] * f, Sr[i][2] * f, Sr[i][3] * f);
         }
     };
     switch (w) {
