@@ -65,14 +65,25 @@ struct SplitTile {
     __bf16 *hi, *lo;
 };
 
+// Slot of tile row r: inside each 16-row block the rows are interleaved,
+// row r at slot 2 (r % 8) + (r / 8) % 2.  At the kTS-element (144-byte) row
+// stride, the eight rows a transposing read (ds_read_b64_tr_b16, frag_tp)
+// gathers per 32 lanes then fall on eight disjoint 8-bank spans (measured: 0
+// bank-conflict cycles per instruction, 2 with rows in order); the 16-byte
+// operand reads, the natural-order transposing reads and the row writes keep
+// their conflict counts, since each touches a whole 16-row block or a single
+// row.  Every tile access of the backward goes through this mapping.
+__device__ __forceinline__ int trow(int r) { return (r & ~15) | ((r & 7) << 1) | ((r >> 3) & 1); }
+
 __device__ __forceinline__ SplitTile tile_at(__bf16 *base, int i) {
     return SplitTile{base + (2 * i) * kTile, base + (2 * i + 1) * kTile};
 }
 
-// tile[idx .. idx + 3] = v (both halves)
-__device__ __forceinline__ void store_split4(SplitTile d, int idx, float4 v) {
+// tile[row][c0 .. c0 + 3] = v (both halves)
+__device__ __forceinline__ void store_split4(SplitTile d, int row, int c0, float4 v) {
     bf16x4 vh, vl;
     split4(v, vh, vl);
+    const int idx = trow(row) * kTS + c0;
     *(bf16x4 *)&d.hi[idx] = vh;
     *(bf16x4 *)&d.lo[idx] = vl;
 }
@@ -84,8 +95,9 @@ struct Frag {
 __device__ __forceinline__ Frag frag(SplitTile s, int row, int ks) {
     const int kq = (threadIdx.x & 63) >> 4;
     Frag f;
-    f.h = *(const bf16x8 *)&s.hi[row * kTS + ks * 32 + kq * 8];
-    f.l = *(const bf16x8 *)&s.lo[row * kTS + ks * 32 + kq * 8];
+    const int idx = trow(row) * kTS + ks * 32 + kq * 8;
+    f.h = *(const bf16x8 *)&s.hi[idx];
+    f.l = *(const bf16x8 *)&s.lo[idx];
     return f;
 }
 
@@ -109,7 +121,7 @@ __device__ __forceinline__ Frag pack_frag(const float (&v)[8]) {
 __device__ __forceinline__ bf16x4 tr4(const __bf16 *arr, int k0, int c0) {
     const int m = threadIdx.x & 15;
     typedef short v4s __attribute__((ext_vector_type(4)));
-    auto p = (__attribute__((address_space(3))) v4s *)(arr + (k0 + (m >> 2)) * kTS + c0 + 4 * (m & 3));
+    auto p = (__attribute__((address_space(3))) v4s *)(arr + trow(k0 + (m >> 2)) * kTS + c0 + 4 * (m & 3));
     return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
 }
 
@@ -145,7 +157,8 @@ __device__ __forceinline__ f32x4 join4(bf16x4 h, bf16x4 l) {
 
 // fp32 values of tile[row][c0 .. c0 + 3]
 __device__ __forceinline__ f32x4 tile_row4(SplitTile s, int row, int c0) {
-    return join4(*(const bf16x4 *)&s.hi[row * kTS + c0], *(const bf16x4 *)&s.lo[row * kTS + c0]);
+    const int idx = trow(row) * kTS + c0;
+    return join4(*(const bf16x4 *)&s.hi[idx], *(const bf16x4 *)&s.lo[idx]);
 }
 
 // column-major staging, tile[c][slot] = f(t, c) (ssd::stage_cols for this element type)
@@ -161,8 +174,8 @@ __device__ __forceinline__ void stage_cols(SplitTile d, F f) {
             v[i] = f(PERM ? perm_token(slot) : slot, c);
         }
         const Frag p = pack_frag(v);
-        *(bf16x8 *)&d.hi[c * kTS + run * 8] = p.h;
-        *(bf16x8 *)&d.lo[c * kTS + run * 8] = p.l;
+        *(bf16x8 *)&d.hi[trow(c) * kTS + run * 8] = p.h;
+        *(bf16x8 *)&d.lo[trow(c) * kTS + run * 8] = p.l;
     }
 }
 

@@ -237,7 +237,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             }
         };
         auto put = [&](SplitTile d, int row, float4 v) __attribute__((always_inline)) {
-            store_split4(d, row * kTS + c4, v);
+            store_split4(d, row, c4, v);
         };
         auto stage_xg = [&](int n) __attribute__((always_inline)) {
             const int par = n & 1, k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         // dSoff^T[n][p] = sum_t (exp2(cs_t) C_t[n]) gy_t[p] from the C and gy
         // tiles the consumers read in the same phase
         auto put_acc = [&](SplitTile d, int pb, f32x4 v) __attribute__((always_inline)) {
-            store_split4(d, (16 * pb + r16) * kTS + 16 * pw + 4 * kq, make_float4(v[0], v[1], v[2], v[3]));
+            store_split4(d, 16 * pb + r16, 16 * pw + 4 * kq, make_float4(v[0], v[1], v[2], v[3]));
         };
         auto stage_su_rev = [&](int n, auto slot_c) __attribute__((always_inline)) {
             constexpr int rr = decltype(slot_c)::value;
@@ -895,7 +895,7 @@ __global__ __launch_bounds__(kWsThreads) void k_bwd_dstate_rev(BwdParams prm, co
                 sprv[sl] = t0 > 0 ? pv : 0;
             }
         };
-        auto put = [&](SplitTile d, int row, float4 v) { store_split4(d, row * kTS + c4, v); };
+        auto put = [&](SplitTile d, int row, float4 v) { store_split4(d, row, c4, v); };
         auto p_stage = [&](int i, int s, auto slot_c) {
             constexpr int sl = decltype(slot_c)::value;
             const bool real = i < nsteps;
@@ -1134,8 +1134,8 @@ __global__ __launch_bounds__(kWsThreads, 2) void k_bwd_run_grad(BwdParams prm, R
                 v.z *= silu_f(zr[j].z);
                 v.w *= silu_f(zr[j].w);
             }
-            store_split4(ge, row * kTS + c4, make_float4(v.x * e, v.y * e, v.z * e, v.w * e));
-            store_split4(ct, row * kTS + c4, ok ? cr[j] : make_float4(0.f, 0.f, 0.f, 0.f));
+            store_split4(ge, row, c4, make_float4(v.x * e, v.y * e, v.z * e, v.w * e));
+            store_split4(ct, row, c4, ok ? cr[j] : make_float4(0.f, 0.f, 0.f, 0.f));
         }
         off += last[0] + last[1];
         if (kSeq) {

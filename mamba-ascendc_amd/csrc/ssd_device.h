@@ -403,6 +403,17 @@ __device__ __forceinline__ _Float16 *opaque_lds(_Float16 *p) {
     return (_Float16 *)(lptr)(uintptr_t)a;
 }
 
+// v as a value the optimizer cannot see through: the product that forms it is
+// rounded once, and no later difference is contracted with it into an FMA.
+// The forward kernels form the chunk cumsum this way, so the per-token values
+// derived from it (decays, scales) get the same bits in every kernel that
+// forms them, whatever each kernel's other uses of the cumsum let the
+// compiler fuse.
+__device__ __forceinline__ float opaque_f(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // The same for any LDS object (a struct of small arrays, say).
 template <class X>
 __device__ __forceinline__ X *opaque_lds_t(X *p) {

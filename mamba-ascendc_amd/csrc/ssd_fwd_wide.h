@@ -276,7 +276,7 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_wide(FwdParams prm, SegParam
         float q = 0.f;
         if (lane < tv) q = discretize_dt(dtr[sl], bias, prm.softplus != 0, prm.lo, prm.hi);
         const float sq = wave_inclusive_scan(q); // prefix sums of q
-        const float cs = Ah2 * sq;               // log2 units
+        const float cs = opaque_f(Ah2 * sq);               // log2 units
         const float cs_last = readlane_f(cs, T - 1);
         int ek = chunk_q_exp(readlane_f(sq, T - 1), wave_max(fabsf(q))); // kSeq: that of the id leaving the chunk
         int ek_tok = ek; // exponent of the token's q (kSeq: that of its id)
