@@ -197,9 +197,10 @@ def fwd_kernel_model(name: str, shape) -> dict:
     elif name == "k_fwd_seg_state":
         per = f4 * (T * p + T + T * n / r)
         fl = 2 * T * p * n
-    elif name == "k_fwd_seg_state_save":
+    elif name in ("k_fwd_seg_state_save", "k_fwd_state_group"):
         # the backward's recompute of the chunk-start states: x, dt, B in,
-        # the state entering every chunk out
+        # the state entering every chunk out (k_fwd_state_group: the same
+        # pass, one workgroup per group walking its heads)
         per = f4 * (T * p + T + T * n / r + p * n)
         fl = 2 * T * p * n
     elif name == "k_bwd_run_grad":
@@ -950,7 +951,7 @@ def model_key(short: str) -> str:
         if len(args) > 1 and args[1] != "0":
             return ("k_bwd_ws_rev_z" if args[0] == "true" else "k_bwd_ws_rev") + seq
         return "k_bwd_ws" + seq
-    return base if base in ("k_bwd_dstate_rev", "k_bwd_run_grad", "k_chunk_cb") else short
+    return base if base in ("k_bwd_dstate_rev", "k_bwd_run_grad", "k_chunk_cb", "k_fwd_state_group") else short
 
 
 SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs

@@ -817,8 +817,14 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
             sp.seg_in_n = pre.nseg;
             sp.in_mult = lay.recompute.mult;
         }
-        ssd::launch_fwd_seg(true, true, false, seq, dim3(units), st, sp_prm, sp);
-        if (int rc = launch_status("k_fwd_seg_state_save", tr, st)) return rc;
+        if (sp.nseg == 1 && !seq && sp_prm.R == 4) {
+            // one workgroup per (b, g) walking its four heads per chunk: B read once
+            ssd::launch_fwd_state_group(dim3((unsigned)(B * s->ngroups)), st, sp_prm);
+            if (int rc = launch_status("k_fwd_state_group", tr, st)) return rc;
+        } else {
+            ssd::launch_fwd_seg(true, true, false, seq, dim3(units), st, sp_prm, sp);
+            if (int rc = launch_status("k_fwd_seg_state_save", tr, st)) return rc;
+        }
     }
     const int64_t bg = (int64_t)B * s->ngroups;
     if (lay.rev.nseg > 0) {

@@ -1,7 +1,9 @@
-// Variants of the fused forward k_fwd_seg and their launcher (declared in
+// Variants of the fused forward k_fwd_seg, the group-major state pass
+// k_fwd_state_group, and their launchers (declared in
 // ssd_launch.h); the library's host code is in mamba2_ssd.hip.
 #define SSD_KERNEL_TEMPLATES_ONLY
 #include "ssd_fwd_fused.h"
+#include "ssd_fwd_group.h"
 #include "ssd_launch.h"
 
 namespace ssd {
@@ -33,6 +35,10 @@ void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, 
         run<false, true, true, false>,   run<false, true, true, true>,
     };
     full[(save ? 4 : 0) + (gate ? 2 : 0) + (seq ? 1 : 0)](grid, st, kp, sp);
+}
+
+void launch_fwd_state_group(dim3 grid, hipStream_t st, const FwdParams &kp) {
+    hipLaunchKernelGGL((k_fwd_state_group<4>), grid, dim3(kWsThreads), 0, st, kp);
 }
 
 }  // namespace ssd

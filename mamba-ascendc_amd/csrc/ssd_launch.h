@@ -16,6 +16,10 @@ struct SegParams;
 void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
                     const FwdParams &kp, const SegParams &sp);
 
+// k_fwd_state_group<4>: the chunk-start states of one segment per stream,
+// one workgroup per (b, g), four heads per group, no sequence ids; grid B G
+void launch_fwd_state_group(dim3 grid, hipStream_t st, const FwdParams &kp);
+
 // k_fwd_wide<save, gate, seq, kp.cb != NULL> (dstate 128)
 void launch_fwd_wide(bool save, bool gate, bool seq, dim3 grid, hipStream_t st, const FwdParams &kp,
                      const SegParams &sp);

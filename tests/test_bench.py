@@ -63,6 +63,9 @@ def test_recompute_pass_model_counts_the_state_writes():
     sv = bench.fwd_kernel_model("k_fwd_seg_state_save", shape)
     assert sv["bytes"] - st["bytes"] == 4 * 64 * 64 * sv["units"]
     assert math.isclose(sv["bytes"] / 1e9, 4.865, rel_tol=1e-3)
+    # the group-major form of the same pass moves the same algorithmic bytes
+    assert bench.fwd_kernel_model("k_fwd_state_group", shape) == sv
+    assert bench.model_key(bench._short("void ssd::k_fwd_state_group<4>(ssd::FwdParams)")) == "k_fwd_state_group"
 
 
 def test_summary_statistics():
