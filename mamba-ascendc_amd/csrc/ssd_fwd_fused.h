@@ -84,11 +84,12 @@ struct SegParams {
 
 constexpr int kXcds = 8; // MI355X: workgroups go round-robin over 8 XCDs
 
-// Workgroup id -> work unit, keeping the R heads of one group on one XCD
-// (consecutive workgroups of an XCD walk the heads of one group, so B and C
-// of a chunk are read from HBM once into that XCD's L2).  Ids past the last
-// full block of kXcds * R map to themselves.  With fewer units than one such
-// block (many heads per group, one round), each XCD takes a contiguous run of
+// Workgroup id -> work unit, in blocks of R consecutive units per XCD: with
+// R the units of one group, the heads of a group share an XCD (consecutive
+// workgroups of an XCD walk the heads of one group, so B and C of a chunk are
+// read from HBM once into that XCD's L2).  Ids past the last full block of
+// kXcds * R map to themselves.  With fewer units than one such block (many
+// heads per group, one round), each XCD takes a contiguous run of
 // total / kXcds units instead (the heads of one segment of a group, so B and
 // C of a chunk reach a few XCDs' L2 rather than all eight).
 __device__ __forceinline__ int xcd_unit(int id, int total, int R) {
