@@ -113,12 +113,14 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int r16 = lane & 15, kq = lane >> 4;
-    // unit = (b * G + g) * nseg + sg.  Each XCD takes blocks of eight
-    // consecutive groups (xcd_unit), so the ddt and dt rows the 32 heads of
-    // a token share (one 128-byte line) pass through one L2: C3 backward 0.4 %
-    // faster than with the groups of a line on eight XCDs.  (The same blocks
-    // ran the forward 4 % slower, which keeps one group per block.)
-    const int ub = xcd_unit(blockIdx.x, (int)gridDim.x, nseg * (prm.R < 32 ? 32 / prm.R : 1));
+    // unit = (b * G + g) * nseg + sg.  With one run per stream each XCD takes
+    // blocks of eight consecutive groups (xcd_unit), so the ddt and dt rows
+    // the 32 heads of a token share (one 128-byte line) pass through one L2:
+    // C3 backward 0.4 % faster than with the groups of a line on eight XCDs.
+    // With several runs per stream (C4) the same blocks ran 1.5-2 % slower
+    // than consecutive workgroups on consecutive units, and the forward 4 %
+    // slower, which keeps one group per block.
+    const int ub = nseg == 1 ? xcd_unit(blockIdx.x, (int)gridDim.x, prm.R < 32 ? 32 / prm.R : 1) : (int)blockIdx.x;
     const int sg = ub % nseg, bg = ub / nseg;
     const int g = bg % prm.G, b = bg / prm.G;
     const int R = kRev ? kRevR : prm.R, H = prm.H, G = prm.G, K = prm.K;
