@@ -1,4 +1,4 @@
-"""The forward under HIP graph capture, and its empty-sequence path.
+"""The forward and the M1 backward under HIP graph capture, and the forward's empty-sequence path.
 
 The forward enqueues kernels only (no memset or memcpy nodes, no allocation):
 the empty sequence (seqlen 0, allowed by the C ABI) writes its final state
@@ -153,5 +153,82 @@ def test_captured_forward_replays_match_eager(shape, feats, noalloc):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want_out) and torch.equal(fin, want_fin), rep
+        assert bool(torch.isfinite(y).all())
+    _say("  3 replays identical to the eager call")
+
+
+CAPTURED_BWD = [
+    # [B, L, H, P, N, chunk, G], features, keep the forward's chunk states
+    ([2, 200, 128, 64, 64, 64, 32], ("D", "bias", "init"), False),  # group-major state recompute
+    ([2, 200, 128, 64, 64, 64, 32], ("D", "bias", "init"), True),   # saved chunk states
+    ([2, 700, 8, 64, 64, 64, 2], ("z", "init"), False),             # runs: pre-pass + recurrence over runs
+]
+
+
+@pytest.mark.parametrize("shape,feats,saved", CAPTURED_BWD,
+                         ids=[f"{c[0]}-{'saved' if c[2] else 'recompute'}" for c in CAPTURED_BWD])
+def test_captured_backward_replays_match_eager(shape, feats, saved):
+    """The M1 backward enqueues kernels only as well (state recompute, run
+    pre-pass, recurrence over runs, the fused chunk kernel, the fixed-order
+    finalize), so a captured call replays bit for bit."""
+    _need_gpu()
+    from ascend_kernel import _runtime as rt
+    from ascend_kernel import mamba2 as m
+
+    lib = rt.load_library()
+    b, l, h, p, n, chunk, g = shape
+    _say(f"capture bwd {shape} {feats} saved {saved}")
+    dev = {k: v.cuda() for k, v in make_inputs(shape, seed=43, features=feats).items()}
+    gen = torch.Generator().manual_seed(9)
+    dout = torch.randn(b, l, h, p, generator=gen).cuda()
+    dfin = torch.randn(b, h, p, n, generator=gen).cuda()
+    D, z, bias, init = dev.get("D"), dev.get("z"), dev.get("dt_bias"), dev.get("initial_states")
+    _, _, pre_gate, states, _ = m._fwd_raw(dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"], D, z, bias, init,
+                                           chunk, True, 0.0, math.inf, want_pre_gate=z is not None,
+                                           want_states=saved)
+    flags = m._flags(D, z, bias, init, True) | (rt.SAVED_STATES if saved else 0)
+    shp = m._shape(dev["x"], dev["B"], chunk)
+    nb = ctypes.c_size_t(0)
+    rt.check(lib.mamba2_ssd_bwd_m1_workspace_size(ctypes.byref(shp), flags, ctypes.byref(nb)), "ws", lib)
+    ws = torch.empty(max(1, nb.value), dtype=torch.uint8, device="cuda")
+    grads = {"dx": torch.empty_like(dev["x"]), "ddt": torch.empty_like(dev["dt"]),
+             "dA": torch.empty_like(dev["A"]), "dB": torch.empty_like(dev["B"]), "dC": torch.empty_like(dev["C"]),
+             "dD": torch.empty_like(D) if D is not None else None,
+             "dz": torch.empty_like(z) if z is not None else None,
+             "ddt_bias": torch.empty_like(bias) if bias is not None else None,
+             "dinit": torch.empty_like(init) if init is not None else None}
+    P = m._ptr
+    args = rt.Mamba2SsdBwdArgs(
+        shp, flags, 0.0, m._limit(math.inf),
+        P(dev["x"]), P(dev["dt"]), P(dev["A"]), P(dev["B"]), P(dev["C"]), P(D), P(z), P(bias), P(init),
+        P(dout), P(dfin), P(pre_gate), P(states),
+        P(grads["dx"]), P(grads["ddt"]), P(grads["dA"]), P(grads["dB"]), P(grads["dC"]),
+        P(grads["dD"]), P(grads["dz"]), P(grads["ddt_bias"]), P(grads["dinit"]), None)
+
+    def call(stream):
+        return lib.mamba2_ssd_bwd_m1(ctypes.byref(args), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                     ctypes.c_void_p(stream.cuda_stream))
+
+    rt.check(call(torch.cuda.current_stream()), "eager", lib)
+    torch.cuda.synchronize()
+    want = {k: v.clone() for k, v in grads.items() if v is not None}
+    assert all(bool(torch.isfinite(v).all()) for v in want.values())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = call(torch.cuda.current_stream())
+    rt.check(rc, "captured", lib)
+    import ascend_kernel
+    other = {k: v.cuda() for k, v in make_inputs([1, 256, 2, 64, 64, 64, 1], seed=44).items()}
+    for rep in range(3):
+        for v in grads.values():
+            if v is not None:
+                v.fill_(math.nan)
+        y, _ = ascend_kernel.mamba2_ssd_fwd(other["x"], other["dt"], other["A"], other["B"], other["C"], 64,
+                                            dt_softplus=True, return_final_state=True)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for k, v in want.items():
+            assert torch.equal(grads[k], v), (rep, k)
         assert bool(torch.isfinite(y).all())
     _say("  3 replays identical to the eager call")
