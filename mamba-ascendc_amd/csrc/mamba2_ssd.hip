@@ -817,8 +817,10 @@ int bwd_impl(const Mamba2SsdBwdArgs *a, void *workspace, size_t workspace_bytes,
             sp.seg_in_n = pre.nseg;
             sp.in_mult = lay.recompute.mult;
         }
-        if (sp.nseg == 1 && !seq && sp_prm.R == 4) {
-            // one workgroup per (b, g) walking its four heads per chunk: B read once
+        if (sp.nseg == 1 && !seq && sp_prm.R == 4 && B * s->ngroups >= kMinStreams) {
+            // one workgroup per (b, g) walking its four heads per chunk: B read
+            // once; with fewer (b, g) streams than CUs the per-head pass keeps
+            // more of the GPU busy
             ssd::launch_fwd_state_group(dim3((unsigned)(B * s->ngroups)), st, sp_prm);
             if (int rc = launch_status("k_fwd_state_group", tr, st)) return rc;
         } else {

@@ -16,7 +16,7 @@
 // flight instead (a ring of four head steps).  C3: 1.003 ms and 5.11 GB
 // (1.05x the algorithmic bytes) against 1.075 ms and 5.85 GB for the
 // per-head pass.  Used for one segment per stream without sequence ids,
-// R = 4.
+// R = 4, and at least as many (b, g) streams as CUs.
 //
 // The math is that of mamba_torch/ssd_reference.py:113-189 (chunk states and
 // the inter-chunk recurrence).

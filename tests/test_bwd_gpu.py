@@ -390,7 +390,7 @@ def test_ssdcore_module_trains():
     ([4, 330, 256, 64, 64, 64, 64], ("D2", "bias"), False),            # fused reverse, one run per stream
     ([2, 400, 16, 64, 64, 128, 4], ("z", "init"), True),               # packed sequences
     ([1, 700, 16, 64, 64, 64, 2], ("D", "init"), False),               # split path (8 heads per group)
-    ([2, 200, 128, 64, 64, 64, 32], ("D", "bias", "init"), False),     # group-major recompute with initial states
+    ([4, 130, 256, 64, 64, 64, 64], ("D", "bias", "init"), False),     # group-major recompute with initial states
 ], ids=["reverse-runs", "fused-reverse", "packed", "split", "group-recompute-init"])
 def test_training_policy_recompute_matches_saved(shape, features, packed):
     """The save-vs-recompute policy (TrainingPolicy.save_chunk_states) changes

@@ -159,8 +159,8 @@ def test_captured_forward_replays_match_eager(shape, feats, noalloc):
 
 CAPTURED_BWD = [
     # [B, L, H, P, N, chunk, G], features, keep the forward's chunk states
-    ([2, 200, 128, 64, 64, 64, 32], ("D", "bias", "init"), False),  # group-major state recompute
-    ([2, 200, 128, 64, 64, 64, 32], ("D", "bias", "init"), True),   # saved chunk states
+    ([4, 130, 256, 64, 64, 64, 64], ("D", "bias", "init"), False),  # group-major state recompute
+    ([4, 130, 256, 64, 64, 64, 64], ("D", "bias", "init"), True),   # saved chunk states
     ([2, 700, 8, 64, 64, 64, 2], ("z", "init"), False),             # runs: pre-pass + recurrence over runs
 ]
 
