@@ -115,6 +115,13 @@ def bwd_runs(shape):
     return math.ceil(k / m)
 
 
+def fwd_folds(shape):
+    """True when the fused forward of this shape launches no segment
+    recurrence (one segment, or full segments that fold the pre-segments
+    into their entering states)."""
+    return _fwd_plan(shape)[3]
+
+
 def fwd_segments(shape):
     """(nseg, nseg_pre, nsplit) of the fused forward's plan (mamba2_ssd.hip
     fwd_plan): dstate 128 runs two workgroups per head; with fewer than 256
@@ -122,6 +129,10 @@ def fwd_segments(shape):
     least 6 chunk steps), and the state-only pass runs on segments twice as
     fine (only those before the last full segment when the full segments
     fold them into their entering states themselves)."""
+    return _fwd_plan(shape)[:3]
+
+
+def _fwd_plan(shape):
     b, l, h, p, n, _chunk, g = shape
     k = math.ceil(l / EXEC_CHUNK)
     nsplit = n // 64
@@ -131,7 +142,7 @@ def fwd_segments(shape):
     if k - math.ceil(k / nseg) < 6:
         nseg = 1
     if nseg == 1:
-        return 1, 1, nsplit
+        return 1, 1, nsplit, True
     mt = math.ceil(k / nseg)
     mult = min(2, mt)
     mp = math.ceil(mt / mult)
@@ -139,8 +150,8 @@ def fwd_segments(shape):
     if (nseg - 1) * mult <= 12:
         # each full segment folds the pre-segments before it: the last full
         # segment's own pre-segments are not computed
-        return nseg, (nseg - 1) * mult, nsplit
-    return nseg, math.ceil(k / mp), nsplit
+        return nseg, (nseg - 1) * mult, nsplit, True
+    return nseg, math.ceil(k / mp), nsplit, False
 
 
 def fwd_kernel_model(name: str, shape) -> dict:
@@ -164,6 +175,14 @@ def fwd_kernel_model(name: str, shape) -> dict:
     if name == "k_chunk_state":
         per = f4 * (T * p + T + T * n / r + p * n + 1)
         fl = 2 * T * p * n
+    elif name == "k_state_pass_op":
+        # the standalone state-passing op over every chunk state: chunk
+        # states in, states entering the chunks out, the log decays and the
+        # final state
+        su = b * h * k
+        per = f4 * (2 * p * n + 1)
+        return {"bytes": su * per + b * h * p * n * f4, "flops": su * 2 * p * n, "units": su,
+                "bytes_per_unit": per}
     elif name == "k_state_pass":
         # between the fused forward's segments: segment states in and out
         _, nseg_pre, _ = fwd_segments(shape)
@@ -1037,10 +1056,16 @@ def summarize_profiles(trace_dir, fetch_dir, write_dir, shape, copy_bytes=1 << 3
            f"{fscale:.3f} (fetch) and {wscale:.3f} (write).", "",
            "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled traffic GB | algorithmic GB (kernel model) |",
            "|---|---:|---:|---:|---:|"]
+    folds = fwd_folds(shape)
     for k in fetch:
         t = (fetch[k] * fscale + write.get(k, 0.0) * wscale) * 1024
-        traffic[model_key(k)] = t
-        alg = fwd_kernel_model(model_key(k), shape)["bytes"]
+        key = model_key(k)
+        if key == "k_state_pass" and folds:
+            # the forward folds its segments itself, so every k_state_pass
+            # launch of the run is the standalone op
+            key = "k_state_pass_op"
+        traffic[key] = t
+        alg = fwd_kernel_model(key, shape)["bytes"]
         alg_s = "" if alg != alg else f"{alg / 1e9:.3f}"
         md.append(f"| `{k}` | {fetch[k]:.0f} | {write.get(k, 0.0):.0f} | {t / 1e9:.3f} | {alg_s} |")
     md.append("")

@@ -72,3 +72,20 @@ def test_summary_statistics():
     s = bench.summarize([5.0, 1.0, 3.0, 2.0, 4.0, 6.0, 7.0, 8.0, 9.0, 10.0])
     assert s["median_ms"] == 5.5 and s["min_ms"] == 1.0 and s["max_ms"] == 10.0
     assert s["p90_ms"] == 9.0 and s["n"] == 10 and s["mean_ms"] == 5.5
+
+
+def test_standalone_state_pass_model_matches_the_op_timing():
+    """Profiles attribute the k_state_pass launches of a config run to the
+    standalone state-passing op whenever the forward folds its segments (all
+    five configs); that model is the op's own byte count, the one
+    bench_state_passing divides by (chunk states in, states entering the
+    chunks out, log decays, final state)."""
+    for cfg in sorted(bench.CONFIGS):
+        shape = bench.CONFIGS[cfg]
+        assert bench.fwd_folds(shape), cfg
+        b, l, h, p, n, _chunk, _g = shape
+        k = math.ceil(l / bench.EXEC_CHUNK)
+        want = 4 * (2 * b * h * k * p * n + b * h * k + b * h * p * n)
+        assert bench.fwd_kernel_model("k_state_pass_op", shape)["bytes"] == want
+    # many pre-segments: the forward runs the segment recurrence itself
+    assert not bench.fwd_folds([1, 65536, 8, 64, 64, 64, 1])
