@@ -548,7 +548,9 @@ int fwd_impl(const Mamba2SsdFwdArgs *a, void *workspace, size_t workspace_bytes,
             ssd::launch_fwd_wide(kp.chunk_states != nullptr, kp.has_z != 0, seq, dim3(units), st, kp, sp);
             if (int rc = launch_status(kp.chunk_states ? "k_fwd_wide_save" : "k_fwd_wide", tr, st)) return rc;
         } else {
-            ssd::launch_fwd_seg(false, kp.chunk_states != nullptr, kp.has_z != 0, seq, dim3(units), st, kp, sp);
+            // one round of workgroups (at most one per CU): the latency form
+            ssd::launch_fwd_seg(false, kp.chunk_states != nullptr, kp.has_z != 0, seq, dim3(units), st, kp, sp,
+                                (int64_t)units <= kMinStreams);
             if (int rc = launch_status(kp.chunk_states ? "k_fwd_seg_save" : "k_fwd_seg", tr, st)) return rc;
         }
         if (varlen) {

@@ -195,7 +195,9 @@ __device__ __forceinline__ void fold_entry(f32x4 (&acc)[kN], const float *U, con
 // backward's recompute of the states it was not given).
 // kGate: the z gate (prm.has_z), whose z rows the consumers prefetch a chunk ahead.
 // kSeq: packed sequences (prm.seq_idx).
-template <bool kStateOnly, bool kSave = false, bool kGate = false, bool kSeq = false>
+// kLat: the latency form of the C.S products, for grids of at most one
+// workgroup per CU (each workgroup's step latency is then the kernel time).
+template <bool kStateOnly, bool kSave = false, bool kGate = false, bool kSeq = false, bool kLat = false>
 __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams sp) {
     constexpr int T = 64, P = 64, N = 64;
     constexpr int TS = kSeq ? T : 1; // per-token sequence arrays (kSeq only)
@@ -631,12 +633,41 @@ __global__ __launch_bounds__(kWsThreads) void k_fwd_seg(FwdParams prm, SegParams
                     // faster; without this fence the scheduler interleaves
                     // them with the mask, C3 3.5 % slower)
                     __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (kLat) {
+                        // latency form: the T4 fragments of p-block pb + 1 read
+                        // while pb's products run, the order pinned by the
+                        // groups below (left alone, the scheduler issues each
+                        // read just before its product and waits for it).  C4
+                        // (one round of 256 workgroups) 0.0327 -> 0.0312 ms; at
+                        // C3 (8 rounds per CU, the CU's LDS and issue shared by
+                        // the waves) 1.344 -> 1.358 ms, so many-round grids keep
+                        // the serial form.  Same products in the same order.
+                        Frag f4[2][2];
+                        f4[0][0] = frag(t4, r16, 0);
+                        f4[0][1] = frag(t4, r16, 1);
     #pragma unroll
-                    for (int pb = 0; pb < 4; ++pb) {
-                        acc[pb] = zero4();
+                        for (int pb = 0; pb < 4; ++pb) {
+                            if (pb < 3) {
+                                f4[(pb + 1) & 1][0] = frag(t4, 16 * (pb + 1) + r16, 0);
+                                f4[(pb + 1) & 1][1] = frag(t4, 16 * (pb + 1) + r16, 1);
+                            }
+                            acc[pb] = mma3f(f4[pb & 1][0], Cown[0], zero4());
+                            acc[pb] = mma3f(f4[pb & 1][1], Cown[1], acc[pb]);
+                        }
+                        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // reads of p-blocks 0, 1
+                        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);  // products of p-block 0
+                        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // reads of p-block 2
+                        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);  // p-block 1
+                        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // reads of p-block 3
+                        __builtin_amdgcn_sched_group_barrier(0x008, 12, 0); // p-blocks 2, 3
+                    } else {
     #pragma unroll
-                        for (int ks = 0; ks < 2; ++ks)
-                            acc[pb] = mma3f(frag(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
+                        for (int pb = 0; pb < 4; ++pb) {
+                            acc[pb] = zero4();
+    #pragma unroll
+                            for (int ks = 0; ks < 2; ++ks)
+                                acc[pb] = mma3f(frag(t4, 16 * pb + r16, ks), Cown[ks], acc[pb]);
+                        }
                     }
     #pragma unroll
                     for (int j = 0; j < 4; ++j) {

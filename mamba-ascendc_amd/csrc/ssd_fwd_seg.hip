@@ -9,9 +9,9 @@
 namespace ssd {
 namespace {
 
-template <bool kStateOnly, bool kSave, bool kGate, bool kSeq>
+template <bool kStateOnly, bool kSave, bool kGate, bool kSeq, bool kLat = false>
 void run(dim3 grid, hipStream_t st, const FwdParams &kp, const SegParams &sp) {
-    hipLaunchKernelGGL((k_fwd_seg<kStateOnly, kSave, kGate, kSeq>), grid, dim3(kWsThreads), 0, st,
+    hipLaunchKernelGGL((k_fwd_seg<kStateOnly, kSave, kGate, kSeq, kLat>), grid, dim3(kWsThreads), 0, st,
                        kp, sp);
 }
 
@@ -20,12 +20,18 @@ using Run = void (*)(dim3, hipStream_t, const FwdParams &, const SegParams &);
 }  // namespace
 
 void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
-                    const FwdParams &kp, const SegParams &sp) {
+                    const FwdParams &kp, const SegParams &sp, bool latency) {
     if (state_only) {
         if (save)
             (seq ? run<true, true, false, true> : run<true, true, false, false>)(grid, st, kp, sp);
         else
             (seq ? run<true, false, false, true> : run<true, false, false, false>)(grid, st, kp, sp);
+        return;
+    }
+    if (latency && !gate && !seq) {
+        // the plain and saving passes (the z-gated and packed forms, whose
+        // registers are fuller, keep the one form)
+        (save ? run<false, true, false, false, true> : run<false, false, false, false, true>)(grid, st, kp, sp);
         return;
     }
     static const Run full[8] = {

@@ -12,9 +12,11 @@ namespace ssd {
 
 struct SegParams;
 
-// k_fwd_seg<state_only, save, gate, seq> (state_only excludes gate)
+// k_fwd_seg<state_only, save, gate, seq> (state_only excludes gate); latency:
+// the full pass's form for grids of at most one workgroup per CU (plain and
+// saving passes; ignored for the others)
 void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
-                    const FwdParams &kp, const SegParams &sp);
+                    const FwdParams &kp, const SegParams &sp, bool latency = false);
 
 // k_fwd_state_group<4>: the chunk-start states of one segment per stream,
 // one workgroup per (b, g), four heads per group, no sequence ids; grid B G
