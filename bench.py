@@ -943,7 +943,8 @@ def _short(name: str) -> str:
 def model_key(short: str) -> str:
     """Kernel-model / trace name of a (templated) kernel.
 
-    k_fwd_seg<state only, save states, z gate, packed sequences>: <true, false,
+    k_fwd_seg<state only, save states, z gate, packed sequences, latency form
+    (one-round grids; the same pass)>: <true, false,
     ...> is k_fwd_seg_state, <true, true, ...> k_fwd_seg_state_save (the
     backward's recompute of the chunk states), <false, true, ...> k_fwd_seg_save, <false, false, ...>
     k_fwd_seg, with a "_gate" suffix for the z-gated form and "_seq" for

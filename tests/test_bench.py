@@ -48,6 +48,9 @@ def test_traced_names_map_to_distinct_models():
     assert bench._short("void ssd::bwd::k_bwd_ws<false, 4, false>(ssd::BwdParams, int, int)") == \
         "k_bwd_ws<false, 4, false>"
     assert key("k_state_pass") == "k_state_pass"
+    # the latency form of one-round grids is the same pass
+    assert key("k_fwd_seg<false, false, false, false, true>") == "k_fwd_seg"
+    assert key("k_fwd_seg<false, true, false, false, true>") == "k_fwd_seg_save"
     shape = bench.CONFIGS[3]
     for name in ("k_fwd_seg_gate", "k_fwd_seg_save_gate", "k_bwd_ws_rev", "k_bwd_ws_rev_z", "k_fwd_wide",
                  "k_fwd_wide_gate"):
