@@ -890,7 +890,7 @@ def cpu_oracle_baseline(torch, cpu_inp, shape, seed, with_bwd=False, warmup=None
     """The fp32 CPU oracle on the whole configuration, on the same CPU tensors
     the GPU copies came from: the forward (dt_softplus, final state), or with
     `with_bwd` the forward plus the autograd backward of mean(y^2) +
-    mean(final^2) (BASELINE.md's plan; C4).  time.perf_counter_ns around each
+    mean(final^2) (the loss of the reference's backward benchmark; C4).  time.perf_counter_ns around each
     call (benchmarks/mamba2_backward_bench.py:373-376), median; warmup 1 /
     repeat 3 for the 8.6 GB config 3, warmup 3 / repeat 10 otherwise."""
     from oracle.ssd_reference import ssd_chunk_scan_ref
