@@ -228,6 +228,14 @@ def fwd_kernel_model(name: str, shape) -> dict:
         per = f4 * (T * p + T + T * n / r)
         return {"bytes": units * per + runs * f4 * (p * n + 1), "flops": units * 2 * T * p * n,
                 "units": units, "bytes_per_unit": per}
+    elif name == "k_state_pass_bwd":
+        # the backward's recurrence over runs, in place: each run's
+        # contribution and log decay in, the gradient entering it out, plus
+        # the final-state gradient
+        su = b * h * bwd_runs(shape)
+        per = f4 * (2 * p * n + 1)
+        return {"bytes": su * per + b * h * p * n * f4, "flops": su * 2 * p * n, "units": su,
+                "bytes_per_unit": per}
     elif name == "k_bwd_dstate_rev":
         # dout, dt, C in; dU (state gradient leaving each chunk) out
         per = f4 * (T * p + T + T * n / r + p * n)
@@ -971,7 +979,8 @@ def model_key(short: str) -> str:
         if len(args) > 1 and args[1] != "0":
             return ("k_bwd_ws_rev_z" if args[0] == "true" else "k_bwd_ws_rev") + seq
         return "k_bwd_ws" + seq
-    return base if base in ("k_bwd_dstate_rev", "k_bwd_run_grad", "k_chunk_cb", "k_fwd_state_group") else short
+    return base if base in ("k_bwd_dstate_rev", "k_bwd_run_grad", "k_chunk_cb", "k_fwd_state_group",
+                            "k_state_pass_bwd") else short
 
 
 SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs
