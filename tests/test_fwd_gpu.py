@@ -102,6 +102,34 @@ def test_forward_deterministic():
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
+def test_latency_form_matches_serial_form_bitwise():
+    """A grid of at most one workgroup per CU runs the latency form of the
+    C.S products (fragments double-buffered), a larger grid the serial form;
+    both issue the same products in the same order.  The same (b, h) streams
+    in a 256-workgroup grid (B = 2) and a 512-workgroup grid (B = 4, its first
+    two batches identical) give bitwise-equal outputs and final states, in the
+    inference forward and in the training forward that saves the chunk
+    states."""
+    _need_gpu()
+    import ascend_kernel
+
+    big = make_inputs([4, 256, 128, 64, 64, 64, 32], seed=12)
+    small = {k: (v if k == "A" else v[:2].contiguous()) for k, v in big.items()}
+    _say("latency vs serial form: [2|4, 256, 128, 64, 64, 64, 32]")
+    for train in (False, True):
+        res = []
+        for inp in (small, big):
+            dev = {k: v.cuda().requires_grad_(train) for k, v in inp.items()}
+            out, fin = ascend_kernel.mamba2_ssd_fwd(dev["x"], dev["dt"], dev["A"], dev["B"], dev["C"], 64,
+                                                    dt_softplus=True, return_final_state=True)
+            torch.cuda.synchronize()
+            res.append((out.detach().cpu(), fin.detach().cpu()))
+        (y_s, f_s), (y_b, f_b) = res
+        assert torch.isfinite(y_s).all()
+        assert torch.equal(y_s, y_b[:2]), f"train={train}"
+        assert torch.equal(f_s, f_b[:2]), f"train={train}"
+
+
 def test_chunk_size_invariance():
     """The logical chunk size does not change the result (partition invariance)."""
     _need_gpu()
