@@ -172,10 +172,7 @@ constexpr WideTileMap make_wide_tiles(int c0, int c1, int c2, int c3) {
         }
     return m;
 }
-#ifndef SSD_WIDE_TILES
-#define SSD_WIDE_TILES 6, 5, 3, 2
-#endif
-constexpr WideTileMap kWideTiles = make_wide_tiles(SSD_WIDE_TILES);
+constexpr WideTileMap kWideTiles = make_wide_tiles(6, 5, 3, 2);
 
 // kSave: also write the state entering every chunk to prm.chunk_states (the
 // varlen states read them).  kGate: the z gate.  kSeq: packed sequences.
