@@ -28,10 +28,14 @@ void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, 
             (seq ? run<true, false, false, true> : run<true, false, false, false>)(grid, st, kp, sp);
         return;
     }
-    if (latency && !gate && !seq) {
-        // the plain and saving passes (the z-gated and packed forms, whose
+    if (latency && !seq) {
+        // the plain, saving and z-gated passes (the packed forms, whose
         // registers are fuller, keep the one form)
-        (save ? run<false, true, false, false, true> : run<false, false, false, false, true>)(grid, st, kp, sp);
+        static const Run lat[4] = {
+            run<false, false, false, false, true>, run<false, false, true, false, true>,
+            run<false, true, false, false, true>, run<false, true, true, false, true>,
+        };
+        lat[(save ? 2 : 0) + (gate ? 1 : 0)](grid, st, kp, sp);
         return;
     }
     static const Run full[8] = {

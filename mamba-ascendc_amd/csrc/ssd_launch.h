@@ -13,8 +13,8 @@ namespace ssd {
 struct SegParams;
 
 // k_fwd_seg<state_only, save, gate, seq> (state_only excludes gate); latency:
-// the full pass's form for grids of at most one workgroup per CU (plain and
-// saving passes; ignored for the others)
+// the full pass's form for grids of at most one workgroup per CU (plain,
+// saving and z-gated passes; ignored for the packed ones)
 void launch_fwd_seg(bool state_only, bool save, bool gate, bool seq, dim3 grid, hipStream_t st,
                     const FwdParams &kp, const SegParams &sp, bool latency = false);
 
