@@ -61,9 +61,14 @@ __device__ __forceinline__ void split4(float4 v, bf16x4 &hi, bf16x4 &lo) {
     lo = bf16x4{l0[0], l0[1], l1[0], l1[1]};
 }
 
-struct SplitTile {
+// A split tile whose rows are stored interleaved (kIl, see trow) or in order;
+// every accessor below takes the row order from the tile's type, so the
+// writers and readers of one kernel agree by construction.
+template <bool kIl>
+struct SplitTileT {
     __bf16 *hi, *lo;
 };
+using SplitTile = SplitTileT<true>;
 
 // Slot of tile row r: inside each 16-row block the rows are interleaved,
 // row r at slot 2 (r % 8) + (r / 8) % 2.  At the kTS-element (144-byte) row
@@ -72,18 +77,27 @@ struct SplitTile {
 // bank-conflict cycles per instruction, 2 with rows in order); the 16-byte
 // operand reads, the natural-order transposing reads and the row writes keep
 // their conflict counts, since each touches a whole 16-row block or a single
-// row.  Every tile access of the backward goes through this mapping.
-__device__ __forceinline__ int trow(int r) { return (r & ~15) | ((r & 7) << 1) | ((r >> 3) & 1); }
+// row.  The per-lane slot arithmetic costs registers: the z-gated reverse
+// backward at four heads per group, already at 256 VGPRs, spills 4 of them
+// with it (C3 full-feature backward 4.33-4.43 ms against 4.24-4.25 ms with
+// rows in order, while the plain and packed ones gain 1 % and 3 %), so that
+// kernel keeps its rows in order (kIl = false).
+template <bool kIl>
+__device__ __forceinline__ int trow(int r) {
+    return kIl ? ((r & ~15) | ((r & 7) << 1) | ((r >> 3) & 1)) : r;
+}
 
-__device__ __forceinline__ SplitTile tile_at(__bf16 *base, int i) {
-    return SplitTile{base + (2 * i) * kTile, base + (2 * i + 1) * kTile};
+template <bool kIl = true>
+__device__ __forceinline__ SplitTileT<kIl> tile_at(__bf16 *base, int i) {
+    return SplitTileT<kIl>{base + (2 * i) * kTile, base + (2 * i + 1) * kTile};
 }
 
 // tile[row][c0 .. c0 + 3] = v (both halves)
-__device__ __forceinline__ void store_split4(SplitTile d, int row, int c0, float4 v) {
+template <bool kIl>
+__device__ __forceinline__ void store_split4(SplitTileT<kIl> d, int row, int c0, float4 v) {
     bf16x4 vh, vl;
     split4(v, vh, vl);
-    const int idx = trow(row) * kTS + c0;
+    const int idx = trow<kIl>(row) * kTS + c0;
     *(bf16x4 *)&d.hi[idx] = vh;
     *(bf16x4 *)&d.lo[idx] = vl;
 }
@@ -92,10 +106,11 @@ struct Frag {
     bf16x8 h, l;
 };
 
-__device__ __forceinline__ Frag frag(SplitTile s, int row, int ks) {
+template <bool kIl>
+__device__ __forceinline__ Frag frag(SplitTileT<kIl> s, int row, int ks) {
     const int kq = (threadIdx.x & 63) >> 4;
     Frag f;
-    const int idx = trow(row) * kTS + ks * 32 + kq * 8;
+    const int idx = trow<kIl>(row) * kTS + ks * 32 + kq * 8;
     f.h = *(const bf16x8 *)&s.hi[idx];
     f.l = *(const bf16x8 *)&s.lo[idx];
     return f;
@@ -118,10 +133,11 @@ __device__ __forceinline__ Frag pack_frag(const float (&v)[8]) {
 }
 
 // ds_read_b64_tr_b16 (the lane mapping of ssd::tr4)
+template <bool kIl>
 __device__ __forceinline__ bf16x4 tr4(const __bf16 *arr, int k0, int c0) {
     const int m = threadIdx.x & 15;
     typedef short v4s __attribute__((ext_vector_type(4)));
-    auto p = (__attribute__((address_space(3))) v4s *)(arr + trow(k0 + (m >> 2)) * kTS + c0 + 4 * (m & 3));
+    auto p = (__attribute__((address_space(3))) v4s *)(arr + trow<kIl>(k0 + (m >> 2)) * kTS + c0 + 4 * (m & 3));
     return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
 }
 
@@ -130,20 +146,22 @@ __device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
 }
 
 // operand of columns c0 .. c0 + 15 contracting over the tile's rows (natural k order)
-__device__ __forceinline__ Frag frag_tn(SplitTile s, int ks, int c0) {
+template <bool kIl>
+__device__ __forceinline__ Frag frag_tn(SplitTileT<kIl> s, int ks, int c0) {
     const int k0 = 32 * ks + 8 * ((threadIdx.x & 63) >> 4);
     Frag f;
-    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 4, c0));
-    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 4, c0));
+    f.h = cat8(tr4<kIl>(s.hi, k0, c0), tr4<kIl>(s.hi, k0 + 4, c0));
+    f.l = cat8(tr4<kIl>(s.lo, k0, c0), tr4<kIl>(s.lo, k0 + 4, c0));
     return f;
 }
 
 // the same in the perm32 k order of operands taken from MFMA outputs
-__device__ __forceinline__ Frag frag_tp(SplitTile s, int m, int c0) {
+template <bool kIl>
+__device__ __forceinline__ Frag frag_tp(SplitTileT<kIl> s, int m, int c0) {
     const int k0 = 32 * m + 4 * ((threadIdx.x & 63) >> 4);
     Frag f;
-    f.h = cat8(tr4(s.hi, k0, c0), tr4(s.hi, k0 + 16, c0));
-    f.l = cat8(tr4(s.lo, k0, c0), tr4(s.lo, k0 + 16, c0));
+    f.h = cat8(tr4<kIl>(s.hi, k0, c0), tr4<kIl>(s.hi, k0 + 16, c0));
+    f.l = cat8(tr4<kIl>(s.lo, k0, c0), tr4<kIl>(s.lo, k0 + 16, c0));
     return f;
 }
 
@@ -156,14 +174,15 @@ __device__ __forceinline__ f32x4 join4(bf16x4 h, bf16x4 l) {
 }
 
 // fp32 values of tile[row][c0 .. c0 + 3]
-__device__ __forceinline__ f32x4 tile_row4(SplitTile s, int row, int c0) {
-    const int idx = trow(row) * kTS + c0;
+template <bool kIl>
+__device__ __forceinline__ f32x4 tile_row4(SplitTileT<kIl> s, int row, int c0) {
+    const int idx = trow<kIl>(row) * kTS + c0;
     return join4(*(const bf16x4 *)&s.hi[idx], *(const bf16x4 *)&s.lo[idx]);
 }
 
 // column-major staging, tile[c][slot] = f(t, c) (ssd::stage_cols for this element type)
-template <bool PERM, class F>
-__device__ __forceinline__ void stage_cols(SplitTile d, F f) {
+template <bool PERM, bool kIl, class F>
+__device__ __forceinline__ void stage_cols(SplitTileT<kIl> d, F f) {
     const int c = threadIdx.x & 63, tb = threadIdx.x >> 6;
 #pragma unroll
     for (int run = tb; run < 8; run += 4) {
@@ -174,8 +193,8 @@ __device__ __forceinline__ void stage_cols(SplitTile d, F f) {
             v[i] = f(PERM ? perm_token(slot) : slot, c);
         }
         const Frag p = pack_frag(v);
-        *(bf16x8 *)&d.hi[trow(c) * kTS + run * 8] = p.h;
-        *(bf16x8 *)&d.lo[trow(c) * kTS + run * 8] = p.l;
+        *(bf16x8 *)&d.hi[trow<kIl>(c) * kTS + run * 8] = p.h;
+        *(bf16x8 *)&d.lo[trow<kIl>(c) * kTS + run * 8] = p.l;
     }
 }
 

@@ -74,6 +74,10 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     // reverse pass with the z gate: z and pre_gate are loaded after the first
     // barrier of a step instead of half a step ahead (register pressure)
     constexpr bool kLateZ = kHasZ && kRev;
+    // rows of every tile interleaved (trow), except in the z-gated form,
+    // whose registers the slot arithmetic would spill
+    constexpr bool kIl = !kHasZ;
+    using Tile = SplitTileT<kIl>;
     constexpr int T = 64, P = 64, N = 64;
     constexpr int TS = kSeq ? T : 1;
     // x and gy tiles double buffered by step parity (the epilogue of step n
@@ -109,7 +113,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
     // tiles: x(par) = 0 + par, gy(par) = 2 + par, S 4, dU 5, B 6, C 7 (the
     // roles address them through copies of `lds` the optimizer cannot see
     // through)
-    const SplitTile St = tile_at(lds, 4), Ut = tile_at(lds, 5);
+    const Tile St = tile_at<kIl>(lds, 4), Ut = tile_at<kIl>(lds, 5);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int r16 = lane & 15, kq = lane >> 4;
@@ -244,14 +248,14 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 }
             }
         };
-        auto put = [&](SplitTile d, int row, float4 v) __attribute__((always_inline)) {
+        auto put = [&](Tile d, int row, float4 v) __attribute__((always_inline)) {
             store_split4(d, row, c4, v);
         };
         auto stage_xg = [&](int n) __attribute__((always_inline)) {
             const int par = n & 1, k = chunk_of(n), h = g * R + n % R, tv = tvalid(k);
             const int64_t xo = (((int64_t)b * prm.L + (int64_t)k * T) * H + h) * P;
             __bf16 *lp = opaque_lds_t(lds);
-            const SplitTile xt = tile_at(lp, par), gt = tile_at(lp, 2 + par);
+            const Tile xt = tile_at<kIl>(lp, par), gt = tile_at<kIl>(lp, 2 + par);
             const auto rdz = buf_rsrc(kHasZ ? prm.dz + xo : prm.x + xo);
             float4 dD4 = z4; // sum over this lane's rows of x gy, columns c4 .. c4 + 3
 #pragma unroll
@@ -335,7 +339,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         auto stage_bc = [&](int n) __attribute__((always_inline)) {
             const int tv = tvalid(chunk_of(min(n, NS - 1)));
             __bf16 *lp = opaque_lds_t(lds);
-            const SplitTile bt = tile_at(lp, 6), ct = tile_at(lp, 7);
+            const Tile bt = tile_at<kIl>(lp, 6), ct = tile_at<kIl>(lp, 7);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const bool ok = rt + 16 * j < tv;
@@ -358,14 +362,14 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
         // this chunk into the carry, g <- dSoff + exp2(cs_last) g, with
         // dSoff^T[n][p] = sum_t (exp2(cs_t) C_t[n]) gy_t[p] from the C and gy
         // tiles the consumers read in the same phase
-        auto put_acc = [&](SplitTile d, int pb, f32x4 v) __attribute__((always_inline)) {
+        auto put_acc = [&](Tile d, int pb, f32x4 v) __attribute__((always_inline)) {
             store_split4(d, 16 * pb + r16, 16 * pw + 4 * kq, make_float4(v[0], v[1], v[2], v[3]));
         };
         auto stage_su_rev = [&](int n, auto slot_c) __attribute__((always_inline)) {
             constexpr int rr = decltype(slot_c)::value;
             const int par = n & 1;
             __bf16 *lp = opaque_lds_t(lds);
-            const SplitTile st_ = tile_at(lp, 4), ut = tile_at(lp, 5), ct = tile_at(lp, 7);
+            const Tile st_ = tile_at<kIl>(lp, 4), ut = tile_at<kIl>(lp, 5), ct = tile_at<kIl>(lp, 7);
             float sdu = 0.f;
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
@@ -391,7 +395,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 for (int j = 0; j < 8; ++j) v[j] = ((float)f.h[j] + (float)f.l[j]) * ev[j];
                 ae[m] = pack_frag(v);
             }
-            const SplitTile gt = tile_at(lp, 2 + par);
+            const Tile gt = tile_at<kIl>(lp, 2 + par);
             const float alpha = kSeq ? exp2_f(s_cs[par][T - 1]) * s_carry[par] : exp2_f(s_cs[par][T - 1]);
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
@@ -545,7 +549,7 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
                 // D gy joins dx (wave-uniform: without D neither is read)
 #pragma unroll
                 for (int pb = 0; pb < 4; ++pb) {
-                    ga[pb] = tile_row4(tile_at(le, 2 + par), own, 16 * pb + cq);
+                    ga[pb] = tile_row4(tile_at<kIl>(le, 2 + par), own, 16 * pb + cq);
                     // s_D holds D per channel (a scalar D repeated)
                     const float4 d4 = *(const float4 *)&s_D[par][16 * pb + cq];
                     Dv[pb] = f32x4{d4.x, d4.y, d4.z, d4.w};
@@ -599,8 +603,8 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
             const bool form_cb = !kRev || r == 0;
             if (n > 0) epilogue(n - 1);
             __bf16 *la = opaque_lds_t(lds);
-            const SplitTile xt = tile_at(la, par), gt = tile_at(la, 2 + par);
-            const SplitTile Bt = tile_at(la, 6), Ct = tile_at(la, 7);
+            const Tile xt = tile_at<kIl>(la, par), gt = tile_at<kIl>(la, 2 + par);
+            const Tile Bt = tile_at<kIl>(la, 6), Ct = tile_at<kIl>(la, 7);
 
             // ---------------- phase A: x, gy, B, C
             const float *q_ = s_q[par], *cs_ = s_cs[par], *bT_ = s_bT[par], *bS_ = s_bS[par];
@@ -740,8 +744,8 @@ __global__ __launch_bounds__(kBwsThreads) void k_bwd_ws(BwdParams prm, int nseg,
 
             // ---------------- phase B: S, dU (x, gy of this step are still in LDS)
             __bf16 *lb = opaque_lds_t(lds);
-            const SplitTile xb = tile_at(lb, par), gb = tile_at(lb, 2 + par);
-            const SplitTile St = tile_at(lb, 4), Ut = tile_at(lb, 5);
+            const Tile xb = tile_at<kIl>(lb, par), gb = tile_at<kIl>(lb, 2 + par);
+            const Tile St = tile_at<kIl>(lb, 4), Ut = tile_at<kIl>(lb, 5);
             const float q_o = s_q[par][own], dte_o = s_dte[par][own], ecs_o = s_ecs[par][own];
             float rpart = 0.f, gpart = 0.f;
             {
