@@ -144,7 +144,7 @@ def _fwd_plan(shape):
     if nseg == 1:
         return 1, 1, nsplit, True
     mt = math.ceil(k / nseg)
-    mult = min(2, mt)
+    mult = 1 if mt <= 8 else min(2, mt)  # segments of at most 8 chunks: pre-segments as long
     mp = math.ceil(mt / mult)
     nseg = math.ceil(k / (mult * mp))
     if (nseg - 1) * mult <= 12:

@@ -101,6 +101,13 @@ int64_t nchunks(const Mamba2SsdShape *s) { return (s->seqlen + ssd::kChunk - 1) 
 #endif
 constexpr int64_t kMinStreams = SSD_MIN_STREAMS;
 constexpr int64_t kPreMult = SSD_PRE_MULT;
+// Full segments of at most this many chunks take pre-segments of the same
+// length (factor 1): the state-only pass over a few chunks costs mostly its
+// pipeline fill, so halving its steps gains less than the full pass loses
+// folding twice the entries.  C4 [4,2048,16,64,64] (segments of 8): forward
+// 0.0492 -> 0.0470 ms; C2 (16) at factor 1 0.0700 -> 0.0770 ms and C5 (64)
+// 0.249 -> 0.257-0.266 ms, so longer segments keep kPreMult.
+constexpr int64_t kShortSegment = 8;
 constexpr int64_t kMinSavedChunks = 6;
 // With at most this many pre-segments before the last full segment, each full
 // segment folds the pre-segment contributions onto the initial states in its
@@ -164,7 +171,7 @@ FwdPlan fwd_plan(const Mamba2SsdShape *s, uint32_t flags, bool allow_cb = true) 
         if (nseg > 1) {
             // full segments of M = mult * M_pre chunks, pre-segments of M_pre
             const int64_t Mt = (K + nseg - 1) / nseg;
-            const int64_t mult = kPreMult < Mt ? kPreMult : Mt;
+            const int64_t mult = Mt <= kShortSegment ? 1 : (kPreMult < Mt ? kPreMult : Mt);
             const int64_t Mp = (Mt + mult - 1) / mult;
             pl.mult = (int)mult;
             pl.M_pre = (int)Mp;

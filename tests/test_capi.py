@@ -100,10 +100,11 @@ def test_workspace_size_formula():
     fwd = lib.mamba2_ssd_fwd_workspace_size
     assert ws(fwd, batch=8, seqlen=4096, nheads=256, ngroups=64) == 0
     # 64 streams, 32 chunks -> 4 segments of 8 chunks, whose entering states
-    # each segment folds from the pre-segments of 4 chunks before it: the 6
-    # before the last segment, [B,H,6,P,N] + [B,H,6]
+    # each segment folds from the state-only contributions of the segments
+    # before it (short segments: pre-segments of the same 8 chunks): the 3
+    # before the last segment, [B,H,3,P,N] + [B,H,3]
     got = ws(fwd, batch=4, seqlen=2048, nheads=16, ngroups=4)
-    assert 4 * 16 * 6 * 64 * 64 * 4 + 4 * 16 * 6 * 4 <= got <= 4 * 16 * 6 * (64 * 64 + 1) * 4 + 2 * 256
+    assert 4 * 16 * 3 * 64 * 64 * 4 + 4 * 16 * 3 * 4 <= got <= 4 * 16 * 3 * (64 * 64 + 1) * 4 + 2 * 256
     # N = 128: 64 (b, h) x 2 workgroups = 128 streams -> 2 segments of 16
     # chunks, 2 pre-segments before the last; nothing else with 4 heads per
     # group (each workgroup writes its channels of out itself)
@@ -157,11 +158,12 @@ def test_workspace_size_formula():
     split = ws(bwd, batch=8, seqlen=4096, nheads=256, ngroups=32)
     assert split >= 2 * state_buf
     # 16 (b, g) streams of 32 chunks -> 16 runs of 2 chunks each: states
-    # [B,H,K,P,N] + the recompute's pre-segment states [B,H,6,P,N] + run
-    # carries [B,H,16,P,N] + partials, no dstates
+    # [B,H,K,P,N] + the recompute's pre-segment states [B,H,3,P,N] (segments
+    # of 8 chunks, pre-segments as long) + run carries [B,H,16,P,N] +
+    # partials, no dstates
     k = 2048 // 64
     states = 4 * 16 * k * 64 * 64 * 4
-    segs = 4 * 16 * 6 * 64 * 64 * 4
+    segs = 4 * 16 * 3 * 64 * 64 * 4
     carries = 4 * 16 * 16 * 64 * 64 * 4
     got = ws(bwd, batch=4, seqlen=2048, nheads=16, ngroups=4)
     assert states + segs + carries <= got < states + segs + carries + states // 8
